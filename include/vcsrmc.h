@@ -1,0 +1,109 @@
+/*
+ * vcsrmc.h -- C ABI of the MI355X (gfx950) VCSR-MC SpMM library, libvcsrmc.so.
+ *
+ * Plain pointers and sizes only.  Device pointers are HIP device memory of the current
+ * device; `stream` is a hipStream_t passed as void* (NULL = the default stream).  Every entry
+ * point returns a status code (VCSRMC_OK = 0); no exception or exit() crosses this boundary.
+ * The C++ drop-in surface of the reference (include/vcsr_formats.hpp) is a thin layer over
+ * these functions.
+ *
+ * Each entry point names the reference interface it replaces (MuuSeoTia/VCSR_MC,
+ * path:line relative to that repository).
+ */
+#ifndef VCSRMC_H
+#define VCSRMC_H
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes. */
+#define VCSRMC_OK 0
+#define VCSRMC_ERR_ARG 1       /* null pointer, negative size, bad dtype/flag            */
+#define VCSRMC_ERR_SEGW 2      /* segw not in {16,32,48,64}      (src/vcsr_mc.cu:26-27)   */
+#define VCSRMC_ERR_TILEK 3     /* tileK not in {16,32,64,128}    (src/vcsr_mc.cu:385-388) */
+#define VCSRMC_ERR_CSR 4       /* row_ptr not monotone / not 0..nnz, column out of range  */
+#define VCSRMC_ERR_UNSORTED 5  /* columns of a row not strictly increasing: unsorted or a
+                                  duplicate coordinate (include/csr.hpp:28-40)           */
+#define VCSRMC_ERR_FORMAT 6    /* uploaded format arrays inconsistent                      */
+#define VCSRMC_ERR_OVERFLOW 7  /* |val| or another size exceeds the int32 of the format   */
+#define VCSRMC_ERR_HIP 8       /* HIP runtime error                                        */
+#define VCSRMC_ERR_STATE 9     /* no format built or uploaded in this handle               */
+
+/* Element type of the dense B operand. */
+#define VCSRMC_B_F32 0
+#define VCSRMC_B_F16 1
+
+typedef struct vcsrmc_format_s *vcsrmc_t;
+
+typedef struct vcsrmc_info {
+    int M, N, segw, bundle, num_segments;
+    int num_groups;        /* G = group_depth.size()                 */
+    long long nval;        /* |lcol| = |val| = group_ptr[G]          */
+    int num_items;         /* item_gbeg.size()                       */
+    float scale;           /* FP16 range scale (1 for FP32 formats)  */
+    int fp32;              /* 1: vcsr_mc_fp32, 0: vcsr_mc            */
+    long long nnz;
+    int num_panels;        /* execution layout: non-empty 16-row panels */
+    int num_chunks;        /* 32-column compacted tiles                 */
+    int num_units;         /* kernel work units                         */
+    int device;            /* HIP device the format lives on            */
+} vcsrmc_info;
+
+/* Handle holding one device-resident format (the reference keeps one format in
+ * namespace-static device pointers, src/vcsr_mc.cu:126-131; a handle removes that limit). */
+int vcsrmc_create(vcsrmc_t *out);
+
+/* Frees the device copies and the handle.  Replaces destroy_vcsr_mc_device
+ * (include/vcsr_formats.hpp:26, src/vcsr_mc.cu:397-404). */
+int vcsrmc_destroy(vcsrmc_t h);
+
+/* FP16 range scale of the values of a device array (src/vcsr_mc.cu:14-22, evaluated as the
+ * reference binary does, see DESIGN).  Replaces half_scale (include/vcsr_formats.hpp:11). */
+int vcsrmc_half_scale(const float *d_val, long long nnz, float *scale, void *stream);
+
+/* Builds the format on the GPU from a device CSR (row_ptr[M+1], col[nnz] strictly increasing
+ * inside each row, val[nnz]).  Replaces csr_to_vcsr_mc followed by upload_vcsr_mc_device
+ * (include/vcsr_formats.hpp:22-23, src/vcsr_mc.cu:25-123, 332-349).  Synchronises `stream`. */
+int vcsrmc_build_csr(vcsrmc_t h, const int *d_row_ptr, const int *d_col, const float *d_val,
+                     int M, int N, int nnz, int fp32, int segw, void *stream);
+
+/* Uploads format arrays held by the caller in host memory (the fields of the reference's
+ * struct VCSRMC, include/vcsr_formats.hpp:14-21), validates them on the device and derives the
+ * execution layout.  Replaces upload_vcsr_mc_device (include/vcsr_formats.hpp:23,
+ * src/vcsr_mc.cu:332-349).  Synchronises `stream`. */
+int vcsrmc_upload(vcsrmc_t h, int M, int N, int segw, int bundle, int num_segments,
+                  int num_groups, long long nval, int num_items, const int *group_ptr,
+                  const int *group_depth, const int *group_seg_base, const int *group_rows,
+                  const int *lcol, const float *val, const int *item_gbeg, const int *item_gend,
+                  float scale, int fp32, void *stream);
+
+/* Sizes and scalar fields of the format in h. */
+int vcsrmc_get_info(vcsrmc_t h, vcsrmc_info *out);
+
+/* Copies the format arrays to caller-provided host buffers sized by vcsrmc_get_info
+ * (group_ptr: G+1, group_depth/group_seg_base: G, group_rows: 16 G, lcol/val: nval,
+ * item_gbeg/item_gend: num_items).  Any pointer may be NULL to skip that array.  This is the
+ * output of csr_to_vcsr_mc (include/vcsr_formats.hpp:22). */
+int vcsrmc_download(vcsrmc_t h, int *group_ptr, int *group_depth, int *group_seg_base,
+                    int *group_rows, int *lcol, float *val, int *item_gbeg, int *item_gend);
+
+/* C += A.B, C (M x O, row-major, ldc = O) and B (N x O, row-major, ldb = O) in device memory.
+ * b_dtype = VCSRMC_B_F32 (the reference's `const float* dB`) or VCSRMC_B_F16 (B already in
+ * binary16, converted once by the caller).  tileK in {16,32,64,128} is the width of the
+ * output-column tile of one work-group, as in the reference.  Rows of C that A does not touch
+ * are left as they are.  If ms is non-NULL the launch is bracketed by two hipEvents on
+ * `stream`, the call waits for it and *ms is the elapsed time (the reference's protocol);
+ * if ms is NULL the launch is asynchronous.  Replaces run_vcsr_mc_spmm_gpu
+ * (include/vcsr_formats.hpp:24-25, src/vcsr_mc.cu:352-394). */
+int vcsrmc_spmm(vcsrmc_t h, const void *dB, int b_dtype, int O, int tileK, float *dC,
+                void *stream, float *ms);
+
+/* Text of a status code, and the detail message of the last failing call on this thread. */
+const char *vcsrmc_status_string(int status);
+const char *vcsrmc_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* VCSRMC_H */

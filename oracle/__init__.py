@@ -1,0 +1,277 @@
+"""ctypes binding of the CPU oracle (test infrastructure only).
+
+Only the test suite, ``__graft_entry__.smoke()`` and the CPU-baseline leg of ``bench.py``
+import this package.  The product library never loads it.  What each function restates
+(file:line of MuuSeoTia/VCSR_MC) and how it is pinned is written in ``vcsrmc_oracle.h``.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libvcsrmc_oracle.so")
+REF_PATH = os.path.join(HERE, "_ref", "libvcsrmc_ref.so")
+REFERENCE_ROOT = "/root/reference"
+
+
+class OrcFormat(C.Structure):
+    _fields_ = [
+        ("M", C.c_int), ("N", C.c_int), ("segw", C.c_int), ("bundle", C.c_int),
+        ("num_segments", C.c_int), ("G", C.c_int), ("nval", C.c_longlong), ("nitems", C.c_int),
+        ("group_ptr", C.POINTER(C.c_int)), ("group_depth", C.POINTER(C.c_int)),
+        ("group_seg_base", C.POINTER(C.c_int)), ("group_rows", C.POINTER(C.c_int)),
+        ("lcol", C.POINTER(C.c_int)), ("val", C.POINTER(C.c_float)),
+        ("item_gbeg", C.POINTER(C.c_int)), ("item_gend", C.POINTER(C.c_int)),
+        ("scale", C.c_float), ("fp32", C.c_int),
+    ]
+
+
+ARRAYS = ("group_ptr", "group_depth", "group_seg_base", "group_rows", "lcol", "val",
+          "item_gbeg", "item_gend")
+
+
+def build(force: bool = False, ref: bool | None = None) -> None:
+    """Compile the oracle (and, where the reference sources exist, oracle/_ref)."""
+    if force or not os.path.exists(LIB_PATH):
+        subprocess.run(["make", "-s", "-C", HERE, "all"], check=True)
+    if ref is None:
+        ref = os.path.isdir(os.path.join(REFERENCE_ROOT, "src"))
+    if ref and (force or not os.path.exists(REF_PATH)):
+        subprocess.run(["make", "-s", "-C", HERE, "ref"], check=True)
+
+
+_lib = None
+_ref = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = C.CDLL(LIB_PATH)
+        i32p, f32p, f64p = C.POINTER(C.c_int), C.POINTER(C.c_float), C.POINTER(C.c_double)
+        L.orc_half_scale.restype = C.c_float
+        L.orc_half_scale.argtypes = [f32p, C.c_longlong]
+        L.orc_f32_to_f16.restype = C.c_uint16
+        L.orc_f32_to_f16.argtypes = [C.c_float]
+        L.orc_f16_to_f32.restype = C.c_float
+        L.orc_f16_to_f32.argtypes = [C.c_uint16]
+        L.orc_f32_to_f16_array.argtypes = [f32p, C.POINTER(C.c_uint16), C.c_longlong]
+        L.orc_round_f16_array.argtypes = [f32p, f32p, C.c_longlong]
+        L.orc_build.restype = C.c_int
+        L.orc_build.argtypes = [i32p, i32p, f32p, C.c_int, C.c_int, C.c_int, C.c_int,
+                                C.POINTER(OrcFormat)]
+        L.orc_free.argtypes = [C.POINTER(OrcFormat)]
+        L.orc_canonicalize.restype = C.c_int
+        L.orc_canonicalize.argtypes = [C.POINTER(OrcFormat)]
+        L.orc_spmm_csr.argtypes = [i32p, i32p, f32p, C.c_int, f32p, C.c_int, C.c_int, C.c_float,
+                                   f64p, f64p]
+        L.orc_spmm_format.argtypes = [C.POINTER(OrcFormat), f32p, C.c_int, f64p]
+        L.orc_cpu_spmm_f64.argtypes = [i32p, i32p, f32p, C.c_int, f32p, C.c_int, f64p]
+        L.orc_cpu_spmm_f64_rows.argtypes = [i32p, i32p, f32p, C.c_int, C.c_int, f32p, C.c_int, f64p]
+        L.orc_cpu_spmm_f64_omp.argtypes = [i32p, i32p, f32p, C.c_int, C.c_int, f32p, C.c_int, f64p,
+                                           C.c_int]
+        _lib = L
+    return _lib
+
+
+def ref_available() -> bool:
+    return os.path.exists(REF_PATH)
+
+
+def ref_lib():
+    global _ref
+    if _ref is None:
+        R = C.CDLL(REF_PATH)
+        R.ref_build.restype = C.c_int
+        R.ref_build.argtypes = [C.POINTER(C.c_int), C.POINTER(C.c_int), C.POINTER(C.c_float),
+                                C.c_int, C.c_int, C.c_int, C.c_int, C.POINTER(OrcFormat),
+                                C.c_char_p, C.c_int]
+        R.ref_half_scale.restype = C.c_float
+        R.ref_half_scale.argtypes = [C.POINTER(C.c_float), C.c_int]
+        _ref = R
+    return _ref
+
+
+def _p(a, ct):
+    return a.ctypes.data_as(C.POINTER(ct))
+
+
+def _i32(a):
+    return np.ascontiguousarray(a, dtype=np.int32)
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+class Format(dict):
+    """A VCSRMC format as a dict of numpy arrays plus scalar fields."""
+
+
+def _take(f: OrcFormat) -> Format:
+    out = Format(M=f.M, N=f.N, segw=f.segw, bundle=f.bundle, num_segments=f.num_segments,
+                 scale=np.float32(f.scale), fp32=bool(f.fp32))
+    sizes = dict(group_ptr=f.G + 1, group_depth=f.G, group_seg_base=f.G, group_rows=16 * f.G,
+                 lcol=f.nval, val=f.nval, item_gbeg=f.nitems, item_gend=f.nitems)
+    for name in ARRAYS:
+        n = sizes[name]
+        ptr = getattr(f, name)
+        dt = np.float32 if name == "val" else np.int32
+        out[name] = np.ctypeslib.as_array(ptr, shape=(n,)).astype(dt, copy=True) if n else \
+            np.zeros(0, dt)
+    return out
+
+
+def _to_struct(fm: Format, keep: list) -> OrcFormat:
+    s = OrcFormat()
+    s.M, s.N, s.segw, s.bundle, s.num_segments = fm["M"], fm["N"], fm["segw"], fm["bundle"], \
+        fm["num_segments"]
+    s.G = len(fm["group_depth"])
+    s.nval = len(fm["val"])
+    s.nitems = len(fm["item_gbeg"])
+    for name in ARRAYS:
+        dt = np.float32 if name == "val" else np.int32
+        a = np.ascontiguousarray(fm[name], dtype=dt)
+        if a.size == 0:
+            a = np.zeros(1, dt)
+        keep.append(a)
+        setattr(s, name, _p(a, C.c_float if name == "val" else C.c_int))
+    s.scale = float(fm["scale"])
+    s.fp32 = int(fm["fp32"])
+    return s
+
+
+class OracleError(RuntimeError):
+    pass
+
+
+def half_scale(val) -> np.float32:
+    v = _f32(val)
+    return np.float32(lib().orc_half_scale(_p(v, C.c_float), v.size))
+
+
+def f32_to_f16_bits(x) -> np.ndarray:
+    x = _f32(x)
+    out = np.empty(x.shape, np.uint16)
+    lib().orc_f32_to_f16_array(_p(x, C.c_float), _p(out, C.c_uint16), x.size)
+    return out
+
+
+def round_f16(x) -> np.ndarray:
+    x = _f32(x)
+    out = np.empty(x.shape, np.float32)
+    lib().orc_round_f16_array(_p(x, C.c_float), _p(out, C.c_float), x.size)
+    return out
+
+
+def build_format(row_ptr, col, val, M, N, segw=16, fp32=False) -> Format:
+    rp, ci, vv = _i32(row_ptr), _i32(col), _f32(val)
+    if ci.size == 0:
+        ci = np.zeros(1, np.int32); vv = np.zeros(1, np.float32)
+    f = OrcFormat()
+    rc = lib().orc_build(_p(rp, C.c_int), _p(ci, C.c_int), _p(vv, C.c_float), M, N, segw,
+                         int(fp32), C.byref(f))
+    if rc != 0:
+        raise OracleError(f"orc_build failed with status {rc}")
+    try:
+        return _take(f)
+    finally:
+        lib().orc_free(C.byref(f))
+
+
+def canonicalize(fm: Format) -> Format:
+    keep: list = []
+    s = _to_struct(fm, keep)
+    rc = lib().orc_canonicalize(C.byref(s))
+    if rc != 0:
+        raise OracleError(f"orc_canonicalize failed with status {rc}")
+    out = Format({k: v for k, v in fm.items()})
+    for name in ("group_rows", "lcol", "val"):
+        out[name] = keep[ARRAYS.index(name)][: len(fm[name])].copy()
+    return out
+
+
+def spmm_csr(row_ptr, col, val, M, B, mode=0, scale=1.0):
+    """Returns (R, rowL1) in float64; mode 0 = FP32 inputs, 1 = FP16 input model."""
+    rp, ci, vv, Bf = _i32(row_ptr), _i32(col), _f32(val), _f32(B)
+    if ci.size == 0:
+        ci = np.zeros(1, np.int32); vv = np.zeros(1, np.float32)
+    O = Bf.shape[1]
+    R = np.empty((M, O), np.float64)
+    L1 = np.empty(M, np.float64)
+    lib().orc_spmm_csr(_p(rp, C.c_int), _p(ci, C.c_int), _p(vv, C.c_float), M,
+                       _p(Bf, C.c_float), O, mode, float(scale), _p(R, C.c_double),
+                       _p(L1, C.c_double))
+    return R, L1
+
+
+def spmm_format(fm: Format, B) -> np.ndarray:
+    keep: list = []
+    s = _to_struct(fm, keep)
+    Bf = _f32(B)
+    R = np.empty((fm["M"], Bf.shape[1]), np.float64)
+    lib().orc_spmm_format(C.byref(s), _p(Bf, C.c_float), Bf.shape[1], _p(R, C.c_double))
+    return R
+
+
+def cpu_spmm_f64(row_ptr, col, val, B, r0=0, r1=None, threads=1, R=None):
+    """The reference driver's CPU SpMM (main.cpp:202-207) over rows [r0, r1)."""
+    rp, ci, vv, Bf = _i32(row_ptr), _i32(col), _f32(val), _f32(B)
+    M = rp.size - 1
+    r1 = M if r1 is None else r1
+    O = Bf.shape[1]
+    if R is None:
+        R = np.zeros((M, O), np.float64)
+    if threads <= 1:
+        lib().orc_cpu_spmm_f64_rows(_p(rp, C.c_int), _p(ci, C.c_int), _p(vv, C.c_float), r0, r1,
+                                    _p(Bf, C.c_float), O, _p(R, C.c_double))
+    else:
+        lib().orc_cpu_spmm_f64_omp(_p(rp, C.c_int), _p(ci, C.c_int), _p(vv, C.c_float), r0, r1,
+                                   _p(Bf, C.c_float), O, _p(R, C.c_double), threads)
+    return R
+
+
+def ref_build_format(row_ptr, col, val, M, N, segw=16, fp32=False) -> Format:
+    """The reference's own csr_to_vcsr_mc (oracle/_ref), CPU only."""
+    rp, ci, vv = _i32(row_ptr), _i32(col), _f32(val)
+    if ci.size == 0:
+        ci = np.zeros(1, np.int32); vv = np.zeros(1, np.float32)
+    f = OrcFormat()
+    err = C.create_string_buffer(512)
+    rc = ref_lib().ref_build(_p(rp, C.c_int), _p(ci, C.c_int), _p(vv, C.c_float), M, N, segw,
+                             int(fp32), C.byref(f), err, 512)
+    if rc != 0:
+        raise OracleError(err.value.decode())
+    try:
+        return _take(f)
+    finally:
+        lib().orc_free(C.byref(f))
+
+
+def ref_half_scale(val) -> np.float32:
+    v = _f32(val)
+    if v.size == 0:
+        v1 = np.zeros(1, np.float32)
+        return np.float32(ref_lib().ref_half_scale(_p(v1, C.c_float), 0))
+    return np.float32(ref_lib().ref_half_scale(_p(v, C.c_float), v.size))
+
+
+def formats_equal(a: Format, b: Format) -> list:
+    """Names of the fields that differ (empty list = identical, bit for bit)."""
+    bad = []
+    for k in ("M", "N", "segw", "bundle", "num_segments", "fp32"):
+        if a[k] != b[k]:
+            bad.append(k)
+    if np.float32(a["scale"]).tobytes() != np.float32(b["scale"]).tobytes():
+        bad.append("scale")
+    for k in ARRAYS:
+        x, y = np.asarray(a[k]), np.asarray(b[k])
+        if x.shape != y.shape or x.tobytes() != y.tobytes():
+            bad.append(k)
+    return bad

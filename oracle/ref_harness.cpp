@@ -1,0 +1,67 @@
+// ref_harness.cpp -- C entry points over the reference's own host format builder.
+//
+// TEST INFRASTRUCTURE ONLY.  oracle/Makefile compiles MuuSeoTia/VCSR_MC's src/vcsr_mc.cu
+// where it lies (with the reference's own HIP flags, CMakeLists.txt:24-27) and links it with
+// this file into oracle/_ref/libvcsrmc_ref.so.  Tests call it on the CPU only (no HIP API is
+// used) to pin the oracle's restatement of csr_to_vcsr_mc (src/vcsr_mc.cu:25-123) and
+// half_scale (src/vcsr_mc.cu:14-22), and to write the golden fixtures under tests/golden/.
+#include <cstdlib>
+#include <cstring>
+#include <exception>
+
+#include "vcsr_formats.hpp"   // the reference's header (include/vcsr_formats.hpp)
+#include "../oracle/vcsrmc_oracle.h"
+
+namespace {
+template <typename T>
+T* dup(const std::vector<T>& v) {
+    T* p = static_cast<T*>(std::malloc(sizeof(T) * (v.size() ? v.size() : 1)));
+    if (p && !v.empty()) std::memcpy(p, v.data(), sizeof(T) * v.size());
+    return p;
+}
+}  // namespace
+
+extern "C" {
+
+// Runs the reference's csr_to_vcsr_mc on a host CSR.  Returns 0, or 1 when the reference
+// threw (its message is copied into err).  The arrays are malloc'd; free with orc_free.
+int ref_build(const int* row_ptr, const int* col, const float* val, int M, int N, int segw,
+              int fp32, orc_format* out, char* err, int errlen) {
+    std::memset(out, 0, sizeof *out);
+    try {
+        CSR csr;
+        csr.M = M; csr.N = N; csr.nnz = M ? row_ptr[M] : 0;
+        csr.row_ptr.assign(row_ptr, row_ptr + M + 1);
+        csr.col.assign(col, col + csr.nnz);
+        csr.val.assign(val, val + csr.nnz);
+        VCSRMC V = csr_to_vcsr_mc(csr, fp32 != 0, segw);
+        out->M = V.M; out->N = V.N; out->segw = V.segw; out->bundle = V.bundle;
+        out->num_segments = V.num_segments;
+        out->G = (int)V.group_depth.size();
+        out->nval = (long long)V.val.size();
+        out->nitems = (int)V.item_gbeg.size();
+        out->group_ptr = dup(V.group_ptr);
+        out->group_depth = dup(V.group_depth);
+        out->group_seg_base = dup(V.group_seg_base);
+        out->group_rows = dup(V.group_rows);
+        out->lcol = dup(V.lcol);
+        out->val = dup(V.val);
+        out->item_gbeg = dup(V.item_gbeg);
+        out->item_gend = dup(V.item_gend);
+        out->scale = V.scale;
+        out->fp32 = V.fp32 ? 1 : 0;
+        return 0;
+    } catch (const std::exception& e) {
+        if (err && errlen > 0) { std::strncpy(err, e.what(), errlen - 1); err[errlen - 1] = 0; }
+        return 1;
+    }
+}
+
+float ref_half_scale(const float* val, int nnz) {
+    CSR csr;
+    csr.nnz = nnz;
+    csr.val.assign(val, val + nnz);
+    return half_scale(csr);
+}
+
+}  // extern "C"

@@ -1,0 +1,59 @@
+"""The C ABI libraries load on a machine without a GPU and export every function their headers
+declare; the C++ drop-in surface exports the reference's five functions.  No compute calls."""
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+INC = os.path.join(ROOT, "include")
+
+
+def declared(header):
+    text = open(os.path.join(INC, header)).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(vcsrmc_\w+)\s*\(", text)))
+
+
+@pytest.mark.parametrize("header,lib", [("vcsrmc.h", "libvcsrmc.so"),
+                                        ("vcsrmc_bench.h", "libvcsrmc_bench.so")])
+def test_exports_every_declared_symbol(header, lib):
+    path = os.path.join(ROOT, "vcsr_mc_amd", lib)
+    assert os.path.exists(path), f"{lib} not built"
+    L = ctypes.CDLL(path)
+    names = declared(header)
+    assert names
+    missing = [n for n in names if not hasattr(L, n)]
+    assert not missing, missing
+
+
+def test_cpp_dropin_symbols():
+    path = os.path.join(ROOT, "vcsr_mc_amd", "libvcsrmc.so")
+    out = subprocess.run(["nm", "-DC", "--defined-only", path], capture_output=True, text=True,
+                         check=True).stdout
+    for sig in ("half_scale(CSR const&)",
+                "csr_to_vcsr_mc(CSR const&, bool, int)",
+                "upload_vcsr_mc_device(VCSRMC const&)",
+                "run_vcsr_mc_spmm_gpu(VCSRMC const&, float const*, int, int, float*, "
+                "ihipStream_t*, float&)",
+                "destroy_vcsr_mc_device(ihipStream_t*)"):
+        assert sig in out, sig
+
+
+def test_status_strings_without_gpu():
+    L = ctypes.CDLL(os.path.join(ROOT, "vcsr_mc_amd", "libvcsrmc.so"))
+    L.vcsrmc_status_string.restype = ctypes.c_char_p
+    assert b"tileK" in L.vcsrmc_status_string(3)
+    assert b"segw" in L.vcsrmc_status_string(2)
+
+
+def test_no_oracle_in_product():
+    """The product library must not link or name the oracle."""
+    for lib in ("libvcsrmc.so",):
+        path = os.path.join(ROOT, "vcsr_mc_amd", lib)
+        deps = subprocess.run(["ldd", path], capture_output=True, text=True).stdout
+        assert "oracle" not in deps
+        syms = subprocess.run(["nm", "-D", path], capture_output=True, text=True).stdout
+        assert "orc_" not in syms and "ref_build" not in syms

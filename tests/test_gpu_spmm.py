@@ -1,0 +1,158 @@
+"""GPU SpMM vs the oracle.  Parity gate: per row r,
+    ||C_gpu[r,:] - C_ref[r,:]||_1 <= tau * sum_k sum_p |a_rp b_{c_p,k}|,
+tau = 1e-5 for FP32 inputs and 2e-3 for FP16 inputs, with C_ref the oracle's double-precision
+product of the same (FP16-quantised, for vcsr_mc) operands."""
+import numpy as np
+import pytest
+
+import vcsr_mc_amd as vm
+from conftest import random_csr
+from gpu_util import dev, row_l1_parity, say, sub_csr
+
+pytestmark = pytest.mark.gpu
+
+TAU = {True: 1e-5, False: 2e-3}
+
+
+def run_spmm(rp, c, v, M, N, B, fp32, tileK=128, segw=32, b16=False, C0=None, upload=None):
+    import torch
+    if upload is None:
+        f = vm.DeviceFormat.from_device_csr(dev(rp), dev(c), dev(v), M, N, fp32, segw)
+    else:
+        f = vm.DeviceFormat.from_host_format(upload)
+    with f:
+        dB = dev(B)
+        if b16:
+            dB = dB.half()
+        C = dev(C0) if C0 is not None else torch.zeros((M, B.shape[1]), dtype=torch.float32,
+                                                       device="cuda")
+        f.spmm(dB, C, tileK=tileK)
+        torch.cuda.synchronize()
+        return C.cpu().numpy(), f.info()
+
+
+def check(orc, rp, c, v, M, N, B, fp32, **kw):
+    C, info = run_spmm(rp, c, v, M, N, B, fp32, **kw)
+    scale = info["scale"]
+    R, L1 = orc.spmm_csr(rp, c, v, M, B, mode=0 if fp32 else 1, scale=scale)
+    if kw.get("C0") is not None:
+        R = R + kw["C0"].astype(np.float64)
+    ok, worst, row = row_l1_parity(C, R, L1, TAU[fp32])
+    assert ok, f"row {row}: error / bound = {worst:.3g}"
+    return C, R
+
+
+@pytest.mark.parametrize("fp32", [False, True])
+@pytest.mark.parametrize("tileK", [16, 32, 64, 128])
+def test_random_all_tiles(orc, fp32, tileK):
+    rng = np.random.default_rng(tileK + fp32)
+    for O in (1, 7, 16, 100, 128, 256):
+        M, N = int(rng.integers(1, 700)), int(rng.integers(1, 700))
+        rp, c, v = random_csr(rng, M, N, density=float(rng.choice([0.002, 0.02, 0.2])),
+                              empty_frac=0.2)
+        B = rng.uniform(-1, 1, (N, O)).astype(np.float32)
+        say("random", fp32, tileK, O, M, N, c.size)
+        check(orc, rp, c, v, M, N, B, fp32, tileK=tileK)
+
+
+@pytest.mark.parametrize("fp32", [False, True])
+def test_split_panels_and_accumulate(orc, fp32):
+    """Heavy rows make panels of > 16 tiles (split units, atomic merge); C starts non-zero and
+    rows A does not touch must come back bit-identical."""
+    rng = np.random.default_rng(11)
+    M, N, O = 900, 5000, 128
+    rp, c, v = random_csr(rng, M, N, density=0.001, heavy_rows=5, heavy_nnz=4000,
+                          empty_frac=0.3)
+    B = rng.uniform(-1, 1, (N, O)).astype(np.float32)
+    C0 = rng.uniform(-1, 1, (M, O)).astype(np.float32)
+    C0[5] = -0.0
+    say("split+accumulate", fp32)
+    C, _ = check(orc, rp, c, v, M, N, B, fp32, C0=C0)
+    empty = np.diff(rp) == 0
+    assert C[empty].tobytes() == C0[empty].tobytes()
+
+
+def test_fp16_b_matches_fp32_b(orc):
+    """FP16 B in HBM (converted by the caller) gives the same result as FP32 B converted in the
+    kernel: both round each B value to binary16."""
+    rng = np.random.default_rng(12)
+    rp, c, v = random_csr(rng, 300, 400, density=0.03)
+    B = rng.uniform(-2, 2, (400, 128)).astype(np.float32)
+    say("fp16 B")
+    C1, _ = run_spmm(rp, c, v, 300, 400, B, False)
+    C2, _ = run_spmm(rp, c, v, 300, 400, B, False, b16=True)
+    assert C1.tobytes() == C2.tobytes()
+    check(orc, rp, c, v, 300, 400, B, False, b16=True)
+
+
+def test_scaled_values(orc):
+    """|A| > 60000: A is divided by the range scale before FP16 and C multiplied back."""
+    rng = np.random.default_rng(13)
+    rp, c, v = random_csr(rng, 200, 300, density=0.05, mag=2e5)
+    B = rng.uniform(-1, 1, (300, 64)).astype(np.float32)
+    say("scaled")
+    C, R = check(orc, rp, c, v, 200, 300, B, False)
+    assert np.abs(R).max() > 1e4
+
+
+def test_subnormal_fp16_values(orc):
+    """Values that become binary16 subnormals must keep their value (no flush to zero)."""
+    rng = np.random.default_rng(14)
+    rp, c, v = random_csr(rng, 64, 64, density=0.3)
+    v = (np.sign(v) * rng.uniform(1e-7, 6e-5, v.size)).astype(np.float32)
+    v[0] = 1.0  # amax = 1: the range scale stays 1, small values stay subnormal
+    B = rng.uniform(-1, 1, (64, 32)).astype(np.float32)
+    say("subnormals")
+    check(orc, rp, c, v, 64, 64, B, False)
+
+
+def test_upload_path_matches_build_path(orc):
+    rng = np.random.default_rng(15)
+    rp, c, v = random_csr(rng, 500, 500, density=0.02)
+    f = orc.build_format(rp, c, v, 500, 500, 16, False)
+    V = vm.VCSRMC(M=500, N=500, segw=16, bundle=16, num_segments=f["num_segments"],
+                  scale=float(f["scale"]), fp32=False, **{k: f[k] for k in vm._FMT_ARRAYS})
+    B = rng.uniform(-1, 1, (500, 128)).astype(np.float32)
+    say("upload path")
+    C1, _ = run_spmm(rp, c, v, 500, 500, B, False, segw=16)
+    C2, _ = run_spmm(rp, c, v, 500, 500, B, False, upload=V)
+    assert C1.tobytes() == C2.tobytes()
+
+
+def test_empty_matrix():
+    import torch
+    say("empty")
+    f = vm.DeviceFormat.from_device_csr(dev(np.zeros(6, np.int32)), dev(np.zeros(0, np.int32)),
+                                        dev(np.zeros(0, np.float32)), 5, 7, False, 16)
+    C = torch.full((5, 8), 3.0, device="cuda")
+    B = torch.ones((7, 8), device="cuda")
+    f.spmm(B, C)
+    assert torch.all(C == 3.0)
+    f.close()
+
+
+@pytest.mark.parametrize("config", [1, 2, 3, 4, 5])
+def test_workloads_row_sample(orc, config):
+    """Full-size workloads (config 2 at its benchmark size, the larger ones scaled to fit a test),
+    checked on a seeded sample of rows against the oracle."""
+    import torch
+    size = {1: 0, 2: 0, 3: 40, 4: 1024, 5: 16}[config]
+    w = vm.WORKLOADS[config]
+    fp32 = w["precision"] == "fp32"
+    A = vm.generate(config, size)
+    O = w["O"]
+    B = vm.dense(A.N, O, seed=vm.SEED_BASE + 100 + config, fp16_exact=not fp32)
+    say("workload", config, size, A.M, A.nnz, O)
+    with vm.DeviceFormat.from_device_csr(dev(A.row_ptr), dev(A.col), dev(A.val), A.M, A.N,
+                                         fp32, 32) as f:
+        dB = dev(B).half() if not fp32 else dev(B)
+        C = torch.zeros((A.M, O), dtype=torch.float32, device="cuda")
+        f.spmm(dB, C, tileK=128)
+        Cn = C.cpu().numpy()
+        scale = f.info()["scale"]
+    rng = np.random.default_rng(config)
+    rows = np.sort(rng.choice(A.M, size=min(A.M, 3000), replace=False))
+    srp, sc, sv = sub_csr(A.row_ptr, A.col, A.val, rows)
+    R, L1 = orc.spmm_csr(srp, sc, sv, len(rows), B, mode=0 if fp32 else 1, scale=scale)
+    ok, worst, row = row_l1_parity(Cn[rows], R, L1, TAU[fp32])
+    assert ok, f"row {rows[row]}: {worst:.3g}"

@@ -1,0 +1,369 @@
+"""vcsr_mc_amd -- MI355X (gfx950) VCSR-MC SpMM.
+
+Python mirror of the reference's C++ surface (MuuSeoTia/VCSR_MC include/vcsr_formats.hpp:11-26)
+over the C ABI of ``libvcsrmc.so`` (include/vcsrmc.h).  Device buffers are torch tensors on a
+ROCm device; torch is only the allocator and stream provider here.  The compute path is the
+HIP library: if it is not built, every entry point raises, there is no fallback.
+
+Reference name                        here
+------------------------------------  -----------------------------------------------
+half_scale(const CSR&)                half_scale(csr)
+csr_to_vcsr_mc(csr, fp32, segw)       csr_to_vcsr_mc(csr, fp32=False, segw=16)
+upload_vcsr_mc_device(V)              upload_vcsr_mc_device(V)
+run_vcsr_mc_spmm_gpu(V, dB, O, ...)   run_vcsr_mc_spmm_gpu(V, dB, O, tileK, dC, stream) -> ms
+destroy_vcsr_mc_device(st)            destroy_vcsr_mc_device(stream)
+
+``DeviceFormat`` is the handle-based form (several formats at once, GPU build straight from a
+device CSR, FP16 B).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from dataclasses import dataclass, field
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libvcsrmc.so")
+BENCH_LIB_PATH = os.path.join(HERE, "libvcsrmc_bench.so")
+
+OK, ERR_ARG, ERR_SEGW, ERR_TILEK, ERR_CSR, ERR_UNSORTED, ERR_FORMAT, ERR_OVERFLOW, ERR_HIP, \
+    ERR_STATE = range(10)
+B_F32, B_F16 = 0, 1
+
+
+class VCSRMCError(RuntimeError):
+    def __init__(self, status: int, msg: str):
+        super().__init__(msg)
+        self.status = status
+
+
+class _Info(C.Structure):
+    _fields_ = [
+        ("M", C.c_int), ("N", C.c_int), ("segw", C.c_int), ("bundle", C.c_int),
+        ("num_segments", C.c_int), ("num_groups", C.c_int), ("nval", C.c_longlong),
+        ("num_items", C.c_int), ("scale", C.c_float), ("fp32", C.c_int), ("nnz", C.c_longlong),
+        ("num_panels", C.c_int), ("num_chunks", C.c_int), ("num_units", C.c_int),
+        ("device", C.c_int),
+    ]
+
+
+_lib_handle = None
+_bench_handle = None
+
+
+def lib():
+    """The product library; raises if it has not been built."""
+    global _lib_handle
+    if _lib_handle is None:
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(f"{LIB_PATH} is not built (run __graft_entry__.build())")
+        L = C.CDLL(LIB_PATH)
+        vp, ip, fp = C.c_void_p, C.POINTER(C.c_int), C.POINTER(C.c_float)
+        L.vcsrmc_create.argtypes = [C.POINTER(vp)]
+        L.vcsrmc_destroy.argtypes = [vp]
+        L.vcsrmc_half_scale.argtypes = [vp, C.c_longlong, fp, vp]
+        L.vcsrmc_build_csr.argtypes = [vp, vp, vp, vp, C.c_int, C.c_int, C.c_int, C.c_int,
+                                       C.c_int, vp]
+        L.vcsrmc_upload.argtypes = [vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
+                                    C.c_longlong, C.c_int, vp, vp, vp, vp, vp, vp, vp, vp,
+                                    C.c_float, C.c_int, vp]
+        L.vcsrmc_get_info.argtypes = [vp, C.POINTER(_Info)]
+        L.vcsrmc_download.argtypes = [vp] + [vp] * 8
+        L.vcsrmc_spmm.argtypes = [vp, vp, C.c_int, C.c_int, C.c_int, vp, vp, fp]
+        L.vcsrmc_status_string.restype = C.c_char_p
+        L.vcsrmc_status_string.argtypes = [C.c_int]
+        L.vcsrmc_last_error.restype = C.c_char_p
+        for f in ("vcsrmc_create", "vcsrmc_destroy", "vcsrmc_half_scale", "vcsrmc_build_csr",
+                  "vcsrmc_upload", "vcsrmc_get_info", "vcsrmc_download", "vcsrmc_spmm"):
+            getattr(L, f).restype = C.c_int
+        _lib_handle = L
+    return _lib_handle
+
+
+def bench_lib():
+    global _bench_handle
+    if _bench_handle is None:
+        if not os.path.exists(BENCH_LIB_PATH):
+            raise ImportError(f"{BENCH_LIB_PATH} is not built (run __graft_entry__.build())")
+        L = C.CDLL(BENCH_LIB_PATH)
+        vp = C.c_void_p
+        L.vcsrmc_gen.argtypes = [C.c_int, C.c_int, C.c_ulonglong, C.POINTER(vp)]
+        L.vcsrmc_gen_info.argtypes = [vp, C.POINTER(C.c_int), C.POINTER(C.c_int),
+                                      C.POINTER(C.c_longlong)]
+        L.vcsrmc_gen_copy.argtypes = [vp, vp, vp, vp]
+        L.vcsrmc_gen_free.argtypes = [vp]
+        L.vcsrmc_gen_dense.argtypes = [C.c_int, C.c_ulonglong, C.c_int, vp, C.c_longlong]
+        L.vcsrmc_rocsparse_spmm.argtypes = [C.c_int, C.c_int, C.c_int, vp, vp, vp, C.c_int, vp,
+                                            C.c_int, C.c_int, vp, C.c_float, C.c_int, vp,
+                                            C.POINTER(C.c_float), C.POINTER(C.c_float)]
+        for f in ("vcsrmc_gen", "vcsrmc_gen_info", "vcsrmc_gen_copy", "vcsrmc_gen_free",
+                  "vcsrmc_gen_dense", "vcsrmc_rocsparse_spmm", "vcsrmc_rocsparse_release"):
+            getattr(L, f).restype = C.c_int
+        _bench_handle = L
+    return _bench_handle
+
+
+def _check(status: int, what: str) -> None:
+    if status != OK:
+        detail = lib().vcsrmc_last_error().decode(errors="replace")
+        raise VCSRMCError(status, f"{what}: {detail or lib().vcsrmc_status_string(status).decode()}")
+
+
+def _ptr(x) -> int | None:
+    """Raw address of a torch tensor or numpy array (None stays None)."""
+    if x is None:
+        return None
+    if isinstance(x, np.ndarray):
+        return x.ctypes.data
+    return int(x.data_ptr())
+
+
+def _stream_ptr(stream) -> int | None:
+    if stream is None:
+        import torch
+        return int(torch.cuda.current_stream().cuda_stream)
+    if isinstance(stream, int):
+        return stream
+    return int(stream.cuda_stream)
+
+
+# ---- host containers mirroring the reference structs -------------------------------------
+@dataclass
+class CSR:
+    """include/csr.hpp:8-13: M, N, nnz, row_ptr[M+1], col[nnz], val[nnz] (host arrays)."""
+    M: int
+    N: int
+    nnz: int
+    row_ptr: np.ndarray
+    col: np.ndarray
+    val: np.ndarray
+
+    @classmethod
+    def from_arrays(cls, row_ptr, col, val, M, N):
+        rp = np.ascontiguousarray(row_ptr, dtype=np.int32)
+        return cls(int(M), int(N), int(rp[-1]) if len(rp) else 0, rp,
+                   np.ascontiguousarray(col, dtype=np.int32),
+                   np.ascontiguousarray(val, dtype=np.float32))
+
+
+_FMT_ARRAYS = ("group_ptr", "group_depth", "group_seg_base", "group_rows", "lcol", "val",
+               "item_gbeg", "item_gend")
+
+
+@dataclass
+class VCSRMC:
+    """include/vcsr_formats.hpp:14-21, with numpy arrays for the std::vectors."""
+    M: int = 0
+    N: int = 0
+    segw: int = 16
+    bundle: int = 16
+    num_segments: int = 0
+    group_ptr: np.ndarray = field(default_factory=lambda: np.zeros(0, np.int32))
+    group_depth: np.ndarray = field(default_factory=lambda: np.zeros(0, np.int32))
+    group_seg_base: np.ndarray = field(default_factory=lambda: np.zeros(0, np.int32))
+    group_rows: np.ndarray = field(default_factory=lambda: np.zeros(0, np.int32))
+    lcol: np.ndarray = field(default_factory=lambda: np.zeros(0, np.int32))
+    val: np.ndarray = field(default_factory=lambda: np.zeros(0, np.float32))
+    item_gbeg: np.ndarray = field(default_factory=lambda: np.zeros(0, np.int32))
+    item_gend: np.ndarray = field(default_factory=lambda: np.zeros(0, np.int32))
+    scale: float = 1.0
+    fp32: bool = False
+
+
+# ---- handle-based device format -----------------------------------------------------------
+class DeviceFormat:
+    """One device-resident VCSR-MC format (a vcsrmc_t handle)."""
+
+    def __init__(self):
+        h = C.c_void_p()
+        _check(lib().vcsrmc_create(C.byref(h)), "vcsrmc_create")
+        self._h = h
+
+    @property
+    def handle(self):
+        if self._h is None:
+            raise VCSRMCError(ERR_STATE, "format closed")
+        return self._h
+
+    def close(self):
+        if getattr(self, "_h", None) is not None:
+            _check(lib().vcsrmc_destroy(self._h), "vcsrmc_destroy")
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    @classmethod
+    def from_device_csr(cls, row_ptr, col, val, M, N, fp32=False, segw=16, stream=None):
+        """GPU build from torch device tensors (int32 row_ptr/col, float32 val)."""
+        f = cls()
+        nnz = int(col.numel())
+        _check(lib().vcsrmc_build_csr(f.handle, _ptr(row_ptr), _ptr(col) if nnz else None,
+                                      _ptr(val) if nnz else None, int(M), int(N), nnz,
+                                      int(bool(fp32)), int(segw), _stream_ptr(stream)),
+               "vcsrmc_build_csr")
+        return f
+
+    @classmethod
+    def from_host_format(cls, V: VCSRMC, stream=None):
+        f = cls()
+        arrs = {}
+        for name in _FMT_ARRAYS:
+            dt = np.float32 if name == "val" else np.int32
+            a = np.ascontiguousarray(getattr(V, name), dtype=dt)
+            arrs[name] = a
+        G = len(arrs["group_depth"])
+        _check(lib().vcsrmc_upload(
+            f.handle, int(V.M), int(V.N), int(V.segw), int(V.bundle), int(V.num_segments), G,
+            len(arrs["val"]), len(arrs["item_gbeg"]),
+            *[(arrs[n].ctypes.data if arrs[n].size else None) for n in _FMT_ARRAYS],
+            float(V.scale), int(bool(V.fp32)), _stream_ptr(stream)), "vcsrmc_upload")
+        return f
+
+    def info(self) -> dict:
+        i = _Info()
+        _check(lib().vcsrmc_get_info(self.handle, C.byref(i)), "vcsrmc_get_info")
+        return {k: getattr(i, k) for k, _ in _Info._fields_}
+
+    def download(self) -> VCSRMC:
+        i = self.info()
+        G, nval, ni = i["num_groups"], i["nval"], i["num_items"]
+        out = {
+            "group_ptr": np.zeros(G + 1, np.int32), "group_depth": np.zeros(G, np.int32),
+            "group_seg_base": np.zeros(G, np.int32), "group_rows": np.zeros(16 * G, np.int32),
+            "lcol": np.zeros(nval, np.int32), "val": np.zeros(nval, np.float32),
+            "item_gbeg": np.zeros(ni, np.int32), "item_gend": np.zeros(ni, np.int32),
+        }
+        _check(lib().vcsrmc_download(self.handle, *[(out[n].ctypes.data if out[n].size else None)
+                                                    for n in _FMT_ARRAYS]), "vcsrmc_download")
+        return VCSRMC(M=i["M"], N=i["N"], segw=i["segw"], bundle=i["bundle"],
+                      num_segments=i["num_segments"], scale=float(np.float32(i["scale"])),
+                      fp32=bool(i["fp32"]), **out)
+
+    def spmm(self, B, C_out, tileK=128, O=None, stream=None, timed=False):
+        """C_out += A . B on the GPU.  B: (N, O) float32 or float16 device tensor; C_out:
+        (M, O) float32.  Returns the event-timed kernel time in ms when timed, else None."""
+        import torch
+        b_dtype = B_F16 if B.dtype == torch.float16 else B_F32
+        if B.dtype not in (torch.float16, torch.float32) or C_out.dtype != torch.float32:
+            raise VCSRMCError(ERR_ARG, "B must be float16/float32 and C float32")
+        if not (B.is_contiguous() and C_out.is_contiguous()):
+            raise VCSRMCError(ERR_ARG, "B and C must be contiguous row-major")
+        O = int(B.shape[1]) if O is None else int(O)
+        ms = C.c_float(0.0)
+        _check(lib().vcsrmc_spmm(self.handle, _ptr(B), b_dtype, O, int(tileK), _ptr(C_out),
+                                 _stream_ptr(stream), C.byref(ms) if timed else None),
+               "vcsrmc_spmm")
+        return ms.value if timed else None
+
+
+# ---- the reference's free functions (global single format, src/vcsr_mc.cu:126-131) ---------
+_global = {"fmt": None, "uploaded": False}
+
+
+def half_scale(csr: CSR) -> float:
+    import torch
+    v = torch.from_numpy(np.ascontiguousarray(csr.val, np.float32)).cuda()
+    s = C.c_float(1.0)
+    _check(lib().vcsrmc_half_scale(_ptr(v) if v.numel() else None, int(v.numel()), C.byref(s),
+                                   _stream_ptr(None)), "half_scale")
+    return s.value
+
+
+def csr_to_vcsr_mc(csr: CSR, fp32: bool = False, segw: int = 16) -> VCSRMC:
+    """The format, built on the GPU and copied back (include/vcsr_formats.hpp:22)."""
+    import torch
+    if segw not in (16, 32, 48, 64):
+        raise VCSRMCError(ERR_SEGW, "vcsr_mc supports segw in {16, 32, 48, 64}")
+    rp = torch.from_numpy(np.ascontiguousarray(csr.row_ptr, np.int32)).cuda()
+    ci = torch.from_numpy(np.ascontiguousarray(csr.col, np.int32)).cuda()
+    vv = torch.from_numpy(np.ascontiguousarray(csr.val, np.float32)).cuda()
+    with DeviceFormat.from_device_csr(rp, ci, vv, csr.M, csr.N, fp32, segw) as f:
+        return f.download()
+
+
+def upload_vcsr_mc_device(V: VCSRMC) -> None:
+    if _global["uploaded"]:
+        return
+    _global["fmt"] = DeviceFormat.from_host_format(V)
+    _global["uploaded"] = True
+
+
+def run_vcsr_mc_spmm_gpu(V: VCSRMC, dB, O: int, tileK: int, dC, stream=None) -> float:
+    """C += A . B, event-timed like the reference (returns ms)."""
+    if len(V.item_gbeg) == 0:
+        return 0.0
+    if not _global["uploaded"]:
+        upload_vcsr_mc_device(V)
+    return _global["fmt"].spmm(dB, dC, tileK=tileK, O=O, stream=stream, timed=True)
+
+
+def destroy_vcsr_mc_device(stream=None) -> None:
+    if _global["fmt"] is not None:
+        _global["fmt"].close()
+    _global["fmt"] = None
+    _global["uploaded"] = False
+
+
+# ---- workloads (libvcsrmc_bench.so) --------------------------------------------------------
+SEED_BASE = 20260923  # the reference's fixed seed (src/main.cpp:165); workload k uses +k
+
+WORKLOADS = {
+    1: dict(name="uniform", precision="fp32", O=128),
+    2: dict(name="powerlaw", precision="fp16", O=128),
+    3: dict(name="stencil27", precision="fp32", O=128),
+    4: dict(name="block32", precision="fp16", O=256),
+    5: dict(name="rmat", precision="fp16", O=128),
+}
+
+
+def generate(config: int, size: int = 0, seed: int | None = None) -> CSR:
+    """Seeded synthetic matrix of a benchmark workload (see include/vcsrmc_bench.h)."""
+    L = bench_lib()
+    seed = SEED_BASE + config if seed is None else seed
+    h = C.c_void_p()
+    if L.vcsrmc_gen(int(config), int(size), C.c_ulonglong(seed), C.byref(h)) != 0:
+        raise VCSRMCError(ERR_ARG, f"generator failed for config {config} size {size}")
+    try:
+        M, N, nnz = C.c_int(), C.c_int(), C.c_longlong()
+        L.vcsrmc_gen_info(h, C.byref(M), C.byref(N), C.byref(nnz))
+        rp = np.empty(M.value + 1, np.int32)
+        col = np.empty(nnz.value, np.int32)
+        val = np.empty(nnz.value, np.float32)
+        L.vcsrmc_gen_copy(h, rp.ctypes.data, col.ctypes.data if nnz.value else None,
+                          val.ctypes.data if nnz.value else None)
+    finally:
+        L.vcsrmc_gen_free(h)
+    return CSR(M.value, N.value, nnz.value, rp, col, val)
+
+
+def dense(n_rows: int, n_cols: int, seed: int, dist: int = 0, fp16_exact: bool = False) -> np.ndarray:
+    out = np.empty((n_rows, n_cols), np.float32)
+    if bench_lib().vcsrmc_gen_dense(int(dist), C.c_ulonglong(seed), int(fp16_exact),
+                                    out.ctypes.data, out.size) != 0:
+        raise VCSRMCError(ERR_ARG, "dense generator failed")
+    return out
+
+
+def rocsparse_spmm(M, N, row_ptr, col, val, B, C_out, alpha=1.0, alg=0, stream=None):
+    """hipSPARSE SpMM C = alpha A.B (beta 0) on device tensors; returns (ms, setup_ms)."""
+    import torch
+    ms, setup = C.c_float(0.0), C.c_float(0.0)
+    rc = bench_lib().vcsrmc_rocsparse_spmm(
+        int(M), int(N), int(col.numel()), _ptr(row_ptr), _ptr(col), _ptr(val),
+        int(val.dtype == torch.float16), _ptr(B), int(B.dtype == torch.float16), int(B.shape[1]),
+        _ptr(C_out), float(alpha), int(alg), _stream_ptr(stream), C.byref(ms), C.byref(setup))
+    if rc != 0:
+        raise VCSRMCError(ERR_HIP, f"hipSPARSE SpMM failed ({rc})")
+    return ms.value, setup.value

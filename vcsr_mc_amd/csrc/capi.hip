@@ -1,0 +1,219 @@
+// capi.hip -- the extern "C" boundary of libvcsrmc.so (declared in include/vcsrmc.h).
+// Internal errors are C++ exceptions carrying a status; they stop here and become return
+// codes, with the message kept per thread for vcsrmc_last_error().
+#include <cstdio>
+#include <new>
+#include <string>
+
+#include "../../include/vcsrmc.h"
+#include "internal.hpp"
+
+struct vcsrmc_format_s {
+    vcsrmc::DeviceFormat F;
+    int device = 0;
+};
+
+namespace vcsrmc {
+
+[[noreturn]] void throw_hip(hipError_t e, const char* what, const char* file, int line) {
+    char buf[512];
+    std::snprintf(buf, sizeof buf, "HIP error %s (%s) in %s at %s:%d", hipGetErrorName(e),
+                  hipGetErrorString(e), what, file, line);
+    throw Error(VCSRMC_ERR_HIP, buf);
+}
+
+}  // namespace vcsrmc
+
+namespace {
+
+thread_local std::string g_last_error;
+
+template <typename Fn>
+int guarded(Fn&& fn) {
+    try {
+        fn();
+        return VCSRMC_OK;
+    } catch (const vcsrmc::Error& e) {
+        g_last_error = e.what();
+        return e.status;
+    } catch (const std::bad_alloc&) {
+        g_last_error = "host allocation failed";
+        return VCSRMC_ERR_HIP;
+    } catch (const std::exception& e) {
+        g_last_error = e.what();
+        return VCSRMC_ERR_HIP;
+    }
+}
+
+// Makes the handle's device current for the scope of a call.
+struct DeviceScope {
+    int prev = -1;
+    explicit DeviceScope(int dev) {
+        VCSRMC_HIP(hipGetDevice(&prev));
+        if (prev != dev) VCSRMC_HIP(hipSetDevice(dev));
+    }
+    ~DeviceScope() {
+        int cur = -1;
+        if (hipGetDevice(&cur) == hipSuccess && cur != prev && prev >= 0) (void)hipSetDevice(prev);
+    }
+};
+
+void need(bool ok, const char* msg) {
+    if (!ok) throw vcsrmc::Error(VCSRMC_ERR_ARG, msg);
+}
+
+}  // namespace
+
+extern "C" {
+
+int vcsrmc_create(vcsrmc_t* out) {
+    return guarded([&] {
+        need(out != nullptr, "null output handle");
+        *out = nullptr;
+        auto* h = new vcsrmc_format_s();
+        if (hipGetDevice(&h->device) != hipSuccess) {
+            delete h;
+            throw vcsrmc::Error(VCSRMC_ERR_HIP, "no HIP device");
+        }
+        *out = h;
+    });
+}
+
+int vcsrmc_destroy(vcsrmc_t h) {
+    return guarded([&] {
+        if (!h) return;
+        {
+            DeviceScope ds(h->device);
+            h->F.clear();
+        }
+        delete h;
+    });
+}
+
+int vcsrmc_half_scale(const float* d_val, long long nnz, float* scale, void* stream) {
+    return guarded([&] {
+        need(scale != nullptr && nnz >= 0 && (nnz == 0 || d_val != nullptr), "bad argument");
+        const float amax = vcsrmc::device_absmax(d_val, nnz, (hipStream_t)stream);
+        *scale = vcsrmc::half_scale_from_amax(amax);
+    });
+}
+
+int vcsrmc_build_csr(vcsrmc_t h, const int* d_row_ptr, const int* d_col, const float* d_val,
+                     int M, int N, int nnz, int fp32, int segw, void* stream) {
+    return guarded([&] {
+        need(h != nullptr, "null handle");
+        DeviceScope ds(h->device);
+        try {
+            vcsrmc::build_from_csr(h->F, d_row_ptr, d_col, d_val, M, N, nnz, segw, fp32,
+                                   (hipStream_t)stream);
+        } catch (...) {
+            h->F.clear();
+            throw;
+        }
+    });
+}
+
+int vcsrmc_upload(vcsrmc_t h, int M, int N, int segw, int bundle, int num_segments,
+                  int num_groups, long long nval, int num_items, const int* group_ptr,
+                  const int* group_depth, const int* group_seg_base, const int* group_rows,
+                  const int* lcol, const float* val, const int* item_gbeg, const int* item_gend,
+                  float scale, int fp32, void* stream) {
+    return guarded([&] {
+        need(h != nullptr, "null handle");
+        need(group_ptr != nullptr, "null group_ptr");
+        DeviceScope ds(h->device);
+        vcsrmc::HostArrays H{M, N, segw, bundle, num_segments, num_groups, num_items, nval,
+                             group_ptr, group_depth, group_seg_base, group_rows, lcol, val,
+                             item_gbeg, item_gend, scale, fp32};
+        try {
+            vcsrmc::build_from_host(h->F, H, (hipStream_t)stream);
+        } catch (...) {
+            h->F.clear();
+            throw;
+        }
+    });
+}
+
+int vcsrmc_get_info(vcsrmc_t h, vcsrmc_info* out) {
+    return guarded([&] {
+        need(h != nullptr && out != nullptr, "null argument");
+        if (!h->F.ready) throw vcsrmc::Error(VCSRMC_ERR_STATE, "no format in this handle");
+        const auto& F = h->F;
+        out->M = F.M; out->N = F.N; out->segw = F.segw; out->bundle = F.bundle;
+        out->num_segments = F.num_segments; out->num_groups = F.G; out->nval = F.nval;
+        out->num_items = F.nitems; out->scale = F.scale; out->fp32 = F.fp32; out->nnz = F.nnz;
+        out->num_panels = F.num_panels; out->num_chunks = F.num_chunks;
+        out->num_units = F.num_units; out->device = h->device;
+    });
+}
+
+int vcsrmc_download(vcsrmc_t h, int* group_ptr, int* group_depth, int* group_seg_base,
+                    int* group_rows, int* lcol, float* val, int* item_gbeg, int* item_gend) {
+    return guarded([&] {
+        need(h != nullptr, "null handle");
+        if (!h->F.ready) throw vcsrmc::Error(VCSRMC_ERR_STATE, "no format in this handle");
+        DeviceScope ds(h->device);
+        const auto& F = h->F;
+        auto get = [](void* dst, const void* src, size_t bytes) {
+            if (dst && bytes) VCSRMC_HIP(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost));
+        };
+        get(group_ptr, F.group_ptr.p, sizeof(int) * ((size_t)F.G + 1));
+        get(group_depth, F.group_depth.p, sizeof(int) * (size_t)F.G);
+        get(group_seg_base, F.group_seg_base.p, sizeof(int) * (size_t)F.G);
+        get(group_rows, F.group_rows.p, sizeof(int) * 16 * (size_t)F.G);
+        get(lcol, F.lcol.p, sizeof(int) * (size_t)F.nval);
+        get(val, F.val.p, sizeof(float) * (size_t)F.nval);
+        get(item_gbeg, F.item_gbeg.p, sizeof(int) * (size_t)F.nitems);
+        get(item_gend, F.item_gend.p, sizeof(int) * (size_t)F.nitems);
+    });
+}
+
+int vcsrmc_spmm(vcsrmc_t h, const void* dB, int b_dtype, int O, int tileK, float* dC,
+                void* stream, float* ms) {
+    return guarded([&] {
+        need(h != nullptr, "null handle");
+        need(b_dtype == VCSRMC_B_F32 || b_dtype == VCSRMC_B_F16, "unknown B dtype");
+        DeviceScope ds(h->device);
+        hipStream_t st = (hipStream_t)stream;
+        if (!ms) {
+            vcsrmc::spmm_launch(h->F, dB, b_dtype == VCSRMC_B_F16, O, tileK, dC, st);
+            return;
+        }
+        hipEvent_t t0, t1;
+        VCSRMC_HIP(hipEventCreate(&t0));
+        VCSRMC_HIP(hipEventCreate(&t1));
+        try {
+            VCSRMC_HIP(hipEventRecord(t0, st));
+            vcsrmc::spmm_launch(h->F, dB, b_dtype == VCSRMC_B_F16, O, tileK, dC, st);
+            VCSRMC_HIP(hipEventRecord(t1, st));
+            VCSRMC_HIP(hipEventSynchronize(t1));
+            VCSRMC_HIP(hipEventElapsedTime(ms, t0, t1));
+        } catch (...) {
+            (void)hipEventDestroy(t0);
+            (void)hipEventDestroy(t1);
+            throw;
+        }
+        VCSRMC_HIP(hipEventDestroy(t0));
+        VCSRMC_HIP(hipEventDestroy(t1));
+    });
+}
+
+const char* vcsrmc_status_string(int status) {
+    switch (status) {
+        case VCSRMC_OK: return "ok";
+        case VCSRMC_ERR_ARG: return "invalid argument";
+        case VCSRMC_ERR_SEGW: return "vcsr_mc supports segw in {16, 32, 48, 64}";
+        case VCSRMC_ERR_TILEK: return "vcsr_mc supports tileK in {16, 32, 64, 128}";
+        case VCSRMC_ERR_CSR: return "invalid CSR";
+        case VCSRMC_ERR_UNSORTED: return "CSR columns not strictly increasing within a row";
+        case VCSRMC_ERR_FORMAT: return "inconsistent format arrays";
+        case VCSRMC_ERR_OVERFLOW: return "format size exceeds int32";
+        case VCSRMC_ERR_HIP: return "HIP runtime error";
+        case VCSRMC_ERR_STATE: return "no format";
+        default: return "unknown status";
+    }
+}
+
+const char* vcsrmc_last_error(void) { return g_last_error.c_str(); }
+
+}  // extern "C"

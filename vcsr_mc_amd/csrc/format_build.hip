@@ -1,0 +1,716 @@
+// format_build.hip -- the VCSR-MC format built on the GPU.
+//
+// Part 1 reproduces csr_to_vcsr_mc (MuuSeoTia/VCSR_MC src/vcsr_mc.cu:25-123) as a pipeline
+// of scans, one stable radix sort and scatters:
+//   1. validate row_ptr, expand the row id of every nonzero (max-scan of row heads)
+//   2. flag the first nonzero of every (segment, row) run; exclusive scan -> pair index
+//   3. pair keys (segment << 6 | segw - count); a stable radix sort orders each segment's
+//      rows by count, descending, ties by ascending row (the reference's order of equal
+//      counts is std::unordered_map iteration order, :59-66; this build fixes it)
+//   4. bundles of 16 -> groups: depth, seg_base, rows; group_ptr = scan of 16*depth
+//   5. depth-major, lane-minor scatter of lcol / val * (1/scale), padded with -1 / 0
+//   6. work items: runs of <= chunk groups of one segment, stable sort by work, descending
+// Part 2 derives the execution layout read by the multiply kernels (16-row panels cut into
+// compacted 32-column tiles; see internal.hpp) from the same nonzeros.
+#include <climits>
+#include <cmath>
+#include <cstring>
+#include <vector>
+
+#include "../../include/vcsrmc.h"
+#include "internal.hpp"
+
+namespace vcsrmc {
+
+// ------------------------------------------------------------------------------------------
+// FP16 range scale.
+// ------------------------------------------------------------------------------------------
+float half_scale_from_amax(float amax) {
+    // src/vcsr_mc.cu:14-22.  The reference binary is compiled with -ffast-math
+    // (CMakeLists.txt:24-27), which evaluates `amax / 60000.0f` as amax * fl(1/60000); that
+    // is reproduced here so the scale (and every val * (1/scale)) matches it bit for bit.
+    const float headroom = 60000.0f;
+    const float min_normal = 6.103515625e-05f;
+    volatile float one = 1.0f;
+    const float inv_headroom = one / headroom;
+    if (amax > headroom) return amax * inv_headroom;
+    if (amax > 0.0f && amax < min_normal) return amax * inv_headroom;
+    return 1.0f;
+}
+
+__global__ __launch_bounds__(256) void k_absmax_bits(const float* __restrict__ v, long long n,
+                                                     unsigned* __restrict__ out) {
+    __shared__ int wsum[4];
+    int m = 0;  // bit pattern of the largest finite-or-inf |v| seen (NaN skipped)
+    for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (long long)gridDim.x * blockDim.x) {
+        const unsigned b = __float_as_uint(v[i]) & 0x7fffffffu;
+        if (b <= 0x7f800000u && (int)b > m) m = (int)b;
+    }
+    int total;
+    block_scan_256(m, OpMax{}, 0, wsum, total);
+    if (threadIdx.x == 0 && total > 0) atomicMax(out, (unsigned)total);
+}
+
+float device_absmax(const float* d_val, long long n, hipStream_t st) {
+    DevBuf<unsigned> bits(1);
+    VCSRMC_HIP(hipMemsetAsync(bits.p, 0, sizeof(unsigned), st));
+    if (n > 0) {
+        const unsigned grid = (unsigned)std::min<long long>(grid_for(n, 256), 4096);
+        hipLaunchKernelGGL(k_absmax_bits, dim3(grid), dim3(256), 0, st, d_val, n, bits.p);
+        VCSRMC_HIP(hipGetLastError());
+    }
+    const unsigned b = read_scalar(bits.p, st);
+    float a;
+    std::memcpy(&a, &b, sizeof a);
+    return a;
+}
+
+// ------------------------------------------------------------------------------------------
+// Part 1 kernels.
+// ------------------------------------------------------------------------------------------
+enum : int { kErrCsr = 1, kErrRange = 2, kErrUnsorted = 4, kErrFormat = 8, kErrDuplicate = 16 };
+
+__global__ void k_check_row_ptr(const int* __restrict__ rp, int M, int nnz, int* __restrict__ err) {
+    const long long r = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (r > M) return;
+    const int a = rp[r];
+    bool bad = a < 0 || a > nnz;
+    if (r == 0) bad |= a != 0;
+    if (r == M) bad |= a != nnz;
+    if (r < M) bad |= rp[r + 1] < a;
+    if (bad) atomicOr(err, kErrCsr);
+}
+
+__global__ void k_mark_row_heads(const int* __restrict__ rp, int M, int* __restrict__ head) {
+    const long long r = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (r >= M) return;
+    const int a = rp[r];
+    if (a < rp[r + 1]) head[a] = (int)r;
+}
+
+// Per nonzero: range / order checks and the (segment, row) run heads.
+__global__ void k_pair_heads(const int* __restrict__ rp, const int* __restrict__ col,
+                             const int* __restrict__ row_of, int nnz, int N, int segw,
+                             int* __restrict__ head, int* __restrict__ err) {
+    const long long p = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (p >= nnz) return;
+    const int r = row_of[p];
+    const int c = col[p];
+    int e = 0;
+    if (c < 0 || c >= N) e |= kErrRange;
+    const bool first = p == rp[r];
+    int h = 1;
+    if (!first) {
+        const int prev = col[p - 1];
+        if (prev >= c) e |= kErrUnsorted;
+        h = (c / segw) != (prev / segw);
+    }
+    head[p] = h;
+    if (e) atomicOr(err, e);
+}
+
+__global__ void k_emit_pairs(const int* __restrict__ head, const int* __restrict__ pidx,
+                             const int* __restrict__ row_of, int nnz, int* __restrict__ pstart,
+                             int* __restrict__ prow) {
+    const long long p = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (p >= nnz) return;
+    if (head[p]) {
+        const int q = pidx[p];
+        pstart[q] = (int)p;
+        prow[q] = row_of[p];
+    }
+}
+
+template <typename K>
+__global__ void k_pair_keys(const int* __restrict__ pstart, const int* __restrict__ col, int P,
+                            int segw, K* __restrict__ key, uint32_t* __restrict__ pay,
+                            int* __restrict__ seg_n) {
+    const long long q = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (q >= P) return;
+    const int cnt = pstart[q + 1] - pstart[q];
+    const int seg = col[pstart[q]] / segw;
+    key[q] = ((K)seg << 6) | (K)(segw - cnt);
+    pay[q] = (uint32_t)q;
+    atomicAdd(&seg_n[seg], 1);
+}
+
+__global__ void k_groups_per_seg(const int* __restrict__ seg_n, int S, int* __restrict__ gnum) {
+    const long long s = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (s < S) gnum[s] = (seg_n[s] + 15) / 16;
+}
+
+template <typename K>
+__global__ void k_group_heads(const K* __restrict__ skey, const int* __restrict__ seg_start,
+                              const int* __restrict__ gbase, int P, int* __restrict__ ghead) {
+    const long long s = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (s >= P) return;
+    const int seg = (int)(skey[s] >> 6);
+    const int j = (int)s - seg_start[seg];
+    if ((j & 15) == 0) ghead[gbase[seg] + (j >> 4)] = (int)s;
+}
+
+template <typename K>
+__global__ void k_group_info(const K* __restrict__ skey, const uint32_t* __restrict__ spay,
+                             const int* __restrict__ ghead, const int* __restrict__ seg_start,
+                             const int* __restrict__ pstart, const int* __restrict__ prow, int G,
+                             int segw, int* __restrict__ depth, int* __restrict__ seg_base,
+                             int* __restrict__ rows, int* __restrict__ size16) {
+    const long long g = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (g >= G) return;
+    const int s = ghead[g];
+    const int seg = (int)(skey[s] >> 6);
+    const int end = seg_start[seg + 1];
+    const uint32_t q = spay[s];
+    const int d = pstart[q + 1] - pstart[q];
+    depth[g] = d;
+    seg_base[g] = seg * segw;
+    size16[g] = 16 * d;
+#pragma unroll
+    for (int lane = 0; lane < 16; ++lane)
+        rows[16 * g + lane] = (s + lane < end) ? prow[spay[s + lane]] : -1;
+}
+
+__global__ void k_to_int(const long long* __restrict__ a, int* __restrict__ b, long long n) {
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) b[i] = (int)a[i];
+}
+
+// One wave per group: 16 lanes per depth level, four levels per step.
+template <typename K>
+__global__ __launch_bounds__(256) void k_fill_group_entries(
+    const K* __restrict__ skey, const uint32_t* __restrict__ spay, const int* __restrict__ ghead,
+    const int* __restrict__ seg_start, const int* __restrict__ pstart,
+    const int* __restrict__ group_ptr, const int* __restrict__ depth,
+    const int* __restrict__ seg_base, const int* __restrict__ col, const float* __restrict__ v,
+    int G, float inv_scale, int* __restrict__ lcol, float* __restrict__ val) {
+    const long long g = ((long long)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    if (g >= G) return;
+    const int lane = threadIdx.x & 63, l16 = lane & 15, dsub = lane >> 4;
+    const int s = ghead[g];
+    const int seg = (int)(skey[s] >> 6);
+    const int end = seg_start[seg + 1];
+    int cnt = 0, p0 = 0;
+    if (s + l16 < end) {
+        const uint32_t q = spay[s + l16];
+        p0 = pstart[q];
+        cnt = pstart[q + 1] - p0;
+    }
+    const int gp = group_ptr[g], dep = depth[g], base = seg_base[g];
+    for (int d = dsub; d < dep; d += 4) {
+        const long long idx = (long long)gp + (long long)d * 16 + l16;
+        if (d < cnt) {
+            lcol[idx] = col[p0 + d] - base;
+            val[idx] = v[p0 + d] * inv_scale;
+        } else {
+            lcol[idx] = -1;
+            val[idx] = 0.0f;
+        }
+    }
+}
+
+__global__ void k_items_per_seg(const int* __restrict__ gnum, int S, int chunk,
+                                int* __restrict__ inum) {
+    const long long s = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (s < S) inum[s] = (gnum[s] + chunk - 1) / chunk;
+}
+
+__global__ void k_make_items(const int* __restrict__ gbase, const int* __restrict__ ibase,
+                             const int* __restrict__ group_ptr, int S, int chunk, int wmax,
+                             int* __restrict__ ib, int* __restrict__ ie, uint32_t* __restrict__ ikey,
+                             uint32_t* __restrict__ ipay) {
+    const long long s = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (s >= S) return;
+    const int g0 = gbase[s], g1 = gbase[s + 1];
+    int i = ibase[s];
+    for (int gb = g0; gb < g1; gb += chunk, ++i) {
+        const int ge = min(gb + chunk, g1);
+        ib[i] = gb;
+        ie[i] = ge;
+        ikey[i] = (uint32_t)(wmax - (group_ptr[ge] - group_ptr[gb]));
+        ipay[i] = (uint32_t)i;
+    }
+}
+
+__global__ void k_gather_items(const uint32_t* __restrict__ spay, const int* __restrict__ ib,
+                               const int* __restrict__ ie, int I, int* __restrict__ gbeg,
+                               int* __restrict__ gend) {
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= I) return;
+    gbeg[i] = ib[spay[i]];
+    gend[i] = ie[spay[i]];
+}
+
+__global__ void k_scale_values(const float* __restrict__ v, float* __restrict__ out, long long n,
+                               float inv_scale) {
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) out[i] = v[i] * inv_scale;
+}
+
+// ------------------------------------------------------------------------------------------
+// Part 2: execution layout from triples (row, col, value already divided by the scale).
+// ------------------------------------------------------------------------------------------
+template <typename K>
+__global__ void k_panel_keys(const int* __restrict__ trow, const int* __restrict__ tcol,
+                             long long n, int cbits, K* __restrict__ key,
+                             uint32_t* __restrict__ pay) {
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const int r = trow[i];
+    key[i] = ((K)(r >> 4) << (cbits + 4)) | ((K)tcol[i] << 4) | (K)(r & 15);
+    pay[i] = (uint32_t)i;
+}
+
+template <typename K>
+__global__ void k_panel_heads(const K* __restrict__ skey, long long n, int cbits,
+                              int* __restrict__ hdist, int* __restrict__ hpanel,
+                              int* __restrict__ err) {
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const K k = skey[i];
+    int hd = 1, hp = 1;
+    if (i > 0) {
+        const K prev = skey[i - 1];
+        if (prev == k) atomicOr(err, kErrDuplicate);
+        hd = (prev >> 4) != (k >> 4);
+        hp = (prev >> (cbits + 4)) != (k >> (cbits + 4));
+    }
+    hdist[i] = hd;
+    hpanel[i] = hp;
+}
+
+template <typename K>
+__global__ void k_panel_starts(const K* __restrict__ skey, const int* __restrict__ hpanel,
+                               const int* __restrict__ pin, long long n, int cbits,
+                               int* __restrict__ pstart, int* __restrict__ ppanel) {
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    if (hpanel[i]) {
+        const int j = pin[i] - 1;
+        pstart[j] = (int)i;
+        ppanel[j] = (int)(skey[i] >> (cbits + 4));
+    }
+}
+
+__global__ void k_panel_chunks(const int* __restrict__ pstart, const int* __restrict__ dc, int NP,
+                               int* __restrict__ nch) {
+    const long long j = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= NP) return;
+    const int ndist = dc[pstart[j + 1] - 1] - dc[pstart[j]] + 1;
+    nch[j] = (ndist + kChunkCols - 1) / kChunkCols;
+}
+
+template <typename K, bool FP32>
+__global__ void k_panel_entries(const K* __restrict__ skey, const uint32_t* __restrict__ spay,
+                                const int* __restrict__ hdist, const int* __restrict__ dc,
+                                const int* __restrict__ pin, const int* __restrict__ pstart,
+                                const int* __restrict__ cbase, const int* __restrict__ tcol,
+                                const float* __restrict__ tval, long long n,
+                                uint32_t* __restrict__ entries, float* __restrict__ evals,
+                                int* __restrict__ chunk_cols, int* __restrict__ chunk_eptr,
+                                int* __restrict__ pmask) {
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const int j = pin[i] - 1;
+    const int lr = dc[i] - dc[pstart[j]];
+    const int c = cbase[j] + lr / kChunkCols;
+    const int k = lr % kChunkCols;
+    const int r16 = (int)(skey[i] & 15);
+    const uint32_t src = spay[i];
+    const float v = tval[src];
+    if constexpr (FP32) {
+        entries[i] = (uint32_t)r16 | ((uint32_t)k << 4);
+        evals[i] = v;
+    } else {
+        const _Float16 h = (_Float16)v;  // v_cvt_f16_f32, round to nearest even
+        entries[i] = (uint32_t)__builtin_bit_cast(unsigned short, h) | ((uint32_t)r16 << 16) |
+                     ((uint32_t)k << 20);
+    }
+    if (hdist[i]) {
+        chunk_cols[(long long)c * kChunkCols + k] = tcol[src];
+        if (k == 0) chunk_eptr[c] = (int)i;
+    }
+    atomicOr(&pmask[j], 1 << r16);
+}
+
+__global__ void k_units_per_panel(const int* __restrict__ nch, int NP, int umax,
+                                  int* __restrict__ nu) {
+    const long long j = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (j < NP) nu[j] = (nch[j] + umax - 1) / umax;
+}
+
+__global__ void k_make_units(const int* __restrict__ cbase, const int* __restrict__ ubase,
+                             const int* __restrict__ ppanel, const int* __restrict__ pmask, int NP,
+                             int umax, int4* __restrict__ units) {
+    const long long j = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= NP) return;
+    const int c0 = cbase[j], c1 = cbase[j + 1];
+    const int u0 = ubase[j], nu = ubase[j + 1] - u0;
+    const int split = nu > 1 ? (1 << 16) : 0;
+    for (int u = 0; u < nu; ++u) {
+        const int cb = c0 + u * umax;
+        units[u0 + u] = make_int4(ppanel[j] * kPanelRows, cb, min(cb + umax, c1),
+                                  (pmask[j] & 0xffff) | split);
+    }
+}
+
+static inline unsigned blocks(long long n) { return grid_for(n, 256); }
+
+#define LAUNCH(kernel, n, ...)                                                                 \
+    do {                                                                                       \
+        if ((n) > 0) {                                                                         \
+            hipLaunchKernelGGL(kernel, dim3(blocks(n)), dim3(256), 0, st, __VA_ARGS__);        \
+            VCSRMC_HIP(hipGetLastError());                                                     \
+        }                                                                                      \
+    } while (0)
+
+static void check_err(const int* d_err, hipStream_t st) {
+    const int e = read_scalar(d_err, st);
+    if (e & kErrCsr) throw Error(VCSRMC_ERR_CSR, "row_ptr is not a monotone 0..nnz sequence");
+    if (e & kErrRange) throw Error(VCSRMC_ERR_CSR, "column index out of range [0, N)");
+    if (e & kErrUnsorted)
+        throw Error(VCSRMC_ERR_UNSORTED,
+                    "columns of a row are not strictly increasing (unsorted or duplicate "
+                    "coordinates)");
+    if (e & kErrFormat) throw Error(VCSRMC_ERR_FORMAT, "format arrays are inconsistent");
+    if (e & kErrDuplicate)
+        throw Error(VCSRMC_ERR_FORMAT, "format holds the same (row, column) twice");
+}
+
+// Units of at most this many chunks; a panel with more chunks is split over several units.
+static int unit_chunk_limit(long long num_chunks) {
+    (void)num_chunks;
+    return 16;
+}
+
+template <typename K>
+static void build_exec_layout_k(DeviceFormat& F, const int* trow, const int* tcol,
+                                const float* tval, long long n, hipStream_t st) {
+    const int num_panels_all = (F.M + kPanelRows - 1) / kPanelRows;
+    const int cbits = bits_for(F.N > 0 ? (unsigned long long)(F.N - 1) : 0ull);
+    const int pbits = bits_for(num_panels_all > 0 ? (unsigned long long)(num_panels_all - 1) : 0ull);
+    const int kbits = pbits + cbits + 4;
+
+    DevBuf<K> k1(n), k2(n);
+    DevBuf<uint32_t> v1(n), v2(n);
+    LAUNCH((k_panel_keys<K>), n, trow, tcol, n, cbits, k1.p, v1.p);
+    K* kp = k1.p; K* ka = k2.p;
+    uint32_t* vp = v1.p; uint32_t* va = v2.p;
+    radix_sort_pairs<K>(kp, vp, ka, va, n, kbits, st);
+
+    DevBuf<int> hdist(n), hpanel(n), dc(n), pin(n), err(1);
+    VCSRMC_HIP(hipMemsetAsync(err.p, 0, sizeof(int), st));
+    LAUNCH((k_panel_heads<K>), n, kp, n, cbits, hdist.p, hpanel.p, err.p);
+    inclusive_sum<int, int>(hdist.p, dc.p, n, st);
+    inclusive_sum<int, int>(hpanel.p, pin.p, n, st);
+    check_err(err.p, st);
+    const int NP = read_scalar(pin.p + (n - 1), st);
+
+    DevBuf<int> pstart(NP + 1), ppanel(NP), nch(NP), cbase(NP + 1), pmask(NP);
+    LAUNCH((k_panel_starts<K>), n, kp, hpanel.p, pin.p, n, cbits, pstart.p, ppanel.p);
+    fill<int>(pstart.p + NP, 1, (int)n, st);
+    LAUNCH(k_panel_chunks, NP, pstart.p, dc.p, NP, nch.p);
+    exclusive_sum<int, int>(nch.p, cbase.p, NP, st);
+    const int NC = read_scalar(cbase.p + NP, st);
+
+    F.chunk_eptr.alloc(NC + 1);
+    F.chunk_cols.alloc((size_t)NC * kChunkCols);
+    F.entries.alloc(n);
+    if (F.fp32) F.evals.alloc(n);
+    fill<int>(F.chunk_cols.p, (long long)NC * kChunkCols, -1, st);
+    fill<int>(F.chunk_eptr.p + NC, 1, (int)n, st);
+    VCSRMC_HIP(hipMemsetAsync(pmask.p, 0, sizeof(int) * (size_t)NP, st));
+    if (F.fp32)
+        LAUNCH((k_panel_entries<K, true>), n, kp, vp, hdist.p, dc.p, pin.p, pstart.p, cbase.p, tcol,
+               tval, n, F.entries.p, F.evals.p, F.chunk_cols.p, F.chunk_eptr.p, pmask.p);
+    else
+        LAUNCH((k_panel_entries<K, false>), n, kp, vp, hdist.p, dc.p, pin.p, pstart.p, cbase.p,
+               tcol, tval, n, F.entries.p, (float*)nullptr, F.chunk_cols.p, F.chunk_eptr.p,
+               pmask.p);
+
+    const int umax = unit_chunk_limit(NC);
+    DevBuf<int> nu(NP), ubase(NP + 1);
+    LAUNCH(k_units_per_panel, NP, nch.p, NP, umax, nu.p);
+    exclusive_sum<int, int>(nu.p, ubase.p, NP, st);
+    const int NU = read_scalar(ubase.p + NP, st);
+    F.units.alloc(NU);
+    LAUNCH(k_make_units, NP, cbase.p, ubase.p, ppanel.p, pmask.p, NP, umax, F.units.p);
+    VCSRMC_HIP(hipStreamSynchronize(st));
+    F.num_panels = NP;
+    F.num_chunks = NC;
+    F.num_units = NU;
+    F.unit_chunks = umax;
+}
+
+static void build_exec_layout(DeviceFormat& F, const int* trow, const int* tcol, const float* tval,
+                              long long n, hipStream_t st) {
+    F.num_panels = F.num_chunks = F.num_units = 0;
+    if (n == 0) return;
+    const int num_panels_all = (F.M + kPanelRows - 1) / kPanelRows;
+    const int cbits = bits_for(F.N > 0 ? (unsigned long long)(F.N - 1) : 0ull);
+    const int pbits = bits_for(num_panels_all > 0 ? (unsigned long long)(num_panels_all - 1) : 0ull);
+    if (pbits + cbits + 4 <= 32) build_exec_layout_k<uint32_t>(F, trow, tcol, tval, n, st);
+    else build_exec_layout_k<unsigned long long>(F, trow, tcol, tval, n, st);
+}
+
+// ------------------------------------------------------------------------------------------
+// Part 1 driver.
+// ------------------------------------------------------------------------------------------
+template <typename K>
+static void build_groups_k(DeviceFormat& F, const int* d_col, const float* d_val,
+                           const int* row_of, const int* pstart, const int* prow, int P, int S,
+                           float inv_scale, hipStream_t st) {
+    const int segw = F.segw;
+    const int kbits = 6 + bits_for((unsigned long long)(S > 0 ? S - 1 : 0));
+    DevBuf<K> k1(P), k2(P);
+    DevBuf<uint32_t> v1(P), v2(P);
+    DevBuf<int> seg_n(S), seg_start(S + 1), gnum(S), gbase(S + 1);
+    VCSRMC_HIP(hipMemsetAsync(seg_n.p, 0, sizeof(int) * (size_t)S, st));
+    LAUNCH((k_pair_keys<K>), P, pstart, d_col, P, segw, k1.p, v1.p, seg_n.p);
+    K* kp = k1.p; K* ka = k2.p;
+    uint32_t* vp = v1.p; uint32_t* va = v2.p;
+    radix_sort_pairs<K>(kp, vp, ka, va, P, kbits, st);
+    exclusive_sum<int, int>(seg_n.p, seg_start.p, S, st);
+    LAUNCH(k_groups_per_seg, S, seg_n.p, S, gnum.p);
+    exclusive_sum<int, int>(gnum.p, gbase.p, S, st);
+    const int G = read_scalar(gbase.p + S, st);
+
+    DevBuf<int> ghead(G), size16(G);
+    DevBuf<long long> gp64(G + 1);
+    F.group_depth.alloc(G);
+    F.group_seg_base.alloc(G);
+    F.group_rows.alloc((size_t)16 * G);
+    F.group_ptr.alloc(G + 1);
+    LAUNCH((k_group_heads<K>), P, kp, seg_start.p, gbase.p, P, ghead.p);
+    LAUNCH((k_group_info<K>), G, kp, vp, ghead.p, seg_start.p, pstart, prow, G, segw,
+           F.group_depth.p, F.group_seg_base.p, F.group_rows.p, size16.p);
+    exclusive_sum<int, long long>(size16.p, gp64.p, G, st);
+    const long long nval = read_scalar(gp64.p + G, st);
+    if (nval > INT_MAX)
+        throw Error(VCSRMC_ERR_OVERFLOW, "|val| of the format exceeds the int32 group_ptr");
+    LAUNCH(k_to_int, (long long)G + 1, gp64.p, F.group_ptr.p, (long long)G + 1);
+    F.lcol.alloc(nval);
+    F.val.alloc(nval);
+    if (G > 0) {
+        hipLaunchKernelGGL((k_fill_group_entries<K>), dim3(grid_for((long long)G * 64, 256)),
+                           dim3(256), 0, st, kp, vp, ghead.p, seg_start.p, pstart, F.group_ptr.p,
+                           F.group_depth.p, F.group_seg_base.p, d_col, d_val, G, inv_scale,
+                           F.lcol.p, F.val.p);
+        VCSRMC_HIP(hipGetLastError());
+    }
+
+    // Work items (src/vcsr_mc.cu:109-121).
+    const int chunk = std::max(1, std::min(32, G / 4096));
+    DevBuf<int> inum(S), ibase(S + 1);
+    LAUNCH(k_items_per_seg, S, gnum.p, S, chunk, inum.p);
+    exclusive_sum<int, int>(inum.p, ibase.p, S, st);
+    const int I = read_scalar(ibase.p + S, st);
+    const int wmax = chunk * 16 * 64;  // work <= chunk groups x 16 lanes x depth <= 64
+    DevBuf<int> ib(I), ie(I);
+    DevBuf<uint32_t> ik1(I), ik2(I), ip1(I), ip2(I);
+    LAUNCH(k_make_items, S, gbase.p, ibase.p, F.group_ptr.p, S, chunk, wmax, ib.p, ie.p, ik1.p,
+           ip1.p);
+    uint32_t *ikp = ik1.p, *ika = ik2.p, *ipp = ip1.p, *ipa = ip2.p;
+    radix_sort_pairs<uint32_t>(ikp, ipp, ika, ipa, I, bits_for((unsigned long long)wmax), st);
+    F.item_gbeg.alloc(I);
+    F.item_gend.alloc(I);
+    LAUNCH(k_gather_items, I, ipp, ib.p, ie.p, I, F.item_gbeg.p, F.item_gend.p);
+    F.G = G;
+    F.nval = nval;
+    F.nitems = I;
+}
+
+void build_from_csr(DeviceFormat& F, const int* d_row_ptr, const int* d_col, const float* d_val,
+                    int M, int N, int nnz, int segw, int fp32, hipStream_t st) {
+    if (segw != 16 && segw != 32 && segw != 48 && segw != 64)
+        throw Error(VCSRMC_ERR_SEGW, "vcsr_mc supports segw in {16, 32, 48, 64}");
+    if (M < 0 || N < 0 || nnz < 0) throw Error(VCSRMC_ERR_ARG, "negative matrix size");
+    if (!d_row_ptr || (nnz > 0 && (!d_col || !d_val)))
+        throw Error(VCSRMC_ERR_ARG, "null CSR pointer");
+    F.clear();
+    F.M = M;
+    F.N = N;
+    F.segw = segw;
+    F.bundle = 16;
+    F.fp32 = fp32 ? 1 : 0;
+    F.nnz = nnz;
+    const int S = (int)(((long long)N + segw - 1) / segw);
+    F.num_segments = S;
+
+    DevBuf<int> err(1);
+    VCSRMC_HIP(hipMemsetAsync(err.p, 0, sizeof(int), st));
+    LAUNCH(k_check_row_ptr, (long long)M + 1, d_row_ptr, M, nnz, err.p);
+    check_err(err.p, st);
+
+    // Scale (src/vcsr_mc.cu:33-34).
+    F.scale = F.fp32 ? 1.0f : half_scale_from_amax(device_absmax(d_val, nnz, st));
+    const float inv_scale = 1.0f / F.scale;
+
+    if (nnz == 0) {
+        F.group_ptr.alloc(1);
+        VCSRMC_HIP(hipMemsetAsync(F.group_ptr.p, 0, sizeof(int), st));
+        VCSRMC_HIP(hipStreamSynchronize(st));
+        F.ready = true;
+        return;
+    }
+
+    // Row of every nonzero.
+    DevBuf<int> row_of(nnz);
+    {
+        DevBuf<int> head(nnz);
+        fill<int>(head.p, nnz, (int)0x80000000, st);
+        LAUNCH(k_mark_row_heads, M, d_row_ptr, M, head.p);
+        inclusive_max(head.p, row_of.p, nnz, st);
+    }
+    // (segment, row) runs.
+    DevBuf<int> phead(nnz), pidx(nnz + 1);
+    LAUNCH(k_pair_heads, nnz, d_row_ptr, d_col, row_of.p, nnz, N, segw, phead.p, err.p);
+    check_err(err.p, st);
+    exclusive_sum<int, int>(phead.p, pidx.p, nnz, st);
+    const int P = read_scalar(pidx.p + nnz, st);
+    DevBuf<int> pstart(P + 1), prow(P);
+    LAUNCH(k_emit_pairs, nnz, phead.p, pidx.p, row_of.p, nnz, pstart.p, prow.p);
+    fill<int>(pstart.p + P, 1, nnz, st);
+    phead.release();
+    pidx.release();
+
+    if (6 + bits_for((unsigned long long)(S - 1)) <= 32)
+        build_groups_k<uint32_t>(F, d_col, d_val, row_of.p, pstart.p, prow.p, P, S, inv_scale, st);
+    else
+        build_groups_k<unsigned long long>(F, d_col, d_val, row_of.p, pstart.p, prow.p, P, S,
+                                           inv_scale, st);
+    pstart.release();
+    prow.release();
+
+    // Execution layout from (row_of, col, val / scale).
+    DevBuf<float> sval(nnz);
+    LAUNCH(k_scale_values, nnz, d_val, sval.p, (long long)nnz, inv_scale);
+    build_exec_layout(F, row_of.p, d_col, sval.p, nnz, st);
+    VCSRMC_HIP(hipStreamSynchronize(st));
+    F.ready = true;
+}
+
+// ------------------------------------------------------------------------------------------
+// Upload of caller-held arrays.
+// ------------------------------------------------------------------------------------------
+__global__ void k_check_groups(const int* __restrict__ gp, const int* __restrict__ depth,
+                               const int* __restrict__ seg_base, const int* __restrict__ rows,
+                               int G, long long nval, int M, int N, int segw,
+                               int* __restrict__ err) {
+    const long long g = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (g > G) return;
+    bool bad = false;
+    if (g == 0) bad |= gp[0] != 0;
+    if (g == G) {
+        bad |= (long long)gp[G] != nval;
+    } else {
+        const int d = depth[g];
+        bad |= d < 0 || (long long)gp[g + 1] - gp[g] != 16LL * d;
+        const int sb = seg_base[g];
+        bad |= sb < 0 || sb >= N || sb % segw != 0;
+        for (int l = 0; l < 16; ++l) {
+            const int r = rows[16 * g + l];
+            bad |= r < -1 || r >= M;
+        }
+    }
+    if (bad) atomicOr(err, kErrFormat);
+}
+
+__global__ void k_expand_flags(const int* __restrict__ gp, const int* __restrict__ seg_base,
+                               const int* __restrict__ rows, const int* __restrict__ lcol, int G,
+                               long long nval, int N, int segw, int* __restrict__ flag,
+                               int* __restrict__ err) {
+    const long long t = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= nval) return;
+    // group of slot t: last g with gp[g] <= t
+    int lo = 0, hi = G;  // gp[lo] <= t < gp[hi]
+    while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if ((long long)gp[mid] <= t) lo = mid; else hi = mid;
+    }
+    const int lane = (int)((t - gp[lo]) & 15);
+    const int lc = lcol[t];
+    int f = 0;
+    if (lc >= 0) {
+        const int r = rows[16 * lo + lane];
+        const long long c = (long long)seg_base[lo] + lc;
+        if (lc >= segw || r < 0 || c >= N) atomicOr(err, kErrFormat);
+        else f = 1;
+    } else if (lc != -1) {
+        atomicOr(err, kErrFormat);
+    }
+    flag[t] = f;
+}
+
+__global__ void k_expand_write(const int* __restrict__ gp, const int* __restrict__ seg_base,
+                               const int* __restrict__ rows, const int* __restrict__ lcol,
+                               const float* __restrict__ val, const int* __restrict__ flag,
+                               const int* __restrict__ pos, int G, long long nval,
+                               int* __restrict__ trow, int* __restrict__ tcol,
+                               float* __restrict__ tval) {
+    const long long t = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= nval || !flag[t]) return;
+    int lo = 0, hi = G;
+    while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if ((long long)gp[mid] <= t) lo = mid; else hi = mid;
+    }
+    const int lane = (int)((t - gp[lo]) & 15);
+    const int i = pos[t];
+    trow[i] = rows[16 * lo + lane];
+    tcol[i] = seg_base[lo] + lcol[t];
+    tval[i] = val[t];
+}
+
+template <typename T>
+static void upload_array(DevBuf<T>& d, const T* h, long long n, hipStream_t st) {
+    d.alloc(n > 0 ? n : 0);
+    if (n > 0) {
+        if (!h) throw Error(VCSRMC_ERR_ARG, "null format array");
+        VCSRMC_HIP(hipMemcpyAsync(d.p, h, sizeof(T) * (size_t)n, hipMemcpyHostToDevice, st));
+    }
+}
+
+void build_from_host(DeviceFormat& F, const HostArrays& H, hipStream_t st) {
+    if (H.segw != 16 && H.segw != 32 && H.segw != 48 && H.segw != 64)
+        throw Error(VCSRMC_ERR_SEGW, "vcsr_mc supports segw in {16, 32, 48, 64}");
+    if (H.M < 0 || H.N < 0 || H.G < 0 || H.nval < 0 || H.nitems < 0 || H.nval > INT_MAX)
+        throw Error(VCSRMC_ERR_ARG, "negative or oversized format size");
+    if (H.bundle != 16) throw Error(VCSRMC_ERR_FORMAT, "bundle must be 16");
+    if (H.nval != 16LL * (H.nval / 16)) throw Error(VCSRMC_ERR_FORMAT, "|val| is not 16 * depth");
+    F.clear();
+    F.M = H.M; F.N = H.N; F.segw = H.segw; F.bundle = H.bundle; F.num_segments = H.num_segments;
+    F.G = H.G; F.nval = H.nval; F.nitems = H.nitems; F.scale = H.scale; F.fp32 = H.fp32 ? 1 : 0;
+    upload_array(F.group_ptr, H.group_ptr, (long long)H.G + 1, st);
+    upload_array(F.group_depth, H.group_depth, H.G, st);
+    upload_array(F.group_seg_base, H.group_seg_base, H.G, st);
+    upload_array(F.group_rows, H.group_rows, 16LL * H.G, st);
+    upload_array(F.lcol, H.lcol, H.nval, st);
+    upload_array(F.val, H.val, H.nval, st);
+    upload_array(F.item_gbeg, H.item_gbeg, H.nitems, st);
+    upload_array(F.item_gend, H.item_gend, H.nitems, st);
+
+    DevBuf<int> err(1);
+    VCSRMC_HIP(hipMemsetAsync(err.p, 0, sizeof(int), st));
+    LAUNCH(k_check_groups, (long long)H.G + 1, F.group_ptr.p, F.group_depth.p,
+           F.group_seg_base.p, F.group_rows.p, H.G, H.nval, H.M, H.N, H.segw, err.p);
+    check_err(err.p, st);
+
+    const long long nval = H.nval;
+    DevBuf<int> flag(nval), pos(nval + 1);
+    LAUNCH(k_expand_flags, nval, F.group_ptr.p, F.group_seg_base.p, F.group_rows.p, F.lcol.p,
+           H.G, nval, H.N, H.segw, flag.p, err.p);
+    check_err(err.p, st);
+    exclusive_sum<int, int>(flag.p, pos.p, nval, st);
+    const int n = nval ? read_scalar(pos.p + nval, st) : 0;
+    F.nnz = n;
+    DevBuf<int> trow(n), tcol(n);
+    DevBuf<float> tval(n);
+    LAUNCH(k_expand_write, nval, F.group_ptr.p, F.group_seg_base.p, F.group_rows.p, F.lcol.p,
+           F.val.p, flag.p, pos.p, H.G, nval, trow.p, tcol.p, tval.p);
+    build_exec_layout(F, trow.p, tcol.p, tval.p, n, st);
+    VCSRMC_HIP(hipStreamSynchronize(st));
+    F.ready = true;
+}
+
+}  // namespace vcsrmc

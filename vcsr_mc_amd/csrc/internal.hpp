@@ -1,0 +1,77 @@
+// internal.hpp -- the device-resident VCSR-MC format and the functions that build and run it.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "primitives.hpp"
+
+namespace vcsrmc {
+
+// Chunk width of the execution layout: one MFMA K block (v_mfma_f32_16x16x32_f16), or eight
+// K steps of v_mfma_f32_16x16x4_f32.
+constexpr int kChunkCols = 32;
+// Rows per panel = MFMA M.
+constexpr int kPanelRows = 16;
+
+// A format on one device.
+//
+// Boundary arrays (the reference's VCSRMC, include/vcsr_formats.hpp:14-21, built or uploaded
+// bit for bit): group_ptr, group_depth, group_seg_base, group_rows, lcol, val, item_gbeg,
+// item_gend.
+//
+// Execution layout (what the multiply kernels read), derived from the same matrix:
+//   units[u]        = {row0, chunk_begin, chunk_end, rowmask | split << 16}
+//                     a run of chunks of one 16-row panel; split = the panel has several
+//                     units, whose partial sums meet in C through atomics
+//   chunk_eptr[c]   = first entry of chunk c (chunk_eptr[num_chunks] = nnz)
+//   chunk_cols[32c+k] = column of the chunk's k-th distinct column, -1 past the end
+//   entries[e]      FP16 format: f16 value | row-in-panel << 16 | k << 20
+//                   FP32 format: row-in-panel | k << 4, with the value in evals[e]
+struct DeviceFormat {
+    int M = 0, N = 0, segw = 16, bundle = 16, num_segments = 0;
+    int G = 0, nitems = 0;
+    long long nval = 0, nnz = 0;
+    float scale = 1.0f;
+    int fp32 = 0;
+
+    DevBuf<int> group_ptr, group_depth, group_seg_base, group_rows, lcol, item_gbeg, item_gend;
+    DevBuf<float> val;
+
+    int num_panels = 0, num_chunks = 0, num_units = 0, unit_chunks = 0;
+    DevBuf<int4> units;
+    DevBuf<int> chunk_eptr, chunk_cols;
+    DevBuf<uint32_t> entries;
+    DevBuf<float> evals;
+
+    bool ready = false;
+    void clear() { *this = DeviceFormat(); }
+};
+
+// FP16 range scale from the largest finite |value| (src/vcsr_mc.cu:14-22 as the reference
+// binary evaluates it; see half_scale_from_amax).
+float half_scale_from_amax(float amax);
+float device_absmax(const float* d_val, long long n, hipStream_t st);
+
+// GPU format pipeline from a device CSR (src/vcsr_mc.cu:25-123).
+void build_from_csr(DeviceFormat& F, const int* d_row_ptr, const int* d_col, const float* d_val,
+                    int M, int N, int nnz, int segw, int fp32, hipStream_t st);
+
+// Format arrays given by the caller (host pointers, src/vcsr_mc.cu:332-349), validated on
+// the device, then the execution layout is derived from them.
+struct HostArrays {
+    int M, N, segw, bundle, num_segments, G, nitems;
+    long long nval;
+    const int *group_ptr, *group_depth, *group_seg_base, *group_rows, *lcol;
+    const float* val;
+    const int *item_gbeg, *item_gend;
+    float scale;
+    int fp32;
+};
+void build_from_host(DeviceFormat& F, const HostArrays& H, hipStream_t st);
+
+// C += A.B (src/vcsr_mc.cu:352-394 semantics).  b_f16: B is binary16 in HBM.
+void spmm_launch(const DeviceFormat& F, const void* dB, bool b_f16, int O, int tileK, float* dC,
+                 hipStream_t st);
+
+}  // namespace vcsrmc
