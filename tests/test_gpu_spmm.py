@@ -81,7 +81,10 @@ def test_fp16_b_matches_fp32_b(orc):
     say("fp16 B")
     C1, _ = run_spmm(rp, c, v, 300, 400, B, False)
     C2, _ = run_spmm(rp, c, v, 300, 400, B, False, b16=True)
-    assert C1.tobytes() == C2.tobytes()
+    # identical operands; only the order of the atomic merge of split panels may differ
+    _, L1 = orc.spmm_csr(rp, c, v, 300, B, mode=1)
+    ok, worst, _ = row_l1_parity(C1, C2.astype(np.float64), L1, 1e-6)
+    assert ok, worst
     check(orc, rp, c, v, 300, 400, B, False, b16=True)
 
 
@@ -116,7 +119,9 @@ def test_upload_path_matches_build_path(orc):
     say("upload path")
     C1, _ = run_spmm(rp, c, v, 500, 500, B, False, segw=16)
     C2, _ = run_spmm(rp, c, v, 500, 500, B, False, upload=V)
-    assert C1.tobytes() == C2.tobytes()
+    _, L1 = orc.spmm_csr(rp, c, v, 500, B, mode=1)
+    ok, worst, _ = row_l1_parity(C1, C2.astype(np.float64), L1, 1e-6)
+    assert ok, worst
 
 
 def test_empty_matrix():

@@ -377,7 +377,10 @@ static void check_err(const int* d_err, hipStream_t st) {
         throw Error(VCSRMC_ERR_FORMAT, "format holds the same (row, column) twice");
 }
 
-// Units of at most this many chunks; a panel with more chunks is split over several units.
+// Tiles per unit.  The multiply kernel spreads a unit's tiles over the waves of one
+// work-group and merges them in LDS, so only panels with more tiles than this are split over
+// several units (merged in C with device-scope atomics, which on MI355X resolve past the
+// per-XCD L2 and are expensive).
 static int unit_chunk_limit(long long num_chunks) {
     (void)num_chunks;
     return 16;

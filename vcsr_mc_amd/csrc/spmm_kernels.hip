@@ -39,122 +39,99 @@ __device__ __forceinline__ int unit_of_block(int bid, int num_units) {
     return (bid & 7) * per + (bid >> 3);
 }
 
+// Raw B values of the 8 tile rows a lane feeds into the MFMA B operand (kept in the storage
+// type until use, so a prefetched load is never waited for early by a conversion).
+template <int VEC, typename TB>
+struct BRows {
+    TB v[8][VEC];
+};
+
 template <int VEC, typename TB, bool ALIGNED>
-__device__ __forceinline__ void load_b_row(const TB* __restrict__ B, int col, long long O, int c0,
-                                           _Float16 (&out)[VEC]) {
-    if (col < 0) {
+__device__ __forceinline__ void load_b_rows(const TB* __restrict__ B, const int (&cols)[8],
+                                            long long O, int c0, BRows<VEC, TB>& R) {
 #pragma unroll
-        for (int q = 0; q < VEC; ++q) out[q] = (_Float16)0.0f;
-        return;
-    }
-    const TB* src = B + (long long)col * O + c0;
-    if constexpr (ALIGNED) {
-        if (c0 < O) {
-            if constexpr (sizeof(TB) == 2) {
-                if constexpr (VEC == 1) {
-                    out[0] = src[0];
-                } else if constexpr (VEC == 8) {
-                    const half8 v = *reinterpret_cast<const half8*>(src);
+    for (int i = 0; i < 8; ++i) {
+        const int col = cols[i];
+        const TB* src = B + (long long)(col < 0 ? 0 : col) * O + c0;
+        if constexpr (ALIGNED) {
+            const bool ok = col >= 0 && c0 < O;
+            if constexpr (sizeof(TB) == 2 && VEC >= 2) {
+                typedef _Float16 hv __attribute__((ext_vector_type(VEC)));
+                hv x = {};
+                if (ok) x = *reinterpret_cast<const hv*>(src);
 #pragma unroll
-                    for (int q = 0; q < 8; ++q) out[q] = v[q];
-                } else {
-                    typedef _Float16 hv __attribute__((ext_vector_type(VEC)));
-                    const hv v = *reinterpret_cast<const hv*>(src);
+                for (int q = 0; q < VEC; ++q) R.v[i][q] = x[q];
+            } else if constexpr (sizeof(TB) == 4 && VEC >= 4) {
 #pragma unroll
-                    for (int q = 0; q < VEC; ++q) out[q] = v[q];
+                for (int h = 0; h < VEC; h += 4) {
+                    floatx4 x = {0.f, 0.f, 0.f, 0.f};
+                    if (ok) x = *reinterpret_cast<const floatx4*>(src + h);
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) R.v[i][h + q] = x[q];
                 }
             } else {
-                if constexpr (VEC >= 4) {
 #pragma unroll
-                    for (int h = 0; h < VEC; h += 4) {
-                        const floatx4 v = *reinterpret_cast<const floatx4*>(src + h);
-#pragma unroll
-                        for (int q = 0; q < 4; ++q) out[h + q] = (_Float16)v[q];
-                    }
-                } else {
-#pragma unroll
-                    for (int q = 0; q < VEC; ++q) out[q] = (_Float16)src[q];
-                }
+                for (int q = 0; q < VEC; ++q) R.v[i][q] = ok ? src[q] : (TB)0;
             }
         } else {
 #pragma unroll
-            for (int q = 0; q < VEC; ++q) out[q] = (_Float16)0.0f;
+            for (int q = 0; q < VEC; ++q) R.v[i][q] = (col >= 0 && c0 + q < O) ? src[q] : (TB)0;
         }
-    } else {
-#pragma unroll
-        for (int q = 0; q < VEC; ++q) out[q] = (c0 + q < O) ? (_Float16)src[q] : (_Float16)0.0f;
     }
 }
 
-template <int TK, typename TB, bool ALIGNED>
-__global__ __launch_bounds__(64) void k_spmm_f16(const int4* __restrict__ units, int num_units,
-                                                 const int* __restrict__ chunk_eptr,
-                                                 const int* __restrict__ chunk_cols,
-                                                 const uint32_t* __restrict__ entries,
-                                                 const TB* __restrict__ B, int O, float scale,
-                                                 float* __restrict__ C) {
+__device__ __forceinline__ void load_cols8(const int* __restrict__ chunk_cols, int c, int g,
+                                           int (&cols)[8]) {
+    const int4 lo = *reinterpret_cast<const int4*>(chunk_cols + (long long)c * kChunkCols + 8 * g);
+    const int4 hi = *reinterpret_cast<const int4*>(chunk_cols + (long long)c * kChunkCols + 8 * g + 4);
+    cols[0] = lo.x; cols[1] = lo.y; cols[2] = lo.z; cols[3] = lo.w;
+    cols[4] = hi.x; cols[5] = hi.y; cols[6] = hi.z; cols[7] = hi.w;
+}
+
+__device__ __forceinline__ void scatter_a_f16(_Float16* As, uint32_t w) {
+    As[((w >> 16) & 15) * kApitch + ((w >> 20) & 31)] =
+        __builtin_bit_cast(_Float16, (unsigned short)(w & 0xffffu));
+}
+
+// Orders the LDS traffic of one wave (its private A tile): LDS instructions of a wave execute
+// in issue order, so a wavefront-scope fence (no instruction, a compiler barrier) is enough.
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Adds the unit's 16 x TK result into C.  W == 1: straight from the accumulators (lane (n, g)
+// owns rows 4g..4g+3, columns k0 + VEC n .. + VEC - 1).  W > 1: every wave parks its partial
+// tile in LDS, then the work-group sums the W partials and writes each row with consecutive
+// threads on consecutive columns.  Split panels merge through atomics; other rows are a
+// read-modify-write (C += A.B).  Rows outside the panel's row mask are never touched.
+template <int TK, int W>
+__device__ __forceinline__ void merge_into_c(const floatx4 (&acc)[TK / 16], float scale,
+                                             const int4& U, int k0, int O, bool c4,
+                                             float* __restrict__ C, float* P) {
     constexpr int VEC = TK / 16;
-    __shared__ __attribute__((aligned(16))) _Float16 As[16 * kApitch];
-    const int lane = threadIdx.x, n = lane & 15, g = lane >> 4;
-    const int u = unit_of_block(blockIdx.x, num_units);
-    if (u >= num_units) return;
-    const int4 U = units[u];
-    const int k0 = blockIdx.y * TK;
-    const int c0 = k0 + VEC * n;
-    const long long OL = O;
-
-    floatx4 acc[VEC];
-#pragma unroll
-    for (int q = 0; q < VEC; ++q) acc[q] = floatx4{0.f, 0.f, 0.f, 0.f};
-
-    _Float16* my_a = &As[n * kApitch + 8 * g];
-    for (int c = U.y; c < U.z; ++c) {
-        const int4 cl = *reinterpret_cast<const int4*>(chunk_cols + (long long)c * kChunkCols + 8 * g);
-        const int4 ch = *reinterpret_cast<const int4*>(chunk_cols + (long long)c * kChunkCols + 8 * g + 4);
-        const int cols[8] = {cl.x, cl.y, cl.z, cl.w, ch.x, ch.y, ch.z, ch.w};
-        _Float16 R[8][VEC];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) load_b_row<VEC, TB, ALIGNED>(B, cols[i], OL, c0, R[i]);
-
-        const int eb = chunk_eptr[c], ee = chunk_eptr[c + 1];
-        *reinterpret_cast<half8*>(my_a) = half8{0, 0, 0, 0, 0, 0, 0, 0};
-        __syncthreads();
-        for (int e = eb + lane; e < ee; e += 64) {
-            const uint32_t w = entries[e];
-            As[((w >> 16) & 15) * kApitch + ((w >> 20) & 31)] =
-                __builtin_bit_cast(_Float16, (unsigned short)(w & 0xffffu));
-        }
-        __syncthreads();
-        const half8 a = *reinterpret_cast<const half8*>(my_a);
-        __syncthreads();
-#pragma unroll
-        for (int q = 0; q < VEC; ++q) {
-            const half8 b = half8{R[0][q], R[1][q], R[2][q], R[3][q],
-                                  R[4][q], R[5][q], R[6][q], R[7][q]};
-            acc[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc[q], 0, 0, 0);
-        }
-    }
-
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, n = lane & 15, g = lane >> 4;
     const bool split = (U.w >> 16) & 1;
+    const long long OL = O;
+    if constexpr (W == 1) {
+        const int c0 = k0 + VEC * n;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int rl = 4 * g + i;
-        if (!((U.w >> rl) & 1)) continue;
-        float* crow = C + (long long)(U.x + rl) * OL + c0;
-        if (split) {
+        for (int i = 0; i < 4; ++i) {
+            const int rl = 4 * g + i;
+            if (!((U.w >> rl) & 1)) continue;
+            float* crow = C + (long long)(U.x + rl) * OL + c0;
+            if (split) {
 #pragma unroll
-            for (int q = 0; q < VEC; ++q)
-                if (c0 + q < O) atomicAdd(crow + q, acc[q][i] * scale);
-        } else {
-            if constexpr (ALIGNED && VEC >= 4) {
-                if (c0 < O) {
+                for (int q = 0; q < VEC; ++q)
+                    if (c0 + q < O) atomicAdd(crow + q, acc[q][i] * scale);
+            } else if (VEC >= 4 && c4 && c0 + VEC <= O) {
 #pragma unroll
-                    for (int h = 0; h < VEC; h += 4) {
-                        floatx4 v = *reinterpret_cast<floatx4*>(crow + h);
+                for (int h = 0; h < VEC; h += 4) {
+                    floatx4 v = *reinterpret_cast<floatx4*>(crow + h);
 #pragma unroll
-                        for (int q = 0; q < 4; ++q) v[q] += acc[h + q][i] * scale;
-                        *reinterpret_cast<floatx4*>(crow + h) = v;
-                    }
+                    for (int q = 0; q < 4; ++q) v[q] += acc[(h + q) % VEC][i] * scale;
+                    *reinterpret_cast<floatx4*>(crow + h) = v;
                 }
             } else {
 #pragma unroll
@@ -162,49 +139,56 @@ __global__ __launch_bounds__(64) void k_spmm_f16(const int4* __restrict__ units,
                     if (c0 + q < O) crow[q] += acc[q][i] * scale;
             }
         }
-    }
-}
-
-template <int VEC, bool ALIGNED>
-__device__ __forceinline__ void load_b_row_f32(const float* __restrict__ B, int col, long long O,
-                                               int c0, float (&out)[VEC]) {
-    if (col < 0) {
-#pragma unroll
-        for (int q = 0; q < VEC; ++q) out[q] = 0.0f;
-        return;
-    }
-    const float* src = B + (long long)col * O + c0;
-    if constexpr (ALIGNED && VEC >= 4) {
-        if (c0 < O) {
-#pragma unroll
-            for (int h = 0; h < VEC; h += 4) {
-                const floatx4 v = *reinterpret_cast<const floatx4*>(src + h);
-#pragma unroll
-                for (int q = 0; q < 4; ++q) out[h + q] = v[q];
-            }
-        } else {
-#pragma unroll
-            for (int q = 0; q < VEC; ++q) out[q] = 0.0f;
-        }
     } else {
+        float* Pw = P + wave * 16 * TK;
 #pragma unroll
-        for (int q = 0; q < VEC; ++q) out[q] = (c0 + q < O) ? src[q] : 0.0f;
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int q = 0; q < VEC; ++q) Pw[(4 * g + i) * TK + VEC * n + q] = acc[q][i];
+        __syncthreads();
+        for (int e = threadIdx.x * 4; e < 16 * TK; e += 64 * W * 4) {
+            const int row = e / TK, col = e % TK;
+            if (!((U.w >> row) & 1)) continue;
+            floatx4 sum = *reinterpret_cast<const floatx4*>(P + e);
+#pragma unroll
+            for (int w = 1; w < W; ++w) {
+                const floatx4 x = *reinterpret_cast<const floatx4*>(P + w * 16 * TK + e);
+                sum += x;
+            }
+            const int cc = k0 + col;
+            if (cc >= O) continue;
+            float* crow = C + (long long)(U.x + row) * OL + cc;
+            if (split) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    if (cc + j < O) atomicAdd(crow + j, sum[j] * scale);
+            } else if (c4 && cc + 4 <= O) {
+                floatx4 v = *reinterpret_cast<floatx4*>(crow);
+                v += sum * scale;
+                *reinterpret_cast<floatx4*>(crow) = v;
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    if (cc + j < O) crow[j] += sum[j] * scale;
+            }
+        }
     }
 }
 
-// FP32 format: A tile stored K-step-major so a lane's 8 K values (k = 4s + g, s = 0..7) are
-// contiguous: At[(k & 3) * 128 + row * 8 + (k >> 2)].
-template <int TK, bool ALIGNED>
-__global__ __launch_bounds__(64) void k_spmm_f32(const int4* __restrict__ units, int num_units,
-                                                 const int* __restrict__ chunk_eptr,
-                                                 const int* __restrict__ chunk_cols,
-                                                 const uint32_t* __restrict__ entries,
-                                                 const float* __restrict__ evals,
-                                                 const float* __restrict__ B, int O,
-                                                 float* __restrict__ C) {
+// FP16 format.  W waves per work-group share one unit: wave w takes tiles U.y + w, +W, ...
+// Each wave pipelines its tiles: while tile c is multiplied, the B rows and the first 128
+// nonzeros of its next tile and the column indices of the tile after are in flight.
+template <int TK, typename TB, bool ALIGNED, int W>
+__global__ __launch_bounds__(64 * W) void k_spmm_f16(const int4* __restrict__ units, int num_units,
+                                                     const int* __restrict__ chunk_eptr,
+                                                     const int* __restrict__ chunk_cols,
+                                                     const uint32_t* __restrict__ entries,
+                                                     const TB* __restrict__ B, int O, float scale,
+                                                     bool c4, float* __restrict__ C) {
     constexpr int VEC = TK / 16;
-    __shared__ __attribute__((aligned(16))) float At[4 * 16 * 8];
-    const int lane = threadIdx.x, n = lane & 15, g = lane >> 4;
+    __shared__ __attribute__((aligned(16))) _Float16 As[W][16 * kApitch];
+    __shared__ __attribute__((aligned(16))) float P[W > 1 ? W * 16 * TK : 4];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
     const int u = unit_of_block(blockIdx.x, num_units);
     if (u >= num_units) return;
     const int4 U = units[u];
@@ -215,108 +199,235 @@ __global__ __launch_bounds__(64) void k_spmm_f32(const int4* __restrict__ units,
     floatx4 acc[VEC];
 #pragma unroll
     for (int q = 0; q < VEC; ++q) acc[q] = floatx4{0.f, 0.f, 0.f, 0.f};
+    _Float16* Aw = As[wave];
+    _Float16* my_a = &Aw[n * kApitch + 8 * g];
 
-    float* my_a = &At[g * 128 + n * 8];
-    for (int c = U.y; c < U.z; ++c) {
-        const int* cc = chunk_cols + (long long)c * kChunkCols;
-        int cols[8];
-#pragma unroll
-        for (int s = 0; s < 8; ++s) cols[s] = cc[4 * s + g];
-        float R[8][VEC];
-#pragma unroll
-        for (int s = 0; s < 8; ++s) load_b_row_f32<VEC, ALIGNED>(B, cols[s], OL, c0, R[s]);
-
-        const int eb = chunk_eptr[c], ee = chunk_eptr[c + 1];
-        *reinterpret_cast<floatx4*>(my_a) = floatx4{0.f, 0.f, 0.f, 0.f};
-        *reinterpret_cast<floatx4*>(my_a + 4) = floatx4{0.f, 0.f, 0.f, 0.f};
-        __syncthreads();
-        for (int e = eb + lane; e < ee; e += 64) {
-            const uint32_t w = entries[e];
-            const int r = w & 15, k = (w >> 4) & 31;
-            At[(k & 3) * 128 + r * 8 + (k >> 2)] = evals[e];
+    int c = U.y + wave;
+    if (c < U.z) {
+        int cols_next[8];
+        BRows<VEC, TB> R;
+        {
+            int cols[8];
+            load_cols8(chunk_cols, c, g, cols);
+            load_b_rows<VEC, TB, ALIGNED>(B, cols, OL, c0, R);
         }
-        __syncthreads();
-        const floatx4 a_lo = *reinterpret_cast<const floatx4*>(my_a);
-        const floatx4 a_hi = *reinterpret_cast<const floatx4*>(my_a + 4);
-        __syncthreads();
-        const float a[8] = {a_lo[0], a_lo[1], a_lo[2], a_lo[3], a_hi[0], a_hi[1], a_hi[2], a_hi[3]};
-#pragma unroll
-        for (int s = 0; s < 8; ++s) {
-            if (__ballot(cols[s] >= 0) == 0) break;  // padding columns sit at the end of a tile
-#pragma unroll
-            for (int q = 0; q < VEC; ++q)
-                acc[q] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s], R[s][q], acc[q], 0, 0, 0);
-        }
-    }
+        if (c + W < U.z) load_cols8(chunk_cols, c + W, g, cols_next);
+        int eb = chunk_eptr[c], ee = chunk_eptr[c + 1];
+        uint32_t w0 = 0, w1 = 0;
+        if (eb + lane < ee) w0 = entries[eb + lane];
+        if (eb + 64 + lane < ee) w1 = entries[eb + 64 + lane];
 
-    const bool split = (U.w >> 16) & 1;
+        for (; c < U.z; c += W) {
+            const bool has1 = c + W < U.z;
+            BRows<VEC, TB> Rn;
+            int eb1 = 0, ee1 = 0;
+            uint32_t n0 = 0, n1 = 0;
+            int cols_after[8];
+            if (has1) {
+                load_b_rows<VEC, TB, ALIGNED>(B, cols_next, OL, c0, Rn);
+                eb1 = chunk_eptr[c + W];
+                ee1 = chunk_eptr[c + W + 1];
+                if (eb1 + lane < ee1) n0 = entries[eb1 + lane];
+                if (eb1 + 64 + lane < ee1) n1 = entries[eb1 + 64 + lane];
+                if (c + 2 * W < U.z) load_cols8(chunk_cols, c + 2 * W, g, cols_after);
+            }
+            *reinterpret_cast<half8*>(my_a) = half8{0, 0, 0, 0, 0, 0, 0, 0};
+            wave_lds_sync();
+            if (eb + lane < ee) scatter_a_f16(Aw, w0);
+            if (eb + 64 + lane < ee) scatter_a_f16(Aw, w1);
+            for (int e = eb + 128 + lane; e < ee; e += 64) scatter_a_f16(Aw, entries[e]);
+            wave_lds_sync();
+            const half8 a = *reinterpret_cast<const half8*>(my_a);
+            wave_lds_sync();
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int rl = 4 * g + i;
-        if (!((U.w >> rl) & 1)) continue;
-        float* crow = C + (long long)(U.x + rl) * OL + c0;
-        if (split) {
+            for (int q = 0; q < VEC; ++q) {
+                const half8 b = half8{(_Float16)R.v[0][q], (_Float16)R.v[1][q],
+                                      (_Float16)R.v[2][q], (_Float16)R.v[3][q],
+                                      (_Float16)R.v[4][q], (_Float16)R.v[5][q],
+                                      (_Float16)R.v[6][q], (_Float16)R.v[7][q]};
+                acc[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc[q], 0, 0, 0);
+            }
+            if (has1) {
+                R = Rn;
 #pragma unroll
-            for (int q = 0; q < VEC; ++q)
-                if (c0 + q < O) atomicAdd(crow + q, acc[q][i]);
-        } else {
-            if constexpr (ALIGNED && VEC >= 4) {
-                if (c0 < O) {
-#pragma unroll
-                    for (int h = 0; h < VEC; h += 4) {
-                        floatx4 v = *reinterpret_cast<floatx4*>(crow + h);
-#pragma unroll
-                        for (int q = 0; q < 4; ++q) v[q] += acc[h + q][i];
-                        *reinterpret_cast<floatx4*>(crow + h) = v;
-                    }
-                }
-            } else {
-#pragma unroll
-                for (int q = 0; q < VEC; ++q)
-                    if (c0 + q < O) crow[q] += acc[q][i];
+                for (int i = 0; i < 8; ++i) cols_next[i] = cols_after[i];
+                w0 = n0; w1 = n1;
+                eb = eb1; ee = ee1;
             }
         }
     }
+    merge_into_c<TK, W>(acc, scale, U, k0, O, c4, C, P);
+}
+
+// FP32 format: eight K steps of v_mfma_f32_16x16x4_f32 per tile.  The A tile is stored
+// K-step-major so a lane's 8 values (k = 4s + g, s = 0..7) are contiguous:
+// At[(k & 3) * 128 + row * 8 + (k >> 2)].
+template <int VEC>
+struct FRows {
+    float v[8][VEC];
+};
+
+template <int VEC, bool ALIGNED>
+__device__ __forceinline__ void load_b_rows_f32(const float* __restrict__ B, const int (&cols)[8],
+                                                long long O, int c0, FRows<VEC>& R) {
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+        const int col = cols[s];
+        const float* src = B + (long long)(col < 0 ? 0 : col) * O + c0;
+        if constexpr (ALIGNED && VEC >= 4) {
+            const bool ok = col >= 0 && c0 < O;
+#pragma unroll
+            for (int h = 0; h < VEC; h += 4) {
+                floatx4 x = {0.f, 0.f, 0.f, 0.f};
+                if (ok) x = *reinterpret_cast<const floatx4*>(src + h);
+#pragma unroll
+                for (int q = 0; q < 4; ++q) R.v[s][h + q] = x[q];
+            }
+        } else {
+#pragma unroll
+            for (int q = 0; q < VEC; ++q) R.v[s][q] = (col >= 0 && c0 + q < O) ? src[q] : 0.0f;
+        }
+    }
+}
+
+__device__ __forceinline__ void load_cols_steps(const int* __restrict__ chunk_cols, int c, int g,
+                                                int (&cols)[8]) {
+    const int* cc = chunk_cols + (long long)c * kChunkCols;
+#pragma unroll
+    for (int s = 0; s < 8; ++s) cols[s] = cc[4 * s + g];
+}
+
+template <int TK, bool ALIGNED, int W>
+__global__ __launch_bounds__(64 * W) void k_spmm_f32(const int4* __restrict__ units, int num_units,
+                                                     const int* __restrict__ chunk_eptr,
+                                                     const int* __restrict__ chunk_cols,
+                                                     const uint32_t* __restrict__ entries,
+                                                     const float* __restrict__ evals,
+                                                     const float* __restrict__ B, int O, bool c4,
+                                                     float* __restrict__ C) {
+    constexpr int VEC = TK / 16;
+    __shared__ __attribute__((aligned(16))) float At[W][4 * 16 * 8];
+    __shared__ __attribute__((aligned(16))) float P[W > 1 ? W * 16 * TK : 4];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
+    const int u = unit_of_block(blockIdx.x, num_units);
+    if (u >= num_units) return;
+    const int4 U = units[u];
+    const int k0 = blockIdx.y * TK;
+    const int c0 = k0 + VEC * n;
+    const long long OL = O;
+
+    floatx4 acc[VEC];
+#pragma unroll
+    for (int q = 0; q < VEC; ++q) acc[q] = floatx4{0.f, 0.f, 0.f, 0.f};
+    float* Aw = At[wave];
+    float* my_a = &Aw[g * 128 + n * 8];
+
+    int c = U.y + wave;
+    if (c < U.z) {
+        int cols[8], cols_next[8];
+        FRows<VEC> R;
+        load_cols_steps(chunk_cols, c, g, cols);
+        load_b_rows_f32<VEC, ALIGNED>(B, cols, OL, c0, R);
+        if (c + W < U.z) load_cols_steps(chunk_cols, c + W, g, cols_next);
+        for (; c < U.z; c += W) {
+            const bool has1 = c + W < U.z;
+            FRows<VEC> Rn;
+            int cols_after[8];
+            if (has1) {
+                load_b_rows_f32<VEC, ALIGNED>(B, cols_next, OL, c0, Rn);
+                if (c + 2 * W < U.z) load_cols_steps(chunk_cols, c + 2 * W, g, cols_after);
+            }
+            const int eb = chunk_eptr[c], ee = chunk_eptr[c + 1];
+            *reinterpret_cast<floatx4*>(my_a) = floatx4{0.f, 0.f, 0.f, 0.f};
+            *reinterpret_cast<floatx4*>(my_a + 4) = floatx4{0.f, 0.f, 0.f, 0.f};
+            wave_lds_sync();
+            for (int e = eb + lane; e < ee; e += 64) {
+                const uint32_t w = entries[e];
+                const int r = w & 15, k = (w >> 4) & 31;
+                Aw[(k & 3) * 128 + r * 8 + (k >> 2)] = evals[e];
+            }
+            wave_lds_sync();
+            const floatx4 a_lo = *reinterpret_cast<const floatx4*>(my_a);
+            const floatx4 a_hi = *reinterpret_cast<const floatx4*>(my_a + 4);
+            wave_lds_sync();
+            const float a[8] = {a_lo[0], a_lo[1], a_lo[2], a_lo[3],
+                                a_hi[0], a_hi[1], a_hi[2], a_hi[3]};
+#pragma unroll
+            for (int s = 0; s < 8; ++s) {
+                if (__ballot(cols[s] >= 0) == 0) break;  // padding columns end a tile
+#pragma unroll
+                for (int q = 0; q < VEC; ++q)
+                    acc[q] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s], R.v[s][q], acc[q], 0, 0, 0);
+            }
+            if (has1) {
+                R = Rn;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) { cols[i] = cols_next[i]; cols_next[i] = cols_after[i]; }
+            }
+        }
+    }
+    merge_into_c<TK, W>(acc, 1.0f, U, k0, O, c4, C, P);
+}
+
+// Waves per work-group: enough work-groups in flight to cover the chip (256 CUs x 4 SIMDs,
+// several waves each) while units are few; one wave per unit once units alone fill it.
+static int waves_per_unit(int num_units) {
+    if (num_units >= 8192) return 1;
+    if (num_units >= 4096) return 2;
+    return 4;
+}
+
+template <int TK, int W>
+static void launch_w(const DeviceFormat& F, const void* dB, bool b_f16, int O, float* dC,
+                     hipStream_t st) {
+    constexpr int VEC = TK / 16;
+    // Vector loads of B need O % VEC == 0 and a 16-byte aligned base.
+    const bool aligned = (O % VEC) == 0 && ((uintptr_t)dB % 16) == 0;
+    const bool c4 = (O % 4) == 0 && ((uintptr_t)dC % 16) == 0;
+    const dim3 grid((unsigned)(8 * ((F.num_units + 7) / 8)), (unsigned)((O + TK - 1) / TK));
+    const dim3 block(64 * W);
+    if (F.fp32) {
+        const float* B = static_cast<const float*>(dB);
+        if (aligned)
+            hipLaunchKernelGGL((k_spmm_f32<TK, true, W>), grid, block, 0, st, F.units.p,
+                               F.num_units, F.chunk_eptr.p, F.chunk_cols.p, F.entries.p, F.evals.p,
+                               B, O, c4, dC);
+        else
+            hipLaunchKernelGGL((k_spmm_f32<TK, false, W>), grid, block, 0, st, F.units.p,
+                               F.num_units, F.chunk_eptr.p, F.chunk_cols.p, F.entries.p, F.evals.p,
+                               B, O, c4, dC);
+    } else if (b_f16) {
+        const _Float16* B = static_cast<const _Float16*>(dB);
+        if (aligned)
+            hipLaunchKernelGGL((k_spmm_f16<TK, _Float16, true, W>), grid, block, 0, st, F.units.p,
+                               F.num_units, F.chunk_eptr.p, F.chunk_cols.p, F.entries.p, B, O,
+                               F.scale, c4, dC);
+        else
+            hipLaunchKernelGGL((k_spmm_f16<TK, _Float16, false, W>), grid, block, 0, st, F.units.p,
+                               F.num_units, F.chunk_eptr.p, F.chunk_cols.p, F.entries.p, B, O,
+                               F.scale, c4, dC);
+    } else {
+        const float* B = static_cast<const float*>(dB);
+        if (aligned)
+            hipLaunchKernelGGL((k_spmm_f16<TK, float, true, W>), grid, block, 0, st, F.units.p,
+                               F.num_units, F.chunk_eptr.p, F.chunk_cols.p, F.entries.p, B, O,
+                               F.scale, c4, dC);
+        else
+            hipLaunchKernelGGL((k_spmm_f16<TK, float, false, W>), grid, block, 0, st, F.units.p,
+                               F.num_units, F.chunk_eptr.p, F.chunk_cols.p, F.entries.p, B, O,
+                               F.scale, c4, dC);
+    }
+    VCSRMC_HIP(hipGetLastError());
 }
 
 template <int TK>
 static void launch_tk(const DeviceFormat& F, const void* dB, bool b_f16, int O, float* dC,
                       hipStream_t st) {
-    constexpr int VEC = TK / 16;
-    // Vector loads of B and the float4 epilogue need O % VEC == 0 and 16-byte aligned bases.
-    const bool aligned = (O % VEC) == 0 && ((uintptr_t)dB % 16) == 0 && ((uintptr_t)dC % 16) == 0;
-    const dim3 grid((unsigned)(8 * ((F.num_units + 7) / 8)), (unsigned)((O + TK - 1) / TK));
-    const dim3 block(64);
-    if (F.fp32) {
-        const float* B = static_cast<const float*>(dB);
-        if (aligned)
-            hipLaunchKernelGGL((k_spmm_f32<TK, true>), grid, block, 0, st, F.units.p, F.num_units,
-                               F.chunk_eptr.p, F.chunk_cols.p, F.entries.p, F.evals.p, B, O, dC);
-        else
-            hipLaunchKernelGGL((k_spmm_f32<TK, false>), grid, block, 0, st, F.units.p, F.num_units,
-                               F.chunk_eptr.p, F.chunk_cols.p, F.entries.p, F.evals.p, B, O, dC);
-    } else if (b_f16) {
-        const _Float16* B = static_cast<const _Float16*>(dB);
-        if (aligned)
-            hipLaunchKernelGGL((k_spmm_f16<TK, _Float16, true>), grid, block, 0, st, F.units.p,
-                               F.num_units, F.chunk_eptr.p, F.chunk_cols.p, F.entries.p, B, O,
-                               F.scale, dC);
-        else
-            hipLaunchKernelGGL((k_spmm_f16<TK, _Float16, false>), grid, block, 0, st, F.units.p,
-                               F.num_units, F.chunk_eptr.p, F.chunk_cols.p, F.entries.p, B, O,
-                               F.scale, dC);
-    } else {
-        const float* B = static_cast<const float*>(dB);
-        if (aligned)
-            hipLaunchKernelGGL((k_spmm_f16<TK, float, true>), grid, block, 0, st, F.units.p,
-                               F.num_units, F.chunk_eptr.p, F.chunk_cols.p, F.entries.p, B, O,
-                               F.scale, dC);
-        else
-            hipLaunchKernelGGL((k_spmm_f16<TK, float, false>), grid, block, 0, st, F.units.p,
-                               F.num_units, F.chunk_eptr.p, F.chunk_cols.p, F.entries.p, B, O,
-                               F.scale, dC);
+    switch (waves_per_unit(F.num_units)) {
+        case 1: launch_w<TK, 1>(F, dB, b_f16, O, dC, st); break;
+        case 2: launch_w<TK, 2>(F, dB, b_f16, O, dC, st); break;
+        default: launch_w<TK, 4>(F, dB, b_f16, O, dC, st); break;
     }
-    VCSRMC_HIP(hipGetLastError());
 }
 
 void spmm_launch(const DeviceFormat& F, const void* dB, bool b_f16, int O, int tileK, float* dC,
