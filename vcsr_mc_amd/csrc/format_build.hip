@@ -308,7 +308,7 @@ __global__ void k_panel_entries(const K* __restrict__ skey, const uint32_t* __re
                                 const float* __restrict__ tval, long long n,
                                 uint32_t* __restrict__ entries, float* __restrict__ evals,
                                 int* __restrict__ chunk_cols, int* __restrict__ chunk_eptr,
-                                int* __restrict__ pmask) {
+                                int* __restrict__ pmask, int* __restrict__ echunk) {
     const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
     const int j = pin[i] - 1;
@@ -317,6 +317,7 @@ __global__ void k_panel_entries(const K* __restrict__ skey, const uint32_t* __re
     const int k = lr % kChunkCols;
     const int r16 = (int)(skey[i] & 15);
     const uint32_t src = spay[i];
+    echunk[i] = c;
     const float v = tval[src];
     if constexpr (FP32) {
         entries[i] = (uint32_t)r16 | ((uint32_t)k << 4);
@@ -331,6 +332,35 @@ __global__ void k_panel_entries(const K* __restrict__ skey, const uint32_t* __re
         if (k == 0) chunk_eptr[c] = (int)i;
     }
     atomicOr(&pmask[j], 1 << r16);
+}
+
+__global__ void k_dense_flags(const int* __restrict__ eptr, int NC, int* __restrict__ flag) {
+    const long long c = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (c < NC) flag[c] = (eptr[c + 1] - eptr[c]) > kDenseMin;
+}
+
+__global__ void k_dense_index(const int* __restrict__ flag, const int* __restrict__ idx, int NC,
+                              int* __restrict__ chunk_dense) {
+    const long long c = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (c < NC) chunk_dense[c] = flag[c] ? idx[c] : -1;
+}
+
+template <bool FP32>
+__global__ void k_dense_fill(const uint32_t* __restrict__ entries, const float* __restrict__ evals,
+                             const int* __restrict__ echunk, const int* __restrict__ chunk_dense,
+                             long long n, _Float16* __restrict__ a16, float* __restrict__ a32) {
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const int d = chunk_dense[echunk[i]];
+    if (d < 0) return;
+    const uint32_t w = entries[i];
+    if constexpr (FP32) {
+        const int r = w & 15, k = (w >> 4) & 31;
+        a32[(long long)d * 512 + (k & 3) * 128 + r * 8 + (k >> 2)] = evals[i];
+    } else {
+        const int r = (w >> 16) & 15, k = (w >> 20) & 31;
+        a16[(long long)d * 512 + r * 32 + k] = __builtin_bit_cast(_Float16, (unsigned short)(w & 0xffffu));
+    }
 }
 
 __global__ void k_units_per_panel(const int* __restrict__ nch, int NP, int umax,
@@ -423,13 +453,39 @@ static void build_exec_layout_k(DeviceFormat& F, const int* trow, const int* tco
     fill<int>(F.chunk_cols.p, (long long)NC * kChunkCols, -1, st);
     fill<int>(F.chunk_eptr.p + NC, 1, (int)n, st);
     VCSRMC_HIP(hipMemsetAsync(pmask.p, 0, sizeof(int) * (size_t)NP, st));
+    DevBuf<int> echunk(n);
     if (F.fp32)
         LAUNCH((k_panel_entries<K, true>), n, kp, vp, hdist.p, dc.p, pin.p, pstart.p, cbase.p, tcol,
-               tval, n, F.entries.p, F.evals.p, F.chunk_cols.p, F.chunk_eptr.p, pmask.p);
+               tval, n, F.entries.p, F.evals.p, F.chunk_cols.p, F.chunk_eptr.p, pmask.p,
+               echunk.p);
     else
         LAUNCH((k_panel_entries<K, false>), n, kp, vp, hdist.p, dc.p, pin.p, pstart.p, cbase.p,
                tcol, tval, n, F.entries.p, (float*)nullptr, F.chunk_cols.p, F.chunk_eptr.p,
-               pmask.p);
+               pmask.p, echunk.p);
+
+    // dense copies of well-filled tiles
+    {
+        DevBuf<int> dflag(NC), didx(NC + 1);
+        LAUNCH(k_dense_flags, NC, F.chunk_eptr.p, NC, dflag.p);
+        exclusive_sum<int, int>(dflag.p, didx.p, NC, st);
+        const int ND = read_scalar(didx.p + NC, st);
+        F.chunk_dense.alloc(NC);
+        LAUNCH(k_dense_index, NC, dflag.p, didx.p, NC, F.chunk_dense.p);
+        F.num_dense = ND;
+        if (ND > 0) {
+            if (F.fp32) {
+                F.dense_a32.alloc((size_t)ND * 512);
+                VCSRMC_HIP(hipMemsetAsync(F.dense_a32.p, 0, sizeof(float) * 512 * (size_t)ND, st));
+                LAUNCH((k_dense_fill<true>), n, F.entries.p, F.evals.p, echunk.p, F.chunk_dense.p,
+                       n, (_Float16*)nullptr, F.dense_a32.p);
+            } else {
+                F.dense_a16.alloc((size_t)ND * 512);
+                VCSRMC_HIP(hipMemsetAsync(F.dense_a16.p, 0, sizeof(_Float16) * 512 * (size_t)ND, st));
+                LAUNCH((k_dense_fill<false>), n, F.entries.p, (const float*)nullptr, echunk.p,
+                       F.chunk_dense.p, n, F.dense_a16.p, (float*)nullptr);
+            }
+        }
+    }
 
     const int umax = unit_chunk_limit(NC);
     DevBuf<int> nu(NP), ubase(NP + 1);

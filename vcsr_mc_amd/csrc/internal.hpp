@@ -13,6 +13,8 @@ namespace vcsrmc {
 constexpr int kChunkCols = 32;
 // Rows per panel = MFMA M.
 constexpr int kPanelRows = 16;
+// A tile holding more nonzeros than this (of 16 x 32) is also stored dense.
+constexpr int kDenseMin = 192;
 
 // A format on one device.
 //
@@ -28,6 +30,10 @@ constexpr int kPanelRows = 16;
 //   chunk_cols[32c+k] = column of the chunk's k-th distinct column, -1 past the end
 //   entries[e]      FP16 format: f16 value | row-in-panel << 16 | k << 20
 //                   FP32 format: row-in-panel | k << 4, with the value in evals[e]
+//   chunk_dense[c]  -1, or the index of the tile's dense copy when more than kDenseMin of its
+//                   512 slots are filled: dense_a16[512 d + 32 row + k] (FP16), or
+//                   dense_a32[512 d + 128 (k & 3) + 8 row + (k >> 2)] (FP32) -- exactly the
+//                   order in which MFMA lanes read their A operand, so a lane loads it directly
 struct DeviceFormat {
     int M = 0, N = 0, segw = 16, bundle = 16, num_segments = 0;
     int G = 0, nitems = 0;
@@ -43,6 +49,10 @@ struct DeviceFormat {
     DevBuf<int> chunk_eptr, chunk_cols;
     DevBuf<uint32_t> entries;
     DevBuf<float> evals;
+    int num_dense = 0;
+    DevBuf<int> chunk_dense;
+    DevBuf<_Float16> dense_a16;
+    DevBuf<float> dense_a32;
 
     bool ready = false;
     void clear() { *this = DeviceFormat(); }

@@ -175,14 +175,29 @@ __device__ __forceinline__ void merge_into_c(const floatx4 (&acc)[TK / 16], floa
     }
 }
 
+__device__ __forceinline__ uint4 load_a_state(int d, int c, int lane, int a_off,
+                                              const int* __restrict__ chunk_eptr,
+                                              const uint32_t* __restrict__ entries,
+                                              const _Float16* __restrict__ dense_a) {
+    if (d >= 0) return *reinterpret_cast<const uint4*>(dense_a + (long long)d * 512 + a_off);
+    const int eb = chunk_eptr[c], ee = chunk_eptr[c + 1];
+    uint4 s = {0u, 0u, (unsigned)eb, (unsigned)ee};
+    if (eb + lane < ee) s.x = entries[eb + lane];
+    if (eb + 64 + lane < ee) s.y = entries[eb + 64 + lane];
+    return s;
+}
+
 // FP16 format.  W waves per work-group share one unit: wave w takes tiles U.y + w, +W, ...
-// Each wave pipelines its tiles: while tile c is multiplied, the B rows and the first 128
-// nonzeros of its next tile and the column indices of the tile after are in flight.
+// Each wave pipelines its tiles: while tile c is multiplied, the B rows and the A data (dense
+// operand, or the first 128 nonzeros) of its next tile and the column indices of the tile
+// after are in flight.
 template <int TK, typename TB, bool ALIGNED, int W>
 __global__ __launch_bounds__(64 * W) void k_spmm_f16(const int4* __restrict__ units, int num_units,
                                                      const int* __restrict__ chunk_eptr,
                                                      const int* __restrict__ chunk_cols,
+                                                     const int* __restrict__ chunk_dense,
                                                      const uint32_t* __restrict__ entries,
+                                                     const _Float16* __restrict__ dense_a,
                                                      const TB* __restrict__ B, int O, float scale,
                                                      bool c4, float* __restrict__ C) {
     constexpr int VEC = TK / 16;
@@ -195,6 +210,7 @@ __global__ __launch_bounds__(64 * W) void k_spmm_f16(const int4* __restrict__ un
     const int k0 = blockIdx.y * TK;
     const int c0 = k0 + VEC * n;
     const long long OL = O;
+    const int a_off = n * 32 + 8 * g;  // this lane's A operand inside a dense tile
 
     floatx4 acc[VEC];
 #pragma unroll
@@ -212,33 +228,37 @@ __global__ __launch_bounds__(64 * W) void k_spmm_f16(const int4* __restrict__ un
             load_b_rows<VEC, TB, ALIGNED>(B, cols, OL, c0, R);
         }
         if (c + W < U.z) load_cols8(chunk_cols, c + W, g, cols_next);
-        int eb = chunk_eptr[c], ee = chunk_eptr[c + 1];
-        uint32_t w0 = 0, w1 = 0;
-        if (eb + lane < ee) w0 = entries[eb + lane];
-        if (eb + 64 + lane < ee) w1 = entries[eb + 64 + lane];
+        // A state of a tile in 4 registers: the dense operand (8 halves), or the first two
+        // nonzeros of this lane and the tile's entry range {w0, w1, eb, ee}.
+        int d = chunk_dense[c];
+        uint4 cur = load_a_state(d, c, lane, a_off, chunk_eptr, entries, dense_a);
 
         for (; c < U.z; c += W) {
             const bool has1 = c + W < U.z;
             BRows<VEC, TB> Rn;
-            int eb1 = 0, ee1 = 0;
-            uint32_t n0 = 0, n1 = 0;
+            int d1 = -1;
+            uint4 nxt = {0u, 0u, 0u, 0u};
             int cols_after[8];
             if (has1) {
                 load_b_rows<VEC, TB, ALIGNED>(B, cols_next, OL, c0, Rn);
-                eb1 = chunk_eptr[c + W];
-                ee1 = chunk_eptr[c + W + 1];
-                if (eb1 + lane < ee1) n0 = entries[eb1 + lane];
-                if (eb1 + 64 + lane < ee1) n1 = entries[eb1 + 64 + lane];
+                d1 = chunk_dense[c + W];
+                nxt = load_a_state(d1, c + W, lane, a_off, chunk_eptr, entries, dense_a);
                 if (c + 2 * W < U.z) load_cols8(chunk_cols, c + 2 * W, g, cols_after);
             }
-            *reinterpret_cast<half8*>(my_a) = half8{0, 0, 0, 0, 0, 0, 0, 0};
-            wave_lds_sync();
-            if (eb + lane < ee) scatter_a_f16(Aw, w0);
-            if (eb + 64 + lane < ee) scatter_a_f16(Aw, w1);
-            for (int e = eb + 128 + lane; e < ee; e += 64) scatter_a_f16(Aw, entries[e]);
-            wave_lds_sync();
-            const half8 a = *reinterpret_cast<const half8*>(my_a);
-            wave_lds_sync();
+            half8 a;
+            if (d >= 0) {
+                a = __builtin_bit_cast(half8, cur);
+            } else {
+                const int eb = (int)cur.z, ee = (int)cur.w;
+                *reinterpret_cast<half8*>(my_a) = half8{0, 0, 0, 0, 0, 0, 0, 0};
+                wave_lds_sync();
+                if (eb + lane < ee) scatter_a_f16(Aw, cur.x);
+                if (eb + 64 + lane < ee) scatter_a_f16(Aw, cur.y);
+                for (int e = eb + 128 + lane; e < ee; e += 64) scatter_a_f16(Aw, entries[e]);
+                wave_lds_sync();
+                a = *reinterpret_cast<const half8*>(my_a);
+                wave_lds_sync();
+            }
 #pragma unroll
             for (int q = 0; q < VEC; ++q) {
                 const half8 b = half8{(_Float16)R.v[0][q], (_Float16)R.v[1][q],
@@ -251,27 +271,28 @@ __global__ __launch_bounds__(64 * W) void k_spmm_f16(const int4* __restrict__ un
                 R = Rn;
 #pragma unroll
                 for (int i = 0; i < 8; ++i) cols_next[i] = cols_after[i];
-                w0 = n0; w1 = n1;
-                eb = eb1; ee = ee1;
+                d = d1;
+                cur = nxt;
             }
         }
     }
     merge_into_c<TK, W>(acc, scale, U, k0, O, c4, C, P);
 }
 
-// FP32 format: eight K steps of v_mfma_f32_16x16x4_f32 per tile.  The A tile is stored
-// K-step-major so a lane's 8 values (k = 4s + g, s = 0..7) are contiguous:
-// At[(k & 3) * 128 + row * 8 + (k >> 2)].
+// FP32 format: eight K steps of v_mfma_f32_16x16x4_f32 per tile; lane (n, g) feeds tile
+// columns k = 4s + g (s = 0..7).  The A tile (LDS or dense copy) is K-step-major so a lane's 8
+// values are contiguous: [(k & 3) * 128 + row * 8 + (k >> 2)].  B is fetched in half tiles
+// (steps 0-3, then 4-7) so one half is in flight while the other is multiplied.
 template <int VEC>
 struct FRows {
-    float v[8][VEC];
+    float v[4][VEC];
 };
 
 template <int VEC, bool ALIGNED>
-__device__ __forceinline__ void load_b_rows_f32(const float* __restrict__ B, const int (&cols)[8],
+__device__ __forceinline__ void load_b_half_f32(const float* __restrict__ B, const int* cols,
                                                 long long O, int c0, FRows<VEC>& R) {
 #pragma unroll
-    for (int s = 0; s < 8; ++s) {
+    for (int s = 0; s < 4; ++s) {
         const int col = cols[s];
         const float* src = B + (long long)(col < 0 ? 0 : col) * O + c0;
         if constexpr (ALIGNED && VEC >= 4) {
@@ -297,12 +318,26 @@ __device__ __forceinline__ void load_cols_steps(const int* __restrict__ chunk_co
     for (int s = 0; s < 8; ++s) cols[s] = cc[4 * s + g];
 }
 
+template <int VEC>
+__device__ __forceinline__ void mfma_half_f32(const float (&a)[8], int s0, const int (&cols)[8],
+                                              const FRows<VEC>& R, floatx4 (&acc)[VEC]) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+        if (__ballot(cols[s0 + s] >= 0) == 0) return;  // padding columns end a tile
+#pragma unroll
+        for (int q = 0; q < VEC; ++q)
+            acc[q] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s0 + s], R.v[s][q], acc[q], 0, 0, 0);
+    }
+}
+
 template <int TK, bool ALIGNED, int W>
-__global__ __launch_bounds__(64 * W) void k_spmm_f32(const int4* __restrict__ units, int num_units,
+__global__ __launch_bounds__(64 * W, 3) void k_spmm_f32(const int4* __restrict__ units, int num_units,
                                                      const int* __restrict__ chunk_eptr,
                                                      const int* __restrict__ chunk_cols,
+                                                     const int* __restrict__ chunk_dense,
                                                      const uint32_t* __restrict__ entries,
                                                      const float* __restrict__ evals,
+                                                     const float* __restrict__ dense_a,
                                                      const float* __restrict__ B, int O, bool c4,
                                                      float* __restrict__ C) {
     constexpr int VEC = TK / 16;
@@ -315,52 +350,54 @@ __global__ __launch_bounds__(64 * W) void k_spmm_f32(const int4* __restrict__ un
     const int k0 = blockIdx.y * TK;
     const int c0 = k0 + VEC * n;
     const long long OL = O;
+    const int a_off = g * 128 + n * 8;
 
     floatx4 acc[VEC];
 #pragma unroll
     for (int q = 0; q < VEC; ++q) acc[q] = floatx4{0.f, 0.f, 0.f, 0.f};
     float* Aw = At[wave];
-    float* my_a = &Aw[g * 128 + n * 8];
+    float* my_a = &Aw[a_off];
 
     int c = U.y + wave;
     if (c < U.z) {
         int cols[8], cols_next[8];
-        FRows<VEC> R;
+        FRows<VEC> R0, R1;
         load_cols_steps(chunk_cols, c, g, cols);
-        load_b_rows_f32<VEC, ALIGNED>(B, cols, OL, c0, R);
+        load_b_half_f32<VEC, ALIGNED>(B, cols, OL, c0, R0);
         if (c + W < U.z) load_cols_steps(chunk_cols, c + W, g, cols_next);
         for (; c < U.z; c += W) {
             const bool has1 = c + W < U.z;
-            FRows<VEC> Rn;
-            int cols_after[8];
-            if (has1) {
-                load_b_rows_f32<VEC, ALIGNED>(B, cols_next, OL, c0, Rn);
-                if (c + 2 * W < U.z) load_cols_steps(chunk_cols, c + 2 * W, g, cols_after);
+            load_b_half_f32<VEC, ALIGNED>(B, cols + 4, OL, c0, R1);
+            const int d = chunk_dense[c];
+            floatx4 a_lo, a_hi;
+            if (d >= 0) {
+                a_lo = *reinterpret_cast<const floatx4*>(dense_a + (long long)d * 512 + a_off);
+                a_hi = *reinterpret_cast<const floatx4*>(dense_a + (long long)d * 512 + a_off + 4);
+            } else {
+                const int eb = chunk_eptr[c], ee = chunk_eptr[c + 1];
+                *reinterpret_cast<floatx4*>(my_a) = floatx4{0.f, 0.f, 0.f, 0.f};
+                *reinterpret_cast<floatx4*>(my_a + 4) = floatx4{0.f, 0.f, 0.f, 0.f};
+                wave_lds_sync();
+                for (int e = eb + lane; e < ee; e += 64) {
+                    const uint32_t w = entries[e];
+                    const int r = w & 15, k = (w >> 4) & 31;
+                    Aw[(k & 3) * 128 + r * 8 + (k >> 2)] = evals[e];
+                }
+                wave_lds_sync();
+                a_lo = *reinterpret_cast<const floatx4*>(my_a);
+                a_hi = *reinterpret_cast<const floatx4*>(my_a + 4);
+                wave_lds_sync();
             }
-            const int eb = chunk_eptr[c], ee = chunk_eptr[c + 1];
-            *reinterpret_cast<floatx4*>(my_a) = floatx4{0.f, 0.f, 0.f, 0.f};
-            *reinterpret_cast<floatx4*>(my_a + 4) = floatx4{0.f, 0.f, 0.f, 0.f};
-            wave_lds_sync();
-            for (int e = eb + lane; e < ee; e += 64) {
-                const uint32_t w = entries[e];
-                const int r = w & 15, k = (w >> 4) & 31;
-                Aw[(k & 3) * 128 + r * 8 + (k >> 2)] = evals[e];
-            }
-            wave_lds_sync();
-            const floatx4 a_lo = *reinterpret_cast<const floatx4*>(my_a);
-            const floatx4 a_hi = *reinterpret_cast<const floatx4*>(my_a + 4);
-            wave_lds_sync();
             const float a[8] = {a_lo[0], a_lo[1], a_lo[2], a_lo[3],
                                 a_hi[0], a_hi[1], a_hi[2], a_hi[3]};
-#pragma unroll
-            for (int s = 0; s < 8; ++s) {
-                if (__ballot(cols[s] >= 0) == 0) break;  // padding columns end a tile
-#pragma unroll
-                for (int q = 0; q < VEC; ++q)
-                    acc[q] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s], R.v[s][q], acc[q], 0, 0, 0);
-            }
+            mfma_half_f32<VEC>(a, 0, cols, R0, acc);
+            int cols_after[8];
             if (has1) {
-                R = Rn;
+                load_b_half_f32<VEC, ALIGNED>(B, cols_next, OL, c0, R0);
+                if (c + 2 * W < U.z) load_cols_steps(chunk_cols, c + 2 * W, g, cols_after);
+            }
+            mfma_half_f32<VEC>(a, 4, cols, R1, acc);
+            if (has1) {
 #pragma unroll
                 for (int i = 0; i < 8; ++i) { cols[i] = cols_next[i]; cols_next[i] = cols_after[i]; }
             }
@@ -390,32 +427,32 @@ static void launch_w(const DeviceFormat& F, const void* dB, bool b_f16, int O, f
         const float* B = static_cast<const float*>(dB);
         if (aligned)
             hipLaunchKernelGGL((k_spmm_f32<TK, true, W>), grid, block, 0, st, F.units.p,
-                               F.num_units, F.chunk_eptr.p, F.chunk_cols.p, F.entries.p, F.evals.p,
-                               B, O, c4, dC);
+                               F.num_units, F.chunk_eptr.p, F.chunk_cols.p, F.chunk_dense.p, F.entries.p,
+                               F.evals.p, F.dense_a32.p, B, O, c4, dC);
         else
             hipLaunchKernelGGL((k_spmm_f32<TK, false, W>), grid, block, 0, st, F.units.p,
-                               F.num_units, F.chunk_eptr.p, F.chunk_cols.p, F.entries.p, F.evals.p,
-                               B, O, c4, dC);
+                               F.num_units, F.chunk_eptr.p, F.chunk_cols.p, F.chunk_dense.p, F.entries.p,
+                               F.evals.p, F.dense_a32.p, B, O, c4, dC);
     } else if (b_f16) {
         const _Float16* B = static_cast<const _Float16*>(dB);
         if (aligned)
             hipLaunchKernelGGL((k_spmm_f16<TK, _Float16, true, W>), grid, block, 0, st, F.units.p,
-                               F.num_units, F.chunk_eptr.p, F.chunk_cols.p, F.entries.p, B, O,
-                               F.scale, c4, dC);
+                               F.num_units, F.chunk_eptr.p, F.chunk_cols.p, F.chunk_dense.p,
+                               F.entries.p, F.dense_a16.p, B, O, F.scale, c4, dC);
         else
             hipLaunchKernelGGL((k_spmm_f16<TK, _Float16, false, W>), grid, block, 0, st, F.units.p,
-                               F.num_units, F.chunk_eptr.p, F.chunk_cols.p, F.entries.p, B, O,
-                               F.scale, c4, dC);
+                               F.num_units, F.chunk_eptr.p, F.chunk_cols.p, F.chunk_dense.p,
+                               F.entries.p, F.dense_a16.p, B, O, F.scale, c4, dC);
     } else {
         const float* B = static_cast<const float*>(dB);
         if (aligned)
             hipLaunchKernelGGL((k_spmm_f16<TK, float, true, W>), grid, block, 0, st, F.units.p,
-                               F.num_units, F.chunk_eptr.p, F.chunk_cols.p, F.entries.p, B, O,
-                               F.scale, c4, dC);
+                               F.num_units, F.chunk_eptr.p, F.chunk_cols.p, F.chunk_dense.p,
+                               F.entries.p, F.dense_a16.p, B, O, F.scale, c4, dC);
         else
             hipLaunchKernelGGL((k_spmm_f16<TK, float, false, W>), grid, block, 0, st, F.units.p,
-                               F.num_units, F.chunk_eptr.p, F.chunk_cols.p, F.entries.p, B, O,
-                               F.scale, c4, dC);
+                               F.num_units, F.chunk_eptr.p, F.chunk_cols.p, F.chunk_dense.p,
+                               F.entries.p, F.dense_a16.p, B, O, F.scale, c4, dC);
     }
     VCSRMC_HIP(hipGetLastError());
 }
