@@ -50,6 +50,8 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--graph", action="store_true",
                    help="replay the timed steps from a captured HIP graph")
+    p.add_argument("--copy-probe-mib", type=int, default=0,
+                   help="also run a plain device copy of this size (PMC traffic calibration)")
     return p.parse_args()
 
 
@@ -269,6 +271,16 @@ def main():
         except Exception:
             model = "unknown"
         out["cpu_model"] = model
+
+    if args.copy_probe_mib:
+        # a plain copy of known size: reads and writes copy_probe_mib MiB once
+        nelem = args.copy_probe_mib * (1 << 20) // 4
+        src = torch.ones(nelem, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        out["copy_probe_bytes"] = nelem * 4
 
     fmt.close()
     print(json.dumps(out), flush=True)
