@@ -363,25 +363,45 @@ __global__ void k_dense_fill(const uint32_t* __restrict__ entries, const float* 
     }
 }
 
-__global__ void k_units_per_panel(const int* __restrict__ nch, int NP, int umax,
-                                  int* __restrict__ nu) {
+// Units.  A panel with at most `light_max` tiles is one light unit (one wave); a larger panel
+// is cut into heavy units of at most kHeavyTiles tiles (the waves of a work-group share them).
+__global__ void k_units_per_panel(const int* __restrict__ nch, int NP, int light_max,
+                                  int* __restrict__ nu, int* __restrict__ nheavy) {
     const long long j = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (j < NP) nu[j] = (nch[j] + umax - 1) / umax;
+    if (j >= NP) return;
+    const bool heavy = nch[j] > light_max;
+    const int n = heavy ? (nch[j] + kHeavyTiles - 1) / kHeavyTiles : 1;
+    nu[j] = n;
+    nheavy[j] = heavy ? n : 0;
 }
 
+// Writes the units of panel j (in panel order) with their schedule keys: heavy units first,
+// then light; larger first inside each class (the stable sort keeps panel order on ties).
 __global__ void k_make_units(const int* __restrict__ cbase, const int* __restrict__ ubase,
-                             const int* __restrict__ ppanel, const int* __restrict__ pmask, int NP,
-                             int umax, int4* __restrict__ units) {
+                             const int* __restrict__ ppanel, const int* __restrict__ pmask,
+                             const int* __restrict__ nch, int NP, int light_max,
+                             int4* __restrict__ units, uint32_t* __restrict__ key,
+                             uint32_t* __restrict__ pay) {
     const long long j = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     if (j >= NP) return;
     const int c0 = cbase[j], c1 = cbase[j + 1];
     const int u0 = ubase[j], nu = ubase[j + 1] - u0;
+    const bool heavy = nch[j] > light_max;
     const int split = nu > 1 ? (1 << 16) : 0;
+    const int step = heavy ? kHeavyTiles : (c1 - c0);
     for (int u = 0; u < nu; ++u) {
-        const int cb = c0 + u * umax;
-        units[u0 + u] = make_int4(ppanel[j] * kPanelRows, cb, min(cb + umax, c1),
-                                  (pmask[j] & 0xffff) | split);
+        const int cb = c0 + u * step;
+        const int ce = min(cb + step, c1);
+        units[u0 + u] = make_int4(ppanel[j] * kPanelRows, cb, ce, (pmask[j] & 0xffff) | split);
+        key[u0 + u] = ((heavy ? 0u : 1u) << 16) | (uint32_t)(0xffff - min(ce - cb, 0xffff));
+        pay[u0 + u] = (uint32_t)(u0 + u);
     }
+}
+
+__global__ void k_gather_units(const int4* __restrict__ in, const uint32_t* __restrict__ perm,
+                               int NU, int4* __restrict__ out) {
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < NU) out[i] = in[perm[i]];
 }
 
 static inline unsigned blocks(long long n) { return grid_for(n, 256); }
@@ -407,13 +427,12 @@ static void check_err(const int* d_err, hipStream_t st) {
         throw Error(VCSRMC_ERR_FORMAT, "format holds the same (row, column) twice");
 }
 
-// Tiles per unit.  The multiply kernel spreads a unit's tiles over the waves of one
-// work-group and merges them in LDS, so only panels with more tiles than this are split over
-// several units (merged in C with device-scope atomics, which on MI355X resolve past the
-// per-XCD L2 and are expensive).
-static int unit_chunk_limit(long long num_chunks) {
-    (void)num_chunks;
-    return 16;
+// Panels of at most this many tiles are light units (one wave each, four per work-group);
+// larger panels become heavy units that the four waves of a work-group share and merge in LDS.
+// Small problems make every multi-tile panel heavy so that enough waves are in flight; large
+// ones keep panels of up to 16 tiles on a single wave.
+static int light_tile_limit(long long num_chunks) {
+    return (int)std::max(1LL, std::min(16LL, num_chunks / 8192));
 }
 
 template <typename K>
@@ -487,18 +506,29 @@ static void build_exec_layout_k(DeviceFormat& F, const int* trow, const int* tco
         }
     }
 
-    const int umax = unit_chunk_limit(NC);
-    DevBuf<int> nu(NP), ubase(NP + 1);
-    LAUNCH(k_units_per_panel, NP, nch.p, NP, umax, nu.p);
+    const int light_max = light_tile_limit(NC);
+    DevBuf<int> nu(NP), ubase(NP + 1), nheavy(NP), hbase(NP + 1);
+    LAUNCH(k_units_per_panel, NP, nch.p, NP, light_max, nu.p, nheavy.p);
     exclusive_sum<int, int>(nu.p, ubase.p, NP, st);
+    exclusive_sum<int, int>(nheavy.p, hbase.p, NP, st);
     const int NU = read_scalar(ubase.p + NP, st);
-    F.units.alloc(NU);
-    LAUNCH(k_make_units, NP, cbase.p, ubase.p, ppanel.p, pmask.p, NP, umax, F.units.p);
-    VCSRMC_HIP(hipStreamSynchronize(st));
+    const int NH = read_scalar(hbase.p + NP, st);
+    {
+        DevBuf<int4> raw(NU);
+        DevBuf<uint32_t> k1(NU), k2(NU), v1(NU), v2(NU);
+        LAUNCH(k_make_units, NP, cbase.p, ubase.p, ppanel.p, pmask.p, nch.p, NP, light_max, raw.p,
+               k1.p, v1.p);
+        uint32_t *kp2 = k1.p, *ka2 = k2.p, *vp2 = v1.p, *va2 = v2.p;
+        radix_sort_pairs<uint32_t>(kp2, vp2, ka2, va2, NU, 17, st);
+        F.units.alloc(NU);
+        LAUNCH(k_gather_units, NU, raw.p, vp2, NU, F.units.p);
+        VCSRMC_HIP(hipStreamSynchronize(st));
+    }
     F.num_panels = NP;
     F.num_chunks = NC;
     F.num_units = NU;
-    F.unit_chunks = umax;
+    F.num_heavy = NH;
+    F.light_max = light_max;
 }
 
 static void build_exec_layout(DeviceFormat& F, const int* trow, const int* tcol, const float* tval,

@@ -15,6 +15,9 @@ constexpr int kChunkCols = 32;
 constexpr int kPanelRows = 16;
 // A tile holding more nonzeros than this (of 16 x 32) is also stored dense.
 constexpr int kDenseMin = 192;
+// Tiles per heavy unit (shared by the kWaves waves of one work-group).
+constexpr int kHeavyTiles = 64;
+constexpr int kWaves = 4;
 
 // A format on one device.
 //
@@ -25,7 +28,9 @@ constexpr int kDenseMin = 192;
 // Execution layout (what the multiply kernels read), derived from the same matrix:
 //   units[u]        = {row0, chunk_begin, chunk_end, rowmask | split << 16}
 //                     a run of chunks of one 16-row panel; split = the panel has several
-//                     units, whose partial sums meet in C through atomics
+//                     units, whose partial sums meet in C through atomics.  The first
+//                     num_heavy units are heavy (one work-group each, larger first), the rest
+//                     light (one wave each, four per work-group, larger first).
 //   chunk_eptr[c]   = first entry of chunk c (chunk_eptr[num_chunks] = nnz)
 //   chunk_cols[32c+k] = column of the chunk's k-th distinct column, -1 past the end
 //   entries[e]      FP16 format: f16 value | row-in-panel << 16 | k << 20
@@ -44,7 +49,7 @@ struct DeviceFormat {
     DevBuf<int> group_ptr, group_depth, group_seg_base, group_rows, lcol, item_gbeg, item_gend;
     DevBuf<float> val;
 
-    int num_panels = 0, num_chunks = 0, num_units = 0, unit_chunks = 0;
+    int num_panels = 0, num_chunks = 0, num_units = 0, num_heavy = 0, light_max = 0;
     DevBuf<int4> units;
     DevBuf<int> chunk_eptr, chunk_cols;
     DevBuf<uint32_t> entries;

@@ -187,39 +187,43 @@ __device__ __forceinline__ uint4 load_a_state(int d, int c, int lane, int a_off,
     return s;
 }
 
-// FP16 format.  W waves per work-group share one unit: wave w takes tiles U.y + w, +W, ...
-// Each wave pipelines its tiles: while tile c is multiplied, the B rows and the A data (dense
-// operand, or the first 128 nonzeros) of its next tile and the column indices of the tile
-// after are in flight.
-template <int TK, typename TB, bool ALIGNED, int W>
-__global__ __launch_bounds__(64 * W) void k_spmm_f16(const int4* __restrict__ units, int num_units,
-                                                     const int* __restrict__ chunk_eptr,
-                                                     const int* __restrict__ chunk_cols,
-                                                     const int* __restrict__ chunk_dense,
-                                                     const uint32_t* __restrict__ entries,
-                                                     const _Float16* __restrict__ dense_a,
-                                                     const TB* __restrict__ B, int O, float scale,
-                                                     bool c4, float* __restrict__ C) {
+// Schedule of a 4-wave work-group.  Work-groups [0, H8) run the heavy units (H8 = num_heavy
+// rounded up to a multiple of 8): the four waves share one unit's tiles.  The others run light
+// units, one per wave, mapped so that each XCD walks a contiguous range of them (work-groups
+// are dealt to the 8 XCDs round robin).  Returns false if this wave has nothing to do.
+__device__ __forceinline__ bool schedule(int num_units, int num_heavy, int wave, int& u,
+                                         bool& heavy) {
+    const int h8 = (num_heavy + 7) & ~7;
+    const int b = blockIdx.x;
+    if (b < h8) {
+        heavy = true;
+        u = b;
+        return b < num_heavy;
+    }
+    heavy = false;
+    const int nlw = (num_units - num_heavy + kWaves - 1) / kWaves;
+    const int j = unit_of_block(b - h8, nlw);
+    u = num_heavy + j * kWaves + wave;
+    return j < nlw && u < num_units;
+}
+
+// FP16 tiles [first, end) with stride W of one unit, accumulated into acc.  While tile c is
+// multiplied, the B rows and the A state (dense operand, or first nonzeros and entry range) of
+// the wave's next tile and the column indices of the tile after are in flight.
+template <int TK, typename TB, bool ALIGNED>
+__device__ __forceinline__ void tiles_f16(int first, int end, int W, int lane, int n, int g,
+                                          int c0, long long OL, const int* __restrict__ chunk_eptr,
+                                          const int* __restrict__ chunk_cols,
+                                          const int* __restrict__ chunk_dense,
+                                          const uint32_t* __restrict__ entries,
+                                          const _Float16* __restrict__ dense_a,
+                                          const TB* __restrict__ B, _Float16* Aw,
+                                          floatx4 (&acc)[TK / 16]) {
     constexpr int VEC = TK / 16;
-    __shared__ __attribute__((aligned(16))) _Float16 As[W][16 * kApitch];
-    __shared__ __attribute__((aligned(16))) float P[W > 1 ? W * 16 * TK : 4];
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
-    const int u = unit_of_block(blockIdx.x, num_units);
-    if (u >= num_units) return;
-    const int4 U = units[u];
-    const int k0 = blockIdx.y * TK;
-    const int c0 = k0 + VEC * n;
-    const long long OL = O;
     const int a_off = n * 32 + 8 * g;  // this lane's A operand inside a dense tile
-
-    floatx4 acc[VEC];
-#pragma unroll
-    for (int q = 0; q < VEC; ++q) acc[q] = floatx4{0.f, 0.f, 0.f, 0.f};
-    _Float16* Aw = As[wave];
     _Float16* my_a = &Aw[n * kApitch + 8 * g];
-
-    int c = U.y + wave;
-    if (c < U.z) {
+    int c = first;
+    if (c < end) {
         int cols_next[8];
         BRows<VEC, TB> R;
         {
@@ -227,14 +231,14 @@ __global__ __launch_bounds__(64 * W) void k_spmm_f16(const int4* __restrict__ un
             load_cols8(chunk_cols, c, g, cols);
             load_b_rows<VEC, TB, ALIGNED>(B, cols, OL, c0, R);
         }
-        if (c + W < U.z) load_cols8(chunk_cols, c + W, g, cols_next);
+        if (c + W < end) load_cols8(chunk_cols, c + W, g, cols_next);
         // A state of a tile in 4 registers: the dense operand (8 halves), or the first two
         // nonzeros of this lane and the tile's entry range {w0, w1, eb, ee}.
         int d = chunk_dense[c];
         uint4 cur = load_a_state(d, c, lane, a_off, chunk_eptr, entries, dense_a);
 
-        for (; c < U.z; c += W) {
-            const bool has1 = c + W < U.z;
+        for (; c < end; c += W) {
+            const bool has1 = c + W < end;
             BRows<VEC, TB> Rn;
             int d1 = -1;
             uint4 nxt = {0u, 0u, 0u, 0u};
@@ -243,7 +247,7 @@ __global__ __launch_bounds__(64 * W) void k_spmm_f16(const int4* __restrict__ un
                 load_b_rows<VEC, TB, ALIGNED>(B, cols_next, OL, c0, Rn);
                 d1 = chunk_dense[c + W];
                 nxt = load_a_state(d1, c + W, lane, a_off, chunk_eptr, entries, dense_a);
-                if (c + 2 * W < U.z) load_cols8(chunk_cols, c + 2 * W, g, cols_after);
+                if (c + 2 * W < end) load_cols8(chunk_cols, c + 2 * W, g, cols_after);
             }
             half8 a;
             if (d >= 0) {
@@ -276,7 +280,33 @@ __global__ __launch_bounds__(64 * W) void k_spmm_f16(const int4* __restrict__ un
             }
         }
     }
-    merge_into_c<TK, W>(acc, scale, U, k0, O, c4, C, P);
+}
+
+template <int TK, typename TB, bool ALIGNED>
+__global__ __launch_bounds__(64 * kWaves) void k_spmm_f16(
+    const int4* __restrict__ units, int num_units, int num_heavy,
+    const int* __restrict__ chunk_eptr, const int* __restrict__ chunk_cols,
+    const int* __restrict__ chunk_dense, const uint32_t* __restrict__ entries,
+    const _Float16* __restrict__ dense_a, const TB* __restrict__ B, int O, float scale, bool c4,
+    float* __restrict__ C) {
+    constexpr int VEC = TK / 16;
+    __shared__ __attribute__((aligned(16))) _Float16 As[kWaves][16 * kApitch];
+    __shared__ __attribute__((aligned(16))) float P[kWaves * 16 * TK];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
+    int u;
+    bool heavy;
+    if (!schedule(num_units, num_heavy, wave, u, heavy)) return;
+    const int4 U = units[u];
+    const int k0 = blockIdx.y * TK;
+    const int c0 = k0 + VEC * n;
+    floatx4 acc[VEC];
+#pragma unroll
+    for (int q = 0; q < VEC; ++q) acc[q] = floatx4{0.f, 0.f, 0.f, 0.f};
+    tiles_f16<TK, TB, ALIGNED>(heavy ? U.y + wave : U.y, U.z, heavy ? kWaves : 1, lane, n, g, c0,
+                               (long long)O, chunk_eptr, chunk_cols, chunk_dense, entries, dense_a,
+                               B, As[wave], acc);
+    if (heavy) merge_into_c<TK, kWaves>(acc, scale, U, k0, O, c4, C, P);
+    else merge_into_c<TK, 1>(acc, scale, U, k0, O, c4, C, P);
 }
 
 // FP32 format: eight K steps of v_mfma_f32_16x16x4_f32 per tile; lane (n, g) feeds tile
@@ -330,43 +360,28 @@ __device__ __forceinline__ void mfma_half_f32(const float (&a)[8], int s0, const
     }
 }
 
-template <int TK, bool ALIGNED, int W>
-__global__ __launch_bounds__(64 * W, 3) void k_spmm_f32(const int4* __restrict__ units, int num_units,
-                                                     const int* __restrict__ chunk_eptr,
-                                                     const int* __restrict__ chunk_cols,
-                                                     const int* __restrict__ chunk_dense,
-                                                     const uint32_t* __restrict__ entries,
-                                                     const float* __restrict__ evals,
-                                                     const float* __restrict__ dense_a,
-                                                     const float* __restrict__ B, int O, bool c4,
-                                                     float* __restrict__ C) {
+template <int TK, bool ALIGNED>
+__device__ __forceinline__ void tiles_f32(int first, int end, int W, int lane, int n, int g,
+                                          int c0, long long OL, const int* __restrict__ chunk_eptr,
+                                          const int* __restrict__ chunk_cols,
+                                          const int* __restrict__ chunk_dense,
+                                          const uint32_t* __restrict__ entries,
+                                          const float* __restrict__ evals,
+                                          const float* __restrict__ dense_a,
+                                          const float* __restrict__ B, float* Aw,
+                                          floatx4 (&acc)[TK / 16]) {
     constexpr int VEC = TK / 16;
-    __shared__ __attribute__((aligned(16))) float At[W][4 * 16 * 8];
-    __shared__ __attribute__((aligned(16))) float P[W > 1 ? W * 16 * TK : 4];
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
-    const int u = unit_of_block(blockIdx.x, num_units);
-    if (u >= num_units) return;
-    const int4 U = units[u];
-    const int k0 = blockIdx.y * TK;
-    const int c0 = k0 + VEC * n;
-    const long long OL = O;
     const int a_off = g * 128 + n * 8;
-
-    floatx4 acc[VEC];
-#pragma unroll
-    for (int q = 0; q < VEC; ++q) acc[q] = floatx4{0.f, 0.f, 0.f, 0.f};
-    float* Aw = At[wave];
     float* my_a = &Aw[a_off];
-
-    int c = U.y + wave;
-    if (c < U.z) {
+    int c = first;
+    if (c < end) {
         int cols[8], cols_next[8];
         FRows<VEC> R0, R1;
         load_cols_steps(chunk_cols, c, g, cols);
         load_b_half_f32<VEC, ALIGNED>(B, cols, OL, c0, R0);
-        if (c + W < U.z) load_cols_steps(chunk_cols, c + W, g, cols_next);
-        for (; c < U.z; c += W) {
-            const bool has1 = c + W < U.z;
+        if (c + W < end) load_cols_steps(chunk_cols, c + W, g, cols_next);
+        for (; c < end; c += W) {
+            const bool has1 = c + W < end;
             load_b_half_f32<VEC, ALIGNED>(B, cols + 4, OL, c0, R1);
             const int d = chunk_dense[c];
             floatx4 a_lo, a_hi;
@@ -394,7 +409,7 @@ __global__ __launch_bounds__(64 * W, 3) void k_spmm_f32(const int4* __restrict__
             int cols_after[8];
             if (has1) {
                 load_b_half_f32<VEC, ALIGNED>(B, cols_next, OL, c0, R0);
-                if (c + 2 * W < U.z) load_cols_steps(chunk_cols, c + 2 * W, g, cols_after);
+                if (c + 2 * W < end) load_cols_steps(chunk_cols, c + 2 * W, g, cols_after);
             }
             mfma_half_f32<VEC>(a, 4, cols, R1, acc);
             if (has1) {
@@ -403,68 +418,79 @@ __global__ __launch_bounds__(64 * W, 3) void k_spmm_f32(const int4* __restrict__
             }
         }
     }
-    merge_into_c<TK, W>(acc, 1.0f, U, k0, O, c4, C, P);
 }
 
-// Waves per work-group: enough work-groups in flight to cover the chip (256 CUs x 4 SIMDs,
-// several waves each) while units are few; one wave per unit once units alone fill it.
-static int waves_per_unit(int num_units) {
-    if (num_units >= 8192) return 1;
-    if (num_units >= 4096) return 2;
-    return 4;
-}
-
-template <int TK, int W>
-static void launch_w(const DeviceFormat& F, const void* dB, bool b_f16, int O, float* dC,
-                     hipStream_t st) {
+template <int TK, bool ALIGNED>
+__global__ __launch_bounds__(64 * kWaves, 3) void k_spmm_f32(
+    const int4* __restrict__ units, int num_units, int num_heavy,
+    const int* __restrict__ chunk_eptr, const int* __restrict__ chunk_cols,
+    const int* __restrict__ chunk_dense, const uint32_t* __restrict__ entries,
+    const float* __restrict__ evals, const float* __restrict__ dense_a,
+    const float* __restrict__ B, int O, bool c4, float* __restrict__ C) {
     constexpr int VEC = TK / 16;
-    // Vector loads of B need O % VEC == 0 and a 16-byte aligned base.
-    const bool aligned = (O % VEC) == 0 && ((uintptr_t)dB % 16) == 0;
-    const bool c4 = (O % 4) == 0 && ((uintptr_t)dC % 16) == 0;
-    const dim3 grid((unsigned)(8 * ((F.num_units + 7) / 8)), (unsigned)((O + TK - 1) / TK));
-    const dim3 block(64 * W);
-    if (F.fp32) {
-        const float* B = static_cast<const float*>(dB);
-        if (aligned)
-            hipLaunchKernelGGL((k_spmm_f32<TK, true, W>), grid, block, 0, st, F.units.p,
-                               F.num_units, F.chunk_eptr.p, F.chunk_cols.p, F.chunk_dense.p, F.entries.p,
-                               F.evals.p, F.dense_a32.p, B, O, c4, dC);
-        else
-            hipLaunchKernelGGL((k_spmm_f32<TK, false, W>), grid, block, 0, st, F.units.p,
-                               F.num_units, F.chunk_eptr.p, F.chunk_cols.p, F.chunk_dense.p, F.entries.p,
-                               F.evals.p, F.dense_a32.p, B, O, c4, dC);
-    } else if (b_f16) {
-        const _Float16* B = static_cast<const _Float16*>(dB);
-        if (aligned)
-            hipLaunchKernelGGL((k_spmm_f16<TK, _Float16, true, W>), grid, block, 0, st, F.units.p,
-                               F.num_units, F.chunk_eptr.p, F.chunk_cols.p, F.chunk_dense.p,
-                               F.entries.p, F.dense_a16.p, B, O, F.scale, c4, dC);
-        else
-            hipLaunchKernelGGL((k_spmm_f16<TK, _Float16, false, W>), grid, block, 0, st, F.units.p,
-                               F.num_units, F.chunk_eptr.p, F.chunk_cols.p, F.chunk_dense.p,
-                               F.entries.p, F.dense_a16.p, B, O, F.scale, c4, dC);
-    } else {
-        const float* B = static_cast<const float*>(dB);
-        if (aligned)
-            hipLaunchKernelGGL((k_spmm_f16<TK, float, true, W>), grid, block, 0, st, F.units.p,
-                               F.num_units, F.chunk_eptr.p, F.chunk_cols.p, F.chunk_dense.p,
-                               F.entries.p, F.dense_a16.p, B, O, F.scale, c4, dC);
-        else
-            hipLaunchKernelGGL((k_spmm_f16<TK, float, false, W>), grid, block, 0, st, F.units.p,
-                               F.num_units, F.chunk_eptr.p, F.chunk_cols.p, F.chunk_dense.p,
-                               F.entries.p, F.dense_a16.p, B, O, F.scale, c4, dC);
-    }
-    VCSRMC_HIP(hipGetLastError());
+    __shared__ __attribute__((aligned(16))) float At[kWaves][4 * 16 * 8];
+    __shared__ __attribute__((aligned(16))) float P[kWaves * 16 * TK];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
+    int u;
+    bool heavy;
+    if (!schedule(num_units, num_heavy, wave, u, heavy)) return;
+    const int4 U = units[u];
+    const int k0 = blockIdx.y * TK;
+    const int c0 = k0 + VEC * n;
+    floatx4 acc[VEC];
+#pragma unroll
+    for (int q = 0; q < VEC; ++q) acc[q] = floatx4{0.f, 0.f, 0.f, 0.f};
+    tiles_f32<TK, ALIGNED>(heavy ? U.y + wave : U.y, U.z, heavy ? kWaves : 1, lane, n, g, c0,
+                           (long long)O, chunk_eptr, chunk_cols, chunk_dense, entries, evals,
+                           dense_a, B, At[wave], acc);
+    if (heavy) merge_into_c<TK, kWaves>(acc, 1.0f, U, k0, O, c4, C, P);
+    else merge_into_c<TK, 1>(acc, 1.0f, U, k0, O, c4, C, P);
 }
 
 template <int TK>
 static void launch_tk(const DeviceFormat& F, const void* dB, bool b_f16, int O, float* dC,
                       hipStream_t st) {
-    switch (waves_per_unit(F.num_units)) {
-        case 1: launch_w<TK, 1>(F, dB, b_f16, O, dC, st); break;
-        case 2: launch_w<TK, 2>(F, dB, b_f16, O, dC, st); break;
-        default: launch_w<TK, 4>(F, dB, b_f16, O, dC, st); break;
+    constexpr int VEC = TK / 16;
+    // Vector loads of B need O % VEC == 0 and a 16-byte aligned base.
+    const bool aligned = (O % VEC) == 0 && ((uintptr_t)dB % 16) == 0;
+    const bool c4 = (O % 4) == 0 && ((uintptr_t)dC % 16) == 0;
+    const int h8 = (F.num_heavy + 7) & ~7;
+    const int nlw = (F.num_units - F.num_heavy + kWaves - 1) / kWaves;
+    const dim3 grid((unsigned)(h8 + 8 * ((nlw + 7) / 8)), (unsigned)((O + TK - 1) / TK));
+    const dim3 block(64 * kWaves);
+    const int NU = F.num_units, NH = F.num_heavy;
+    if (F.fp32) {
+        const float* B = static_cast<const float*>(dB);
+        if (aligned)
+            hipLaunchKernelGGL((k_spmm_f32<TK, true>), grid, block, 0, st, F.units.p, NU, NH,
+                               F.chunk_eptr.p, F.chunk_cols.p, F.chunk_dense.p, F.entries.p,
+                               F.evals.p, F.dense_a32.p, B, O, c4, dC);
+        else
+            hipLaunchKernelGGL((k_spmm_f32<TK, false>), grid, block, 0, st, F.units.p, NU, NH,
+                               F.chunk_eptr.p, F.chunk_cols.p, F.chunk_dense.p, F.entries.p,
+                               F.evals.p, F.dense_a32.p, B, O, c4, dC);
+    } else if (b_f16) {
+        const _Float16* B = static_cast<const _Float16*>(dB);
+        if (aligned)
+            hipLaunchKernelGGL((k_spmm_f16<TK, _Float16, true>), grid, block, 0, st, F.units.p, NU,
+                               NH, F.chunk_eptr.p, F.chunk_cols.p, F.chunk_dense.p, F.entries.p,
+                               F.dense_a16.p, B, O, F.scale, c4, dC);
+        else
+            hipLaunchKernelGGL((k_spmm_f16<TK, _Float16, false>), grid, block, 0, st, F.units.p, NU,
+                               NH, F.chunk_eptr.p, F.chunk_cols.p, F.chunk_dense.p, F.entries.p,
+                               F.dense_a16.p, B, O, F.scale, c4, dC);
+    } else {
+        const float* B = static_cast<const float*>(dB);
+        if (aligned)
+            hipLaunchKernelGGL((k_spmm_f16<TK, float, true>), grid, block, 0, st, F.units.p, NU,
+                               NH, F.chunk_eptr.p, F.chunk_cols.p, F.chunk_dense.p, F.entries.p,
+                               F.dense_a16.p, B, O, F.scale, c4, dC);
+        else
+            hipLaunchKernelGGL((k_spmm_f16<TK, float, false>), grid, block, 0, st, F.units.p, NU,
+                               NH, F.chunk_eptr.p, F.chunk_cols.p, F.chunk_dense.p, F.entries.p,
+                               F.dense_a16.p, B, O, F.scale, c4, dC);
     }
+    VCSRMC_HIP(hipGetLastError());
 }
 
 void spmm_launch(const DeviceFormat& F, const void* dB, bool b_f16, int O, int tileK, float* dC,
