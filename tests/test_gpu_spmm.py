@@ -109,19 +109,21 @@ def test_subnormal_fp16_values(orc):
     check(orc, rp, c, v, 64, 64, B, False)
 
 
-def test_upload_path_matches_build_path(orc):
+@pytest.mark.parametrize("fp32", [False, True])
+def test_upload_path_matches_build_path(orc, fp32):
     rng = np.random.default_rng(15)
-    rp, c, v = random_csr(rng, 500, 500, density=0.02)
-    f = orc.build_format(rp, c, v, 500, 500, 16, False)
+    rp, c, v = random_csr(rng, 500, 500, density=0.02, heavy_rows=2, heavy_nnz=300)
+    f = orc.build_format(rp, c, v, 500, 500, 16, fp32)
     V = vm.VCSRMC(M=500, N=500, segw=16, bundle=16, num_segments=f["num_segments"],
-                  scale=float(f["scale"]), fp32=False, **{k: f[k] for k in vm._FMT_ARRAYS})
+                  scale=float(f["scale"]), fp32=fp32, **{k: f[k] for k in vm._FMT_ARRAYS})
     B = rng.uniform(-1, 1, (500, 128)).astype(np.float32)
-    say("upload path")
-    C1, _ = run_spmm(rp, c, v, 500, 500, B, False, segw=16)
-    C2, _ = run_spmm(rp, c, v, 500, 500, B, False, upload=V)
-    _, L1 = orc.spmm_csr(rp, c, v, 500, B, mode=1)
+    say("upload path", fp32)
+    C1, _ = run_spmm(rp, c, v, 500, 500, B, fp32, segw=16)
+    C2, _ = run_spmm(rp, c, v, 500, 500, B, fp32, upload=V)
+    _, L1 = orc.spmm_csr(rp, c, v, 500, B, mode=0 if fp32 else 1)
     ok, worst, _ = row_l1_parity(C1, C2.astype(np.float64), L1, 1e-6)
     assert ok, worst
+    check(orc, rp, c, v, 500, 500, B, fp32, upload=V)
 
 
 def test_empty_matrix():

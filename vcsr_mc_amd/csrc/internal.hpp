@@ -18,6 +18,8 @@ constexpr int kDenseMin = 192;
 // Tiles per heavy unit (shared by the kWaves waves of one work-group).
 constexpr int kHeavyTiles = 64;
 constexpr int kWaves = 4;
+// FP32 panels filled below this many per mille of their tile slots use the VALU row path.
+constexpr int kValuPermille = 0;
 
 // A format on one device.
 //
@@ -35,6 +37,9 @@ constexpr int kWaves = 4;
 //   chunk_cols[32c+k] = column of the chunk's k-th distinct column, -1 past the end
 //   entries[e]      FP16 format: f16 value | row-in-panel << 16 | k << 20
 //                   FP32 format: row-in-panel | k << 4, with the value in evals[e]
+//   units[u].w bit 17 (FP32 formats): the panel is sparse (under 30% of its tile slots filled),
+//                   so the unit runs on VALU FMAs over the panel's rows in csr_rp/csr_col/csr_val
+//                   (the matrix in CSR, value already divided by the scale) instead of MFMA tiles
 //   chunk_dense[c]  -1, or the index of the tile's dense copy when more than kDenseMin of its
 //                   512 slots are filled: dense_a16[512 d + 32 row + k] (FP16), or
 //                   dense_a32[512 d + 128 (k & 3) + 8 row + (k >> 2)] (FP32) -- exactly the
@@ -58,6 +63,8 @@ struct DeviceFormat {
     DevBuf<int> chunk_dense;
     DevBuf<_Float16> dense_a16;
     DevBuf<float> dense_a32;
+    DevBuf<int> csr_rp, csr_col;  // FP32 formats: the matrix in CSR for the VALU units
+    DevBuf<float> csr_val;
 
     bool ready = false;
     void clear() { *this = DeviceFormat(); }

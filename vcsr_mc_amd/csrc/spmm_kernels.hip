@@ -231,7 +231,11 @@ __device__ __forceinline__ void tiles_f16(int first, int end, int W, int lane, i
             load_cols8(chunk_cols, c, g, cols);
             load_b_rows<VEC, TB, ALIGNED>(B, cols, OL, c0, R);
         }
-        if (c + W < end) load_cols8(chunk_cols, c + W, g, cols_next);
+        int d_next = -1;
+        if (c + W < end) {
+            load_cols8(chunk_cols, c + W, g, cols_next);
+            d_next = chunk_dense[c + W];
+        }
         // A state of a tile in 4 registers: the dense operand (8 halves), or the first two
         // nonzeros of this lane and the tile's entry range {w0, w1, eb, ee}.
         int d = chunk_dense[c];
@@ -240,14 +244,16 @@ __device__ __forceinline__ void tiles_f16(int first, int end, int W, int lane, i
         for (; c < end; c += W) {
             const bool has1 = c + W < end;
             BRows<VEC, TB> Rn;
-            int d1 = -1;
             uint4 nxt = {0u, 0u, 0u, 0u};
             int cols_after[8];
+            int d_after = -1;
             if (has1) {
                 load_b_rows<VEC, TB, ALIGNED>(B, cols_next, OL, c0, Rn);
-                d1 = chunk_dense[c + W];
-                nxt = load_a_state(d1, c + W, lane, a_off, chunk_eptr, entries, dense_a);
-                if (c + 2 * W < end) load_cols8(chunk_cols, c + 2 * W, g, cols_after);
+                nxt = load_a_state(d_next, c + W, lane, a_off, chunk_eptr, entries, dense_a);
+                if (c + 2 * W < end) {
+                    load_cols8(chunk_cols, c + 2 * W, g, cols_after);
+                    d_after = chunk_dense[c + 2 * W];
+                }
             }
             half8 a;
             if (d >= 0) {
@@ -275,15 +281,21 @@ __device__ __forceinline__ void tiles_f16(int first, int end, int W, int lane, i
                 R = Rn;
 #pragma unroll
                 for (int i = 0; i < 8; ++i) cols_next[i] = cols_after[i];
-                d = d1;
+                d = d_next;
+                d_next = d_after;
                 cur = nxt;
             }
         }
     }
 }
 
+// Register budget: FP16 B with aligned rows fits three waves per SIMD without spilling; the
+// FP32-B and unaligned variants hold more B data and are given two.
+template <typename TB, bool ALIGNED>
+constexpr int f16_min_waves() { return (sizeof(TB) == 2 && ALIGNED) ? 3 : 2; }
+
 template <int TK, typename TB, bool ALIGNED>
-__global__ __launch_bounds__(64 * kWaves) void k_spmm_f16(
+__global__ __launch_bounds__(64 * kWaves, (f16_min_waves<TB, ALIGNED>())) void k_spmm_f16(
     const int4* __restrict__ units, int num_units, int num_heavy,
     const int* __restrict__ chunk_eptr, const int* __restrict__ chunk_cols,
     const int* __restrict__ chunk_dense, const uint32_t* __restrict__ entries,
@@ -360,6 +372,39 @@ __device__ __forceinline__ void mfma_half_f32(const float (&a)[8], int s0, const
     }
 }
 
+// A state of an FP32 tile in 8 registers: the dense operand (8 floats), or the first two
+// nonzeros of this lane (entry words, values) and the tile's entry range.
+struct AState32 {
+    uint4 x, y;
+};
+
+__device__ __forceinline__ AState32 load_a_state32(int d, int c, int lane, int a_off,
+                                                   const int* __restrict__ chunk_eptr,
+                                                   const uint32_t* __restrict__ entries,
+                                                   const float* __restrict__ evals,
+                                                   const float* __restrict__ dense_a) {
+    AState32 s;
+    if (d >= 0) {
+        s.x = *reinterpret_cast<const uint4*>(dense_a + (long long)d * 512 + a_off);
+        s.y = *reinterpret_cast<const uint4*>(dense_a + (long long)d * 512 + a_off + 4);
+        return s;
+    }
+    const int eb = chunk_eptr[c], ee = chunk_eptr[c + 1];
+    s.x = {0u, 0u, 0u, 0u};
+    s.y = {(unsigned)eb, (unsigned)ee, 0u, 0u};
+    if (eb + lane < ee) { s.x.x = entries[eb + lane]; s.x.z = __float_as_uint(evals[eb + lane]); }
+    if (eb + 64 + lane < ee) {
+        s.x.y = entries[eb + 64 + lane];
+        s.x.w = __float_as_uint(evals[eb + 64 + lane]);
+    }
+    return s;
+}
+
+__device__ __forceinline__ void scatter_a_f32(float* At, uint32_t w, float v) {
+    const int r = w & 15, k = (w >> 4) & 31;
+    At[(k & 3) * 128 + r * 8 + (k >> 2)] = v;
+}
+
 template <int TK, bool ALIGNED>
 __device__ __forceinline__ void tiles_f32(int first, int end, int W, int lane, int n, int g,
                                           int c0, long long OL, const int* __restrict__ chunk_eptr,
@@ -379,25 +424,31 @@ __device__ __forceinline__ void tiles_f32(int first, int end, int W, int lane, i
         FRows<VEC> R0, R1;
         load_cols_steps(chunk_cols, c, g, cols);
         load_b_half_f32<VEC, ALIGNED>(B, cols, OL, c0, R0);
-        if (c + W < end) load_cols_steps(chunk_cols, c + W, g, cols_next);
+        int d_next = -1;
+        if (c + W < end) {
+            load_cols_steps(chunk_cols, c + W, g, cols_next);
+            d_next = chunk_dense[c + W];
+        }
+        int d = chunk_dense[c];
+        AState32 cur = load_a_state32(d, c, lane, a_off, chunk_eptr, entries, evals, dense_a);
         for (; c < end; c += W) {
             const bool has1 = c + W < end;
             load_b_half_f32<VEC, ALIGNED>(B, cols + 4, OL, c0, R1);
-            const int d = chunk_dense[c];
+            AState32 nxt = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};
+            if (has1) nxt = load_a_state32(d_next, c + W, lane, a_off, chunk_eptr, entries, evals,
+                                           dense_a);
             floatx4 a_lo, a_hi;
             if (d >= 0) {
-                a_lo = *reinterpret_cast<const floatx4*>(dense_a + (long long)d * 512 + a_off);
-                a_hi = *reinterpret_cast<const floatx4*>(dense_a + (long long)d * 512 + a_off + 4);
+                a_lo = __builtin_bit_cast(floatx4, cur.x);
+                a_hi = __builtin_bit_cast(floatx4, cur.y);
             } else {
-                const int eb = chunk_eptr[c], ee = chunk_eptr[c + 1];
+                const int eb = (int)cur.y.x, ee = (int)cur.y.y;
                 *reinterpret_cast<floatx4*>(my_a) = floatx4{0.f, 0.f, 0.f, 0.f};
                 *reinterpret_cast<floatx4*>(my_a + 4) = floatx4{0.f, 0.f, 0.f, 0.f};
                 wave_lds_sync();
-                for (int e = eb + lane; e < ee; e += 64) {
-                    const uint32_t w = entries[e];
-                    const int r = w & 15, k = (w >> 4) & 31;
-                    Aw[(k & 3) * 128 + r * 8 + (k >> 2)] = evals[e];
-                }
+                if (eb + lane < ee) scatter_a_f32(Aw, cur.x.x, __uint_as_float(cur.x.z));
+                if (eb + 64 + lane < ee) scatter_a_f32(Aw, cur.x.y, __uint_as_float(cur.x.w));
+                for (int e = eb + 128 + lane; e < ee; e += 64) scatter_a_f32(Aw, entries[e], evals[e]);
                 wave_lds_sync();
                 a_lo = *reinterpret_cast<const floatx4*>(my_a);
                 a_hi = *reinterpret_cast<const floatx4*>(my_a + 4);
@@ -407,14 +458,82 @@ __device__ __forceinline__ void tiles_f32(int first, int end, int W, int lane, i
                                 a_hi[0], a_hi[1], a_hi[2], a_hi[3]};
             mfma_half_f32<VEC>(a, 0, cols, R0, acc);
             int cols_after[8];
+            int d_after = -1;
             if (has1) {
                 load_b_half_f32<VEC, ALIGNED>(B, cols_next, OL, c0, R0);
-                if (c + 2 * W < end) load_cols_steps(chunk_cols, c + 2 * W, g, cols_after);
+                if (c + 2 * W < end) {
+                    load_cols_steps(chunk_cols, c + 2 * W, g, cols_after);
+                    d_after = chunk_dense[c + 2 * W];
+                }
             }
             mfma_half_f32<VEC>(a, 4, cols, R1, acc);
             if (has1) {
 #pragma unroll
                 for (int i = 0; i < 8; ++i) { cols[i] = cols_next[i]; cols_next[i] = cols_after[i]; }
+                d = d_next;
+                d_next = d_after;
+                cur = nxt;
+            }
+        }
+    }
+}
+
+// Sparse FP32 panel on VALU: rows [r_first, r_first + r_count) of the panel, one row at a time
+// from the CSR.  Lane l owns CPL consecutive output columns k0 + CPL l (CPL = 2 at tileK = 128),
+// so every nonzero is one coalesced load of its B row slice plus CPL FMAs; the column index and
+// value are wave-uniform (scalar loads).  The row is added to C once; rows outside the mask
+// are skipped.
+template <int TK, bool ALIGNED>
+__device__ __forceinline__ void rows_f32_valu(const int4& U, int r_first, int r_count, int lane,
+                                              int k0, int O, const int* __restrict__ rp,
+                                              const int* __restrict__ col,
+                                              const float* __restrict__ val,
+                                              const float* __restrict__ B, float* __restrict__ C) {
+    constexpr int CPL = TK >= 64 ? TK / 64 : 1;
+    const int cc = k0 + CPL * lane;
+    const bool active = (TK >= 64 || lane < TK) && cc < O;
+    const long long OL = O;
+    const bool vec = ALIGNED && CPL == 2 && cc + 1 < O;
+    for (int rl = r_first; rl < r_first + r_count; ++rl) {
+        if (!((U.w >> rl) & 1)) continue;
+        const int r = U.x + rl;
+        const int p0 = rp[r], p1 = rp[r + 1];
+        float acc[CPL];
+#pragma unroll
+        for (int q = 0; q < CPL; ++q) acc[q] = 0.0f;
+        auto fma_row = [&](int c, float v) {
+            const float* src = B + (long long)c * OL + cc;
+            if (vec) {
+                const float2 b = *reinterpret_cast<const float2*>(src);
+                acc[0] += v * b.x;
+                acc[CPL - 1] += v * b.y;
+            } else {
+#pragma unroll
+                for (int q = 0; q < CPL; ++q)
+                    if (cc + q < O) acc[q] += v * src[q];
+            }
+        };
+        int p = p0;
+        if (active) {
+            for (; p + 4 <= p1; p += 4) {
+                const int ca = col[p], cb = col[p + 1], ccx = col[p + 2], cd = col[p + 3];
+                const float va = val[p], vb = val[p + 1], vc = val[p + 2], vd = val[p + 3];
+                fma_row(ca, va);
+                fma_row(cb, vb);
+                fma_row(ccx, vc);
+                fma_row(cd, vd);
+            }
+            for (; p < p1; ++p) fma_row(col[p], val[p]);
+            float* crow = C + (long long)r * OL + cc;
+            if (vec) {
+                float2 cv = *reinterpret_cast<float2*>(crow);
+                cv.x += acc[0];
+                cv.y += acc[CPL - 1];
+                *reinterpret_cast<float2*>(crow) = cv;
+            } else {
+#pragma unroll
+                for (int q = 0; q < CPL; ++q)
+                    if (cc + q < O) crow[q] += acc[q];
             }
         }
     }
@@ -426,7 +545,9 @@ __global__ __launch_bounds__(64 * kWaves, 3) void k_spmm_f32(
     const int* __restrict__ chunk_eptr, const int* __restrict__ chunk_cols,
     const int* __restrict__ chunk_dense, const uint32_t* __restrict__ entries,
     const float* __restrict__ evals, const float* __restrict__ dense_a,
-    const float* __restrict__ B, int O, bool c4, float* __restrict__ C) {
+    const int* __restrict__ csr_rp, const int* __restrict__ csr_col,
+    const float* __restrict__ csr_val, const float* __restrict__ B, int O, bool c4,
+    float* __restrict__ C) {
     constexpr int VEC = TK / 16;
     __shared__ __attribute__((aligned(16))) float At[kWaves][4 * 16 * 8];
     __shared__ __attribute__((aligned(16))) float P[kWaves * 16 * TK];
@@ -436,6 +557,11 @@ __global__ __launch_bounds__(64 * kWaves, 3) void k_spmm_f32(
     if (!schedule(num_units, num_heavy, wave, u, heavy)) return;
     const int4 U = units[u];
     const int k0 = blockIdx.y * TK;
+    if ((U.w >> 17) & 1) {  // sparse panel: VALU over its rows (a heavy one: 4 rows per wave)
+        rows_f32_valu<TK, ALIGNED>(U, heavy ? 4 * wave : 0, heavy ? 4 : 16, lane, k0, O, csr_rp,
+                                   csr_col, csr_val, B, C);
+        return;
+    }
     const int c0 = k0 + VEC * n;
     floatx4 acc[VEC];
 #pragma unroll
@@ -464,11 +590,13 @@ static void launch_tk(const DeviceFormat& F, const void* dB, bool b_f16, int O, 
         if (aligned)
             hipLaunchKernelGGL((k_spmm_f32<TK, true>), grid, block, 0, st, F.units.p, NU, NH,
                                F.chunk_eptr.p, F.chunk_cols.p, F.chunk_dense.p, F.entries.p,
-                               F.evals.p, F.dense_a32.p, B, O, c4, dC);
+                               F.evals.p, F.dense_a32.p, F.csr_rp.p, F.csr_col.p, F.csr_val.p, B,
+                               O, c4, dC);
         else
             hipLaunchKernelGGL((k_spmm_f32<TK, false>), grid, block, 0, st, F.units.p, NU, NH,
                                F.chunk_eptr.p, F.chunk_cols.p, F.chunk_dense.p, F.entries.p,
-                               F.evals.p, F.dense_a32.p, B, O, c4, dC);
+                               F.evals.p, F.dense_a32.p, F.csr_rp.p, F.csr_col.p, F.csr_val.p, B,
+                               O, c4, dC);
     } else if (b_f16) {
         const _Float16* B = static_cast<const _Float16*>(dB);
         if (aligned)
