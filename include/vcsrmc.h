@@ -99,6 +99,23 @@ int vcsrmc_download(vcsrmc_t h, int *group_ptr, int *group_depth, int *group_seg
 int vcsrmc_spmm(vcsrmc_t h, const void *dB, int b_dtype, int O, int tileK, float *dC,
                 void *stream, float *ms);
 
+/* Reverse Cuthill-McKee order of the columns of a device CSR (row_ptr[M+1], col[nnz]; any
+ * column order inside a row): d_position[N] receives the new position of every old column,
+ * equal element for element to the reference's rcm_column_order, tie order included
+ * (include/reorder.hpp:17-77).  Computed on the GPU; synchronises `stream`. */
+int vcsrmc_rcm_order(const int *d_row_ptr, const int *d_col, int M, int N, int nnz,
+                     int *d_position, void *stream);
+
+/* Relabels the columns of a device CSR in place, col[p] = position[col[p]], with every row
+ * re-sorted by its new columns (values follow), and, when d_B is non-NULL, writes
+ * d_B_out[position[r], :] = d_B[r, :] (N x O floats, d_B_out distinct from d_B), so that
+ * C = (A P)(P^T B) = A B.  position must be a permutation of 0..N-1 and a row may not hold a
+ * column twice.  Replaces apply_column_permutation (include/reorder.hpp:82-108); synchronises
+ * `stream`. */
+int vcsrmc_apply_column_permutation(const int *d_row_ptr, int *d_col, float *d_val, int M, int N,
+                                    int nnz, const int *d_position, const float *d_B, int O,
+                                    float *d_B_out, void *stream);
+
 /* Text of a status code, and the detail message of the last failing call on this thread. */
 const char *vcsrmc_status_string(int status);
 const char *vcsrmc_last_error(void);

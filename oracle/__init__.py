@@ -76,6 +76,12 @@ def lib():
         L.orc_cpu_spmm_f64_rows.argtypes = [i32p, i32p, f32p, C.c_int, C.c_int, f32p, C.c_int, f64p]
         L.orc_cpu_spmm_f64_omp.argtypes = [i32p, i32p, f32p, C.c_int, C.c_int, f32p, C.c_int, f64p,
                                            C.c_int]
+        L.orc_std_sort_by_key.argtypes = [i32p, C.c_longlong, i32p]
+        L.orc_rcm_order.restype = C.c_int
+        L.orc_rcm_order.argtypes = [i32p, i32p, C.c_int, C.c_int, i32p]
+        L.orc_apply_column_permutation.restype = C.c_int
+        L.orc_apply_column_permutation.argtypes = [i32p, i32p, f32p, C.c_int, C.c_int, i32p, f32p,
+                                                   C.c_int, f32p]
         _lib = L
     return _lib
 
@@ -94,6 +100,11 @@ def ref_lib():
                                 C.c_char_p, C.c_int]
         R.ref_half_scale.restype = C.c_float
         R.ref_half_scale.argtypes = [C.POINTER(C.c_float), C.c_int]
+        i32p, f32p = C.POINTER(C.c_int), C.POINTER(C.c_float)
+        R.ref_std_sort_by_key.argtypes = [i32p, C.c_longlong, i32p]
+        R.ref_rcm_order.argtypes = [i32p, i32p, C.c_int, C.c_int, i32p]
+        R.ref_apply_column_permutation.argtypes = [i32p, i32p, f32p, C.c_int, C.c_int, i32p, f32p,
+                                                   C.c_int]
         _ref = R
     return _ref
 
@@ -275,3 +286,58 @@ def formats_equal(a: Format, b: Format) -> list:
         if x.shape != y.shape or x.tobytes() != y.tobytes():
             bad.append(k)
     return bad
+
+
+# ---- column reordering (rcm_oracle.c; include/reorder.hpp:17-108) ---------------------------
+def std_sort_by_key(a, key) -> np.ndarray:
+    """std::sort(a, a + n, key[x] < key[y]) with libstdc++'s steps (a copy is sorted)."""
+    out = _i32(a).copy()
+    k = _i32(key)
+    lib().orc_std_sort_by_key(_p(out, C.c_int), len(out), _p(k, C.c_int))
+    return out
+
+
+def rcm_order(row_ptr, col, M: int, N: int) -> np.ndarray:
+    rp, ci = _i32(row_ptr), _i32(col)
+    pos = np.zeros(max(N, 1), np.int32)
+    st = lib().orc_rcm_order(_p(rp, C.c_int), _p(ci, C.c_int), int(M), int(N), _p(pos, C.c_int))
+    if st != 0:
+        raise MemoryError("orc_rcm_order")
+    return pos[:N]
+
+
+def apply_column_permutation(row_ptr, col, val, M: int, N: int, position, B=None, O: int = 0):
+    """Returns (col, val, B_out) after the relabelling (B_out None when B is None)."""
+    rp, ci, vv, pos = _i32(row_ptr), _i32(col).copy(), _f32(val).copy(), _i32(position)
+    Bi = _f32(B) if B is not None else None
+    Bo = np.empty_like(Bi) if Bi is not None else None
+    st = lib().orc_apply_column_permutation(
+        _p(rp, C.c_int), _p(ci, C.c_int), _p(vv, C.c_float), int(M), int(N), _p(pos, C.c_int),
+        _p(Bi, C.c_float) if Bi is not None else None, int(O),
+        _p(Bo, C.c_float) if Bo is not None else None)
+    if st != 0:
+        raise MemoryError("orc_apply_column_permutation")
+    return ci, vv, Bo
+
+
+def ref_std_sort_by_key(a, key) -> np.ndarray:
+    out = _i32(a).copy()
+    k = _i32(key)
+    ref_lib().ref_std_sort_by_key(_p(out, C.c_int), len(out), _p(k, C.c_int))
+    return out
+
+
+def ref_rcm_order(row_ptr, col, M: int, N: int) -> np.ndarray:
+    rp, ci = _i32(row_ptr), _i32(col)
+    pos = np.zeros(max(N, 1), np.int32)
+    ref_lib().ref_rcm_order(_p(rp, C.c_int), _p(ci, C.c_int), int(M), int(N), _p(pos, C.c_int))
+    return pos[:N]
+
+
+def ref_apply_column_permutation(row_ptr, col, val, M: int, N: int, position, B=None, O: int = 0):
+    rp, ci, vv, pos = _i32(row_ptr), _i32(col).copy(), _f32(val).copy(), _i32(position)
+    Bi = _f32(B).copy() if B is not None else None
+    ref_lib().ref_apply_column_permutation(_p(rp, C.c_int), _p(ci, C.c_int), _p(vv, C.c_float),
+                                           int(M), int(N), _p(pos, C.c_int),
+                                           _p(Bi, C.c_float) if Bi is not None else None, int(O))
+    return ci, vv, Bi

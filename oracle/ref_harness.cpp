@@ -3,13 +3,17 @@
 // TEST INFRASTRUCTURE ONLY.  oracle/Makefile compiles MuuSeoTia/VCSR_MC's src/vcsr_mc.cu
 // where it lies (with the reference's own HIP flags, CMakeLists.txt:24-27) and links it with
 // this file into oracle/_ref/libvcsrmc_ref.so.  Tests call it on the CPU only (no HIP API is
-// used) to pin the oracle's restatement of csr_to_vcsr_mc (src/vcsr_mc.cu:25-123) and
-// half_scale (src/vcsr_mc.cu:14-22), and to write the golden fixtures under tests/golden/.
+// used) to pin the oracle's restatement of csr_to_vcsr_mc (src/vcsr_mc.cu:25-123),
+// half_scale (src/vcsr_mc.cu:14-22) and the column reordering (include/reorder.hpp, a
+// header-only part of the reference), and to write the golden fixtures under tests/golden/.
 #include <cstdlib>
 #include <cstring>
 #include <exception>
 
+#include <algorithm>
+
 #include "vcsr_formats.hpp"   // the reference's header (include/vcsr_formats.hpp)
+#include "reorder.hpp"        // the reference's header (include/reorder.hpp)
 #include "../oracle/vcsrmc_oracle.h"
 
 namespace {
@@ -62,6 +66,41 @@ float ref_half_scale(const float* val, int nnz) {
     csr.nnz = nnz;
     csr.val.assign(val, val + nnz);
     return half_scale(csr);
+}
+
+// std::sort with the reference's comparator shape (include/reorder.hpp:67-68), as compiled
+// here: pins the oracle's restatement of its steps.
+void ref_std_sort_by_key(int* a, long long n, const int* key) {
+    std::sort(a, a + n, [&](int x, int y) { return key[x] < key[y]; });
+}
+
+static CSR make_csr(const int* row_ptr, const int* col, const float* val, int M, int N) {
+    CSR csr;
+    csr.M = M; csr.N = N; csr.nnz = M ? row_ptr[M] : 0;
+    csr.row_ptr.assign(row_ptr, row_ptr + M + 1);
+    csr.col.assign(col, col + csr.nnz);
+    if (val) csr.val.assign(val, val + csr.nnz);
+    else csr.val.assign(csr.nnz, 1.0f);
+    return csr;
+}
+
+// rcm_column_order (include/reorder.hpp:17-77): position[N].
+void ref_rcm_order(const int* row_ptr, const int* col, int M, int N, int* position) {
+    const std::vector<int> pos = rcm_column_order(make_csr(row_ptr, col, nullptr, M, N));
+    std::copy(pos.begin(), pos.end(), position);
+}
+
+// apply_column_permutation (include/reorder.hpp:82-108): col/val relabelled in place,
+// B (N x O) permuted in place.
+void ref_apply_column_permutation(const int* row_ptr, int* col, float* val, int M, int N,
+                                  const int* position, float* B, int O) {
+    CSR csr = make_csr(row_ptr, col, val, M, N);
+    std::vector<float> hB;
+    if (B) hB.assign(B, B + (size_t)N * O);
+    apply_column_permutation(csr, hB, O, std::vector<int>(position, position + N));
+    std::copy(csr.col.begin(), csr.col.end(), col);
+    std::copy(csr.val.begin(), csr.val.end(), val);
+    if (B) std::copy(hB.begin(), hB.end(), B);
 }
 
 }  // extern "C"

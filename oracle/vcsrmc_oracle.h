@@ -89,6 +89,16 @@ void orc_cpu_spmm_f64_rows(const int *row_ptr, const int *col, const float *val,
 void orc_cpu_spmm_f64_omp(const int *row_ptr, const int *col, const float *val, int r0, int r1,
                           const float *B, int O, double *R, int threads);
 
+/* Column reordering (rcm_oracle.c; include/reorder.hpp:17-108). */
+/* std::sort(a, a + n, key[x] < key[y]) with the steps of GCC 11's libstdc++. */
+void orc_std_sort_by_key(int *a, long long n, const int *key);
+/* rcm_column_order: position[N] = new position of each old column. */
+int orc_rcm_order(const int *row_ptr, const int *col, int M, int N, int *position);
+/* apply_column_permutation: relabels col in place and re-sorts each row (with val); if B and
+ * B_out are non-NULL, B_out[position[r], :] = B[r, :] (N x O). */
+int orc_apply_column_permutation(const int *row_ptr, int *col, float *val, int M, int N,
+                                 const int *position, const float *B, int O, float *B_out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,119 @@
+"""GPU column reordering (vcsrmc_rcm_order / vcsrmc_apply_column_permutation) against the
+oracle's restatement of include/reorder.hpp:17-108 and the committed fixtures made by the
+reference's compiled header: positions, relabelled CSR and permuted B bit for bit."""
+import os
+
+import numpy as np
+import pytest
+
+import vcsr_mc_amd as vm
+from conftest import random_csr
+from gpu_util import dev, say, row_l1_parity
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "rcm_golden.npz")
+
+
+def gpu_rcm(rp, col, M, N):
+    import torch
+    pos = torch.empty(max(N, 1), dtype=torch.int32, device="cuda")
+    vm.rcm_order_device(dev(rp), dev(col), M, N, pos)
+    torch.cuda.synchronize()
+    return pos[:N].cpu().numpy()
+
+
+def gpu_apply(rp, col, val, M, N, pos, B, O):
+    import torch
+    ci, vv = dev(col), dev(val)
+    Bd = dev(np.ascontiguousarray(B, np.float32).reshape(-1))
+    Bo = torch.empty_like(Bd)
+    vm.apply_column_permutation_device(dev(rp), ci, vv, M, N, dev(pos), Bd, Bo, O)
+    torch.cuda.synchronize()
+    return ci.cpu().numpy(), vv.cpu().numpy(), Bo.cpu().numpy().reshape(N, O)
+
+
+def test_rcm_fixtures_gpu():
+    gold = np.load(GOLDEN)
+    for name in gold["cases"]:
+        rp, col = gold[f"{name}/row_ptr"], gold[f"{name}/col"]
+        M, N = (int(x) for x in gold[f"{name}/shape"])
+        say("rcm fixture", name, M, N, col.size)
+        pos = gpu_rcm(rp, col, M, N)
+        assert np.array_equal(pos, gold[f"{name}/position"]), name
+        c2, v2, B2 = gpu_apply(rp, col, gold[f"{name}/val"], M, N, pos, gold[f"{name}/B"], 3)
+        assert np.array_equal(c2, gold[f"{name}/new_col"]), name
+        assert np.array_equal(v2, gold[f"{name}/new_val"]), name
+        assert np.array_equal(B2, gold[f"{name}/new_B"]), name
+
+
+def test_rcm_random_gpu(orc):
+    rng = np.random.default_rng(11)
+    for t in range(40):
+        M, N = int(rng.integers(1, 2000)), int(rng.integers(1, 2000))
+        rp, col, val = random_csr(rng, M, N, nnz_per_row=float(rng.uniform(0, 10)),
+                                  heavy_rows=int(rng.integers(0, 4)), heavy_nnz=400,
+                                  empty_frac=float(rng.uniform(0, 0.5)))
+        say("rcm random", t, M, N, col.size)
+        pos = gpu_rcm(rp, col, M, N)
+        assert np.array_equal(pos, orc.rcm_order(rp, col, M, N)), t
+
+
+@pytest.mark.parametrize("config,size", [(1, 2048), (2, 0), (3, 40), (4, 512), (5, 14)])
+def test_rcm_workloads_gpu(orc, config, size):
+    A = vm.generate(config, size)
+    say("rcm workload", config, size, A.M, A.N, A.nnz)
+    pos = gpu_rcm(A.row_ptr, A.col, A.M, A.N)
+    assert np.array_equal(pos, orc.rcm_order(A.row_ptr, A.col, A.M, A.N))
+    O = 4
+    B = np.random.default_rng(config).uniform(-1, 1, (A.N, O)).astype(np.float32)
+    c2, v2, B2 = gpu_apply(A.row_ptr, A.col, A.val, A.M, A.N, pos, B, O)
+    e2, w2, D2 = orc.apply_column_permutation(A.row_ptr, A.col, A.val, A.M, A.N, pos, B, O)
+    assert np.array_equal(c2, e2) and np.array_equal(v2, w2) and np.array_equal(B2, D2)
+
+
+def test_rcm_no_nonzeros_gpu():
+    # every column isolated: the order is 0..N-1, so position[c] = N - 1 - c
+    N = 37
+    pos = gpu_rcm(np.zeros(6, np.int32), np.zeros(0, np.int32), 5, N)
+    assert np.array_equal(pos, N - 1 - np.arange(N))
+
+
+def test_rcm_errors_gpu():
+    import torch
+    rp = np.array([0, 2, 3], np.int32)
+    col = np.array([0, 5, 1], np.int32)
+    pos = torch.empty(4, dtype=torch.int32, device="cuda")
+    with pytest.raises(vm.VCSRMCError) as e:
+        vm.rcm_order_device(dev(rp), dev(col), 2, 4, pos)  # column 5 >= N
+    assert e.value.status == vm.ERR_CSR
+    col = np.array([0, 1, 1], np.int32)
+    with pytest.raises(vm.VCSRMCError) as e:  # not a permutation
+        vm.apply_column_permutation_device(dev(rp), dev(col), dev(np.ones(3, np.float32)), 2, 4,
+                                           dev(np.array([0, 0, 1, 2], np.int32)))
+    assert e.value.status == vm.ERR_ARG
+    with pytest.raises(vm.VCSRMCError) as e:  # a row holding column 0 twice
+        vm.apply_column_permutation_device(dev(np.array([0, 2], np.int32)),
+                                           dev(np.array([0, 0], np.int32)),
+                                           dev(np.ones(2, np.float32)), 1, 4,
+                                           dev(np.array([3, 2, 1, 0], np.int32)))
+    assert e.value.status == vm.ERR_UNSORTED
+
+
+def test_rcm_then_spmm_gpu(orc):
+    """C = (A P)(P^T B) through the VCSR-MC kernels equals A B (FP32 tolerance)."""
+    import torch
+    A = vm.generate(2, 3000)
+    say("rcm then spmm", A.M, A.N, A.nnz)
+    O = 64
+    B = vm.dense(A.N, O, 5)
+    pos = gpu_rcm(A.row_ptr, A.col, A.M, A.N)
+    c2, v2, B2 = gpu_apply(A.row_ptr, A.col, A.val, A.M, A.N, pos, B, O)
+    with vm.DeviceFormat.from_device_csr(dev(A.row_ptr), dev(c2), dev(v2), A.M, A.N,
+                                         fp32=True, segw=32) as f:
+        Cd = torch.zeros((A.M, O), dtype=torch.float32, device="cuda")
+        f.spmm(dev(B2), Cd, tileK=64)
+        torch.cuda.synchronize()
+    R, L1 = orc.spmm_csr(A.row_ptr, A.col, A.val, A.M, B, mode=0)
+    ok, worst, row = row_l1_parity(Cd.cpu().numpy(), R, L1, 1e-5)
+    assert ok, (worst, row)

@@ -72,11 +72,15 @@ def lib():
         L.vcsrmc_get_info.argtypes = [vp, C.POINTER(_Info)]
         L.vcsrmc_download.argtypes = [vp] + [vp] * 8
         L.vcsrmc_spmm.argtypes = [vp, vp, C.c_int, C.c_int, C.c_int, vp, vp, fp]
+        L.vcsrmc_rcm_order.argtypes = [vp, vp, C.c_int, C.c_int, C.c_int, vp, vp]
+        L.vcsrmc_apply_column_permutation.argtypes = [vp, vp, vp, C.c_int, C.c_int, C.c_int, vp,
+                                                      vp, C.c_int, vp, vp]
         L.vcsrmc_status_string.restype = C.c_char_p
         L.vcsrmc_status_string.argtypes = [C.c_int]
         L.vcsrmc_last_error.restype = C.c_char_p
         for f in ("vcsrmc_create", "vcsrmc_destroy", "vcsrmc_half_scale", "vcsrmc_build_csr",
-                  "vcsrmc_upload", "vcsrmc_get_info", "vcsrmc_download", "vcsrmc_spmm"):
+                  "vcsrmc_upload", "vcsrmc_get_info", "vcsrmc_download", "vcsrmc_spmm",
+                  "vcsrmc_rcm_order", "vcsrmc_apply_column_permutation"):
             getattr(L, f).restype = C.c_int
         _lib_handle = L
     return _lib_handle
@@ -314,6 +318,52 @@ def destroy_vcsr_mc_device(stream=None) -> None:
         _global["fmt"].close()
     _global["fmt"] = None
     _global["uploaded"] = False
+
+
+# ---- column reordering (include/reorder.hpp:17-108), computed on the GPU -------------------
+def rcm_order_device(row_ptr, col, M: int, N: int, position, stream=None) -> None:
+    """Device tensors: position[N] (int32) = new position of every old column."""
+    nnz = int(col.numel())
+    _check(lib().vcsrmc_rcm_order(_ptr(row_ptr), _ptr(col) if nnz else None, int(M), int(N), nnz,
+                                  _ptr(position) if N else None, _stream_ptr(stream)),
+           "rcm_column_order")
+
+
+def apply_column_permutation_device(row_ptr, col, val, M: int, N: int, position, B=None,
+                                    B_out=None, O: int = 0, stream=None) -> None:
+    """Device tensors; col and val relabelled in place, B_out[position[r]] = B[r]."""
+    nnz = int(col.numel())
+    _check(lib().vcsrmc_apply_column_permutation(
+        _ptr(row_ptr), _ptr(col) if nnz else None, _ptr(val) if nnz else None, int(M), int(N),
+        nnz, _ptr(position) if N else None, _ptr(B), int(O), _ptr(B_out), _stream_ptr(stream)),
+        "apply_column_permutation")
+
+
+def rcm_column_order(csr: CSR) -> np.ndarray:
+    """new_position[old_column] of the reverse Cuthill-McKee order (reorder.hpp:17-77)."""
+    import torch
+    rp = torch.from_numpy(np.ascontiguousarray(csr.row_ptr, np.int32)).cuda()
+    ci = torch.from_numpy(np.ascontiguousarray(csr.col, np.int32)).cuda()
+    pos = torch.empty(max(csr.N, 1), dtype=torch.int32, device="cuda")
+    rcm_order_device(rp, ci, csr.M, csr.N, pos)
+    return pos[:csr.N].cpu().numpy()
+
+
+def apply_column_permutation(csr: CSR, hB, O: int, position) -> tuple[CSR, np.ndarray | None]:
+    """(A P, P^T B) of reorder.hpp:82-108; returns the new CSR and B (None if hB is None)."""
+    import torch
+    rp = torch.from_numpy(np.ascontiguousarray(csr.row_ptr, np.int32)).cuda()
+    ci = torch.from_numpy(np.ascontiguousarray(csr.col, np.int32)).cuda()
+    vv = torch.from_numpy(np.ascontiguousarray(csr.val, np.float32)).cuda()
+    pos = torch.from_numpy(np.ascontiguousarray(position, np.int32)).cuda()
+    B = Bo = None
+    if hB is not None:
+        B = torch.from_numpy(np.ascontiguousarray(hB, np.float32).reshape(-1)).cuda()
+        Bo = torch.empty_like(B)
+    apply_column_permutation_device(rp, ci, vv, csr.M, csr.N, pos, B, Bo, O)
+    out = CSR(csr.M, csr.N, csr.nnz, np.array(csr.row_ptr, np.int32), ci.cpu().numpy(),
+              vv.cpu().numpy())
+    return out, (Bo.cpu().numpy().reshape(np.shape(hB)) if hB is not None else None)
 
 
 # ---- workloads (libvcsrmc_bench.so) --------------------------------------------------------

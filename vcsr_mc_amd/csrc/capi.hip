@@ -98,6 +98,22 @@ int vcsrmc_half_scale(const float* d_val, long long nnz, float* scale, void* str
     });
 }
 
+int vcsrmc_rcm_order(const int* d_row_ptr, const int* d_col, int M, int N, int nnz,
+                     int* d_position, void* stream) {
+    return guarded([&] {
+        vcsrmc::rcm_order_device(d_row_ptr, d_col, M, N, nnz, d_position, (hipStream_t)stream);
+    });
+}
+
+int vcsrmc_apply_column_permutation(const int* d_row_ptr, int* d_col, float* d_val, int M, int N,
+                                    int nnz, const int* d_position, const float* d_B, int O,
+                                    float* d_B_out, void* stream) {
+    return guarded([&] {
+        vcsrmc::apply_column_permutation_device(d_row_ptr, d_col, d_val, M, N, nnz, d_position,
+                                                d_B, O, d_B_out, (hipStream_t)stream);
+    });
+}
+
 int vcsrmc_build_csr(vcsrmc_t h, const int* d_row_ptr, const int* d_col, const float* d_val,
                      int M, int N, int nnz, int fp32, int segw, void* stream) {
     return guarded([&] {

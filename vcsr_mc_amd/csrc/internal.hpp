@@ -96,4 +96,14 @@ void build_from_host(DeviceFormat& F, const HostArrays& H, hipStream_t st);
 void spmm_launch(const DeviceFormat& F, const void* dB, bool b_f16, int O, int tileK, float* dC,
                  hipStream_t st);
 
+// Reverse Cuthill-McKee order of the columns of a device CSR (include/reorder.hpp:17-77):
+// position[old column] = new column.  Synchronises `st`.
+void rcm_order_device(const int* rp, const int* col, int M, int N, int nnz, int* position,
+                      hipStream_t st);
+// Column relabelling (include/reorder.hpp:82-108): col and val in place, rows re-sorted by new
+// column; B_out[position[r], :] = B[r, :] when B is given.  Synchronises `st`.
+void apply_column_permutation_device(const int* rp, int* col, float* val, int M, int N, int nnz,
+                                     const int* position, const float* B, int O, float* B_out,
+                                     hipStream_t st);
+
 }  // namespace vcsrmc

@@ -1,0 +1,645 @@
+// reorder.hip -- reverse Cuthill-McKee column order and the column relabelling that goes with
+// it, on the GPU (include/reorder.hpp:17-108 of MuuSeoTia/VCSR_MC).
+//
+// The reference walks the symmetrised pattern breadth-first with one host queue.  Here the
+// same order is produced level by level, every connected component at once:
+//   1. adjacency: the 2 nnz (vertex, neighbour) pairs of the symmetrised pattern, radix-sorted
+//      and deduplicated; the degree counts distinct neighbours, a self-loop included
+//      (reorder.hpp:21-42).
+//   2. rank: vertices in ascending (degree, id) -- the reference's stable_sort of the roots
+//      (reorder.hpp:47-50).
+//   3. components: lock-free union-find that always hooks the root of larger rank under the
+//      root of smaller rank, so each component ends up represented by its lowest-rank vertex,
+//      the root from which the reference's loop (reorder.hpp:54-57) starts that component.
+//   4. levels: level 0 holds every component's root in rank order.  A vertex of level L+1
+//      belongs to the earliest level-L vertex adjacent to it (the one that pops it from the
+//      reference's queue, reorder.hpp:63-66).  A level is ordered by that parent's index, then
+//      inside one parent's children as the reference orders them: ascending id, then
+//      std::sort by degree (reorder.hpp:67-69), whose steps (libstdc++ introsort) one thread per
+//      child group carries out exactly, since equal degrees make the result depend on them.
+//   5. order: vertices sorted by (component rank, level, index in level) give the
+//      Cuthill-McKee order; position = N - 1 - that index (reorder.hpp:72-76).
+#include <algorithm>
+#include <climits>
+#include <cstdint>
+
+#include "../../include/vcsrmc.h"
+#include "internal.hpp"
+
+namespace vcsrmc {
+namespace {
+
+using u64 = unsigned long long;
+
+inline unsigned nblk(long long n) { return grid_for(n, 256); }
+
+#define RLAUNCH(kernel, n, ...)                                                               \
+    do {                                                                                      \
+        if ((n) > 0) {                                                                        \
+            hipLaunchKernelGGL(kernel, dim3(nblk(n)), dim3(256), 0, st, __VA_ARGS__);         \
+            VCSRMC_HIP(hipGetLastError());                                                    \
+        }                                                                                     \
+    } while (0)
+
+enum : int { kBadRowPtr = 1, kBadCol = 2, kBadPerm = 4, kDupCol = 8 };
+
+__global__ void k_check_rp(const int* __restrict__ rp, int M, int nnz, int* __restrict__ err) {
+    const long long r = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (r > M) return;
+    const int a = rp[r];
+    bool bad = a < 0 || a > nnz;
+    if (r == 0) bad |= a != 0;
+    if (r == M) bad |= a != nnz;
+    if (r < M) bad |= rp[r + 1] < a;
+    if (bad) atomicOr(err, kBadRowPtr);
+}
+
+__global__ void k_check_cols(const int* __restrict__ col, long long nnz, int N,
+                             int* __restrict__ err) {
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= nnz) return;
+    const int c = col[i];
+    if (c < 0 || c >= N) atomicOr(err, kBadCol);
+}
+
+void raise_if(const int* d_err, hipStream_t st) {
+    const int e = read_scalar(d_err, st);
+    if (e & kBadRowPtr) throw Error(VCSRMC_ERR_CSR, "row_ptr is not a monotone 0..nnz sequence");
+    if (e & kBadCol) throw Error(VCSRMC_ERR_CSR, "column index out of range [0, N)");
+    if (e & kBadPerm) throw Error(VCSRMC_ERR_ARG, "position is not a permutation of 0..N-1");
+    if (e & kDupCol)
+        throw Error(VCSRMC_ERR_UNSORTED, "a row holds the same column twice");
+}
+
+void check_csr(const int* rp, const int* col, int M, int N, int nnz, int* d_err, hipStream_t st) {
+    VCSRMC_HIP(hipMemsetAsync(d_err, 0, sizeof(int), st));
+    RLAUNCH(k_check_rp, (long long)M + 1, rp, M, nnz, d_err);
+    RLAUNCH(k_check_cols, (long long)nnz, col, (long long)nnz, N, d_err);
+    raise_if(d_err, st);
+}
+
+// ---- 1. adjacency ------------------------------------------------------------------------
+// Nonzero (r, c) contributes r -> c and c -> r when r < N; a row r >= N has no vertex of its
+// own and makes c its own neighbour (twice, merged by the deduplication).
+__global__ void k_adj_pairs(const int* __restrict__ row_of, const int* __restrict__ col,
+                            long long nnz, int N, int nb, u64* __restrict__ key) {
+    const long long p = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (p >= nnz) return;
+    const int r = row_of[p], c = col[p];
+    const bool own = r < N;
+    key[2 * p] = own ? ((u64)r << nb | (u64)c) : ((u64)c << nb | (u64)c);
+    key[2 * p + 1] = (u64)c << nb | (u64)(own ? r : c);
+}
+
+__global__ void k_unique_flags(const u64* __restrict__ key, long long n, int* __restrict__ flag) {
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) flag[i] = (i == 0 || key[i] != key[i - 1]) ? 1 : 0;
+}
+
+__global__ void k_unique_write(const u64* __restrict__ key, const int* __restrict__ flag,
+                               const long long* __restrict__ pos, long long n, int nb,
+                               int* __restrict__ adj_u, int* __restrict__ adj) {
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n || !flag[i]) return;
+    const u64 k = key[i];
+    const long long p = pos[i];
+    adj_u[p] = (int)(k >> nb);
+    adj[p] = (int)(k & ((1ull << nb) - 1));
+}
+
+// head[v] = first adjacency entry of vertex v (lower bound in the sorted adj_u), v in [0, N].
+__global__ void k_heads(const int* __restrict__ adj_u, long long E, int N,
+                        long long* __restrict__ head) {
+    const long long v = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (v > N) return;
+    long long lo = 0, hi = E;
+    while (lo < hi) {
+        const long long mid = (lo + hi) >> 1;
+        if (adj_u[mid] < v) lo = mid + 1;
+        else hi = mid;
+    }
+    head[v] = lo;
+}
+
+// ---- 2. rank -----------------------------------------------------------------------------
+__global__ void k_rank_keys(const long long* __restrict__ head, int N, int nb,
+                            u64* __restrict__ key, uint32_t* __restrict__ val) {
+    const long long v = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (v >= N) return;
+    key[v] = (u64)(head[v + 1] - head[v]) << nb | (u64)v;
+    val[v] = (uint32_t)v;
+}
+
+__global__ void k_scatter_rank(const uint32_t* __restrict__ order, int N, int* __restrict__ rank) {
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < N) rank[order[i]] = (int)i;
+}
+
+// ---- 3. components -----------------------------------------------------------------------
+// parent[] only ever points to a vertex of smaller rank (hooks) or to an ancestor (path
+// halving), so chains strictly decrease in rank and every walk ends at a root.  A root's
+// parent changes only through a successful compare-and-swap; a vertex seen as a non-root
+// never becomes a root again, so the halving store never races with a hook of the same slot.
+__device__ __forceinline__ int uf_load(const int* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ int uf_root(int* parent, int x) {
+    for (;;) {
+        const int p = uf_load(parent + x);
+        if (p == x) return x;
+        const int gp = uf_load(parent + p);
+        if (gp == p) return p;
+        __hip_atomic_store(parent + x, gp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        x = gp;
+    }
+}
+
+__global__ void k_uf_init(int* __restrict__ parent, int N) {
+    const long long v = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (v < N) parent[v] = (int)v;
+}
+
+__global__ void k_uf_hook(const int* __restrict__ adj_u, const int* __restrict__ adj, long long E,
+                          const int* __restrict__ rank, int* parent) {
+    const long long e = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= E) return;
+    int u = adj_u[e], w = adj[e];
+    if (u >= w) return;  // each undirected edge once; self-loops join nothing
+    for (;;) {
+        int a = uf_root(parent, u), b = uf_root(parent, w);
+        if (a == b) return;
+        if (rank[a] > rank[b]) { const int t = a; a = b; b = t; }
+        int expected = b;
+        if (__hip_atomic_compare_exchange_strong(parent + b, &expected, a, __ATOMIC_RELAXED,
+                                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
+            return;
+        u = a;
+        w = b;  // b gained a parent meanwhile: retry from the two old roots
+    }
+}
+
+__global__ void k_uf_flatten(int* parent, int N) {
+    const long long v = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (v < N) {
+        const int r = uf_root(parent, (int)v);
+        __hip_atomic_store(parent + v, r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+// ---- 4. levels ---------------------------------------------------------------------------
+__global__ void k_root_flags(const uint32_t* __restrict__ order, const int* __restrict__ parent,
+                             int N, int* __restrict__ flag) {
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < N) flag[i] = parent[order[i]] == (int)order[i] ? 1 : 0;
+}
+
+__global__ void k_root_list(const uint32_t* __restrict__ order, const int* __restrict__ flag,
+                            const long long* __restrict__ pos, int N, int* __restrict__ front,
+                            int* __restrict__ lev, int* __restrict__ seq) {
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= N || !flag[i]) return;
+    const int v = (int)order[i];
+    const int p = (int)pos[i];
+    front[p] = v;
+    lev[v] = 0;
+    seq[v] = p;
+}
+
+__global__ void k_front_degree(const int* __restrict__ front, int f,
+                               const long long* __restrict__ head, long long* __restrict__ fdeg) {
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < f) {
+        const int v = front[i];
+        fdeg[i] = head[v + 1] - head[v];
+    }
+}
+
+// One thread per (frontier vertex, neighbour) edge.  An unvisited neighbour keeps the smallest
+// frontier index that reaches it; the thread that claims it first appends it to `next`
+// (wave-aggregated counter).  The order of `next` is fixed afterwards by a sort.
+__global__ void k_claim(const int* __restrict__ front, const long long* __restrict__ fofs, int f,
+                        long long Ef, const long long* __restrict__ head,
+                        const int* __restrict__ adj, const int* __restrict__ lev,
+                        int* __restrict__ claim, int* __restrict__ next,
+                        int* __restrict__ count) {
+    const long long e = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    bool first = false;
+    int u = 0;
+    if (e < Ef) {
+        int lo = 0, hi = f;  // largest i with fofs[i] <= e
+        while (hi - lo > 1) {
+            const int mid = (lo + hi) >> 1;
+            if (fofs[mid] <= e) lo = mid;
+            else hi = mid;
+        }
+        const int v = front[lo];
+        u = adj[head[v] + (e - fofs[lo])];
+        if (lev[u] < 0) first = atomicMin(&claim[u], lo) == INT_MAX;
+    }
+    const u64 m = __ballot(first);
+    if (m == 0) return;
+    const int leader = __ffsll((long long)m) - 1;
+    int base = 0;
+    if (lane_id() == leader) base = atomicAdd(count, __popcll(m));
+    base = __shfl(base, leader);
+    if (first) {
+        const u64 below = lane_id() ? (~0ull >> (64 - lane_id())) : 0ull;
+        next[base + __popcll(m & below)] = u;
+    }
+}
+
+__global__ void k_next_keys(const int* __restrict__ next, int n, const int* __restrict__ claim,
+                            int nb, u64* __restrict__ key, uint32_t* __restrict__ val) {
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const int u = next[i];
+    key[i] = (u64)claim[u] << nb | (u64)u;
+    val[i] = (uint32_t)u;
+}
+
+__global__ void k_group_flags(const u64* __restrict__ key, int n, int nb, int* __restrict__ flag) {
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) flag[i] = (i == 0 || (key[i] >> nb) != (key[i - 1] >> nb)) ? 1 : 0;
+}
+
+// Children in (parent, ascending id) order, packed as degree << 32 | id for the group sort.
+__global__ void k_group_pack(const int* __restrict__ flag, const long long* __restrict__ pos,
+                             const uint32_t* __restrict__ val, int n,
+                             const long long* __restrict__ head, int* __restrict__ gstart,
+                             u64* __restrict__ packed) {
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    if (flag[i]) gstart[pos[i]] = (int)i;
+    const uint32_t u = val[i];
+    packed[i] = (u64)(head[u + 1] - head[u]) << 32 | (u64)u;
+}
+
+// std::sort(first, last, [](a, b) { return degree[a] < degree[b]; }) with the steps of GCC 11's
+// libstdc++ (introsort: median-of-three Hoare partitions while a range holds more than 16
+// elements, heapsort once 2 floor(lg n) partition levels are used up, then one insertion pass).
+// The scans carry bounds checks the library omits; they never fire, as the median-of-three
+// pivot and the insertion pass's leftmost minimum stop every scan inside its range.
+__device__ __forceinline__ uint32_t skey(u64 x) { return (uint32_t)(x >> 32); }
+
+__device__ void ls_insert(u64* a, long long lo, long long pos) {
+    const u64 v = a[pos];
+    while (pos > lo && skey(v) < skey(a[pos - 1])) {
+        a[pos] = a[pos - 1];
+        --pos;
+    }
+    a[pos] = v;
+}
+
+__device__ void ls_sift(u64* a, long long base, long long hole, long long len, u64 v) {
+    const long long top = hole;
+    long long child = hole;
+    while (child < (len - 1) / 2) {
+        child = 2 * child + 2;
+        if (skey(a[base + child]) < skey(a[base + child - 1])) --child;
+        a[base + hole] = a[base + child];
+        hole = child;
+    }
+    if ((len & 1) == 0 && child == (len - 2) / 2) {
+        child = 2 * child + 2;
+        a[base + hole] = a[base + child - 1];
+        hole = child - 1;
+    }
+    long long parent = (hole - 1) / 2;
+    while (hole > top && skey(a[base + parent]) < skey(v)) {
+        a[base + hole] = a[base + parent];
+        hole = parent;
+        parent = (hole - 1) / 2;
+    }
+    a[base + hole] = v;
+}
+
+__device__ void ls_heapsort(u64* a, long long lo, long long hi) {
+    const long long len = hi - lo;
+    if (len >= 2)
+        for (long long parent = (len - 2) / 2;; --parent) {
+            ls_sift(a, lo, parent, len, a[lo + parent]);
+            if (parent == 0) break;
+        }
+    for (long long end = hi - 1; end - lo > 0; --end) {
+        const u64 v = a[end];
+        a[end] = a[lo];
+        ls_sift(a, lo, 0, end - lo, v);
+    }
+}
+
+__device__ __forceinline__ void ls_swap(u64* a, long long i, long long j) {
+    const u64 t = a[i];
+    a[i] = a[j];
+    a[j] = t;
+}
+
+__device__ void ls_median_to_first(u64* a, long long dst, long long x, long long y, long long z) {
+    const uint32_t kx = skey(a[x]), ky = skey(a[y]), kz = skey(a[z]);
+    if (kx < ky) {
+        if (ky < kz) ls_swap(a, dst, y);
+        else if (kx < kz) ls_swap(a, dst, z);
+        else ls_swap(a, dst, x);
+    } else if (kx < kz) {
+        ls_swap(a, dst, x);
+    } else if (ky < kz) {
+        ls_swap(a, dst, z);
+    } else {
+        ls_swap(a, dst, y);
+    }
+}
+
+__device__ long long ls_partition(u64* a, long long lo, long long hi, long long piv) {
+    const uint32_t kp = skey(a[piv]);
+    const long long end = hi;
+    for (;;) {
+        while (lo < end && skey(a[lo]) < kp) ++lo;
+        --hi;
+        while (hi > piv && kp < skey(a[hi])) --hi;
+        if (!(lo < hi)) return lo;
+        ls_swap(a, lo, hi);
+        ++lo;
+    }
+}
+
+struct SortRange {
+    int lo, hi, depth;
+};
+
+__device__ void ls_std_sort(u64* a, int n) {
+    if (n <= 1) return;
+    int lg = 0;
+    while ((2ll << lg) <= n) ++lg;
+    SortRange stack[64];
+    int sp = 0;
+    stack[sp++] = {0, n, 2 * lg};
+    while (sp > 0) {
+        const SortRange r = stack[--sp];
+        long long lo = r.lo, hi = r.hi;
+        int depth = r.depth;
+        while (hi - lo > 16) {
+            if (depth == 0) {
+                ls_heapsort(a, lo, hi);
+                break;
+            }
+            --depth;
+            ls_median_to_first(a, lo, lo + 1, lo + (hi - lo) / 2, hi - 1);
+            const long long cut = ls_partition(a, lo + 1, hi, lo);
+            if (sp < 64) stack[sp++] = {(int)cut, (int)hi, depth};
+            hi = cut;
+        }
+    }
+    const int head = n > 16 ? 16 : n;
+    for (int i = 1; i < head; ++i) ls_insert(a, 0, i);
+    for (int i = 16; i < n; ++i) ls_insert(a, 0, i);
+}
+
+__global__ void k_group_sort(const int* __restrict__ gstart, int ngroups, int n,
+                             u64* __restrict__ packed) {
+    const long long g = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (g >= ngroups) return;
+    const int b = gstart[g], e = g + 1 < ngroups ? gstart[g + 1] : n;
+    ls_std_sort(packed + b, e - b);
+}
+
+__global__ void k_level_write(const u64* __restrict__ packed, int n, int level, int base,
+                              int* __restrict__ front, int* __restrict__ lev,
+                              int* __restrict__ seq) {
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const int u = (int)(uint32_t)packed[i];
+    front[i] = u;
+    lev[u] = level;
+    seq[u] = base + (int)i;
+}
+
+// ---- 5. order ----------------------------------------------------------------------------
+__global__ void k_order_keys(const int* __restrict__ parent, const int* __restrict__ rank,
+                             const int* __restrict__ seq, int N, int nb, u64* __restrict__ key,
+                             uint32_t* __restrict__ val) {
+    const long long v = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (v >= N) return;
+    key[v] = (u64)rank[parent[v]] << nb | (u64)seq[v];
+    val[v] = (uint32_t)v;
+}
+
+__global__ void k_positions(const uint32_t* __restrict__ order, int N, int* __restrict__ position) {
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < N) position[order[i]] = N - 1 - (int)i;
+}
+
+// ---- relabelling -------------------------------------------------------------------------
+__global__ void k_perm_check(const int* __restrict__ position, int N, int* __restrict__ seen,
+                             int* __restrict__ err) {
+    const long long v = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (v >= N) return;
+    const int p = position[v];
+    if (p < 0 || p >= N || atomicAdd(&seen[p], 1) != 0) atomicOr(err, kBadPerm);
+}
+
+__global__ void k_relabel_keys(const int* __restrict__ row_of, const int* __restrict__ col,
+                               const int* __restrict__ position, long long nnz, int nb,
+                               u64* __restrict__ key, uint32_t* __restrict__ val) {
+    const long long p = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (p >= nnz) return;
+    key[p] = (u64)row_of[p] << nb | (u64)position[col[p]];
+    val[p] = (uint32_t)p;
+}
+
+__global__ void k_relabel_write(const u64* __restrict__ key, const uint32_t* __restrict__ src,
+                                const float* __restrict__ vin, long long nnz, int nb,
+                                int* __restrict__ col, float* __restrict__ vout,
+                                int* __restrict__ err) {
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= nnz) return;
+    const u64 k = key[i];
+    if (i > 0 && key[i - 1] == k) atomicOr(err, kDupCol);
+    col[i] = (int)(k & ((1ull << nb) - 1));
+    vout[i] = vin[src[i]];
+}
+
+// B_out[position[r], :] = B[r, :]; one thread per element, rows of O consecutive floats.
+__global__ void k_permute_rows(const float* __restrict__ B, const int* __restrict__ position,
+                               int N, int O, float* __restrict__ Bout) {
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (long long)N * O) return;
+    const long long r = i / O, k = i - r * O;
+    Bout[(long long)position[r] * O + k] = B[i];
+}
+
+__global__ void k_mark_heads(const int* __restrict__ rp, int M, int* __restrict__ head) {
+    const long long r = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (r >= M) return;
+    const int a = rp[r];
+    if (a < rp[r + 1]) head[a] = (int)r;
+}
+
+// Row of every nonzero: each non-empty row marks its first slot, a running max fills the rest.
+void row_of_nonzeros(const int* rp, int M, int nnz, int* row_of, hipStream_t st) {
+    DevBuf<int> headmark(nnz);
+    fill<int>(headmark.p, nnz, (int)0x80000000, st);
+    RLAUNCH(k_mark_heads, M, rp, M, headmark.p);
+    inclusive_max(headmark.p, row_of, nnz, st);
+}
+
+}  // namespace
+
+void rcm_order_device(const int* rp, const int* col, int M, int N, int nnz, int* position,
+                      hipStream_t st) {
+    if (M < 0 || N < 0 || nnz < 0) throw Error(VCSRMC_ERR_ARG, "negative matrix size");
+    if (!rp || (nnz > 0 && !col) || (N > 0 && !position))
+        throw Error(VCSRMC_ERR_ARG, "null pointer");
+    if (2ll * nnz >= (1ll << 31))
+        throw Error(VCSRMC_ERR_OVERFLOW, "rcm ordering handles fewer than 2^30 nonzeros");
+    DevBuf<int> err(1);
+    check_csr(rp, col, M, N, nnz, err.p, st);
+    if (N == 0) return;
+
+    const int nb = std::max(1, bits_for((u64)N));  // holds 0..N
+    // 1. adjacency
+    DevBuf<int> adj_u, adj;
+    DevBuf<long long> head((size_t)N + 1);
+    long long E = 0;
+    {
+        const long long P = 2ll * nnz;
+        DevBuf<int> row_of(nnz);
+        if (nnz) row_of_nonzeros(rp, M, nnz, row_of.p, st);
+        DevBuf<u64> k1(P), k2(P);
+        DevBuf<uint32_t> v1(P), v2(P);
+        RLAUNCH(k_adj_pairs, nnz, row_of.p, col, (long long)nnz, N, nb, k1.p);
+        row_of.release();
+        u64 *ka = k1.p, *kb = k2.p;
+        uint32_t *va = v1.p, *vb = v2.p;
+        radix_sort_pairs<u64>(ka, va, kb, vb, P, 2 * nb, st);
+        DevBuf<int> flag(P);
+        DevBuf<long long> pos(P + 1);
+        RLAUNCH(k_unique_flags, P, ka, P, flag.p);
+        exclusive_sum<int, long long>(flag.p, pos.p, P, st);
+        E = P ? read_scalar(pos.p + P, st) : 0;
+        adj_u.alloc(E);
+        adj.alloc(E);
+        RLAUNCH(k_unique_write, P, ka, flag.p, pos.p, P, nb, adj_u.p, adj.p);
+    }
+    RLAUNCH(k_heads, (long long)N + 1, adj_u.p, E, N, head.p);
+
+    // 2. rank
+    DevBuf<uint32_t> order(N);
+    DevBuf<int> rank(N);
+    {
+        DevBuf<u64> k1(N), k2(N);
+        DevBuf<uint32_t> v2(N);
+        RLAUNCH(k_rank_keys, N, head.p, N, nb, k1.p, order.p);
+        u64 *ka = k1.p, *kb = k2.p;
+        uint32_t *va = order.p, *vb = v2.p;
+        radix_sort_pairs<u64>(ka, va, kb, vb, N, 2 * nb, st);
+        if (va != order.p)
+            VCSRMC_HIP(hipMemcpyAsync(order.p, va, sizeof(uint32_t) * (size_t)N,
+                                      hipMemcpyDeviceToDevice, st));
+        RLAUNCH(k_scatter_rank, N, order.p, N, rank.p);
+    }
+
+    // 3. components
+    DevBuf<int> parent(N);
+    RLAUNCH(k_uf_init, N, parent.p, N);
+    RLAUNCH(k_uf_hook, E, adj_u.p, adj.p, E, rank.p, parent.p);
+    RLAUNCH(k_uf_flatten, N, parent.p, N);
+    adj_u.release();
+
+    // 4. levels
+    DevBuf<int> lev(N), seq(N), claim(N), front(N), next(N), count(1);
+    fill<int>(lev.p, N, -1, st);
+    fill<int>(claim.p, N, INT_MAX, st);
+    int f = 0;
+    {
+        DevBuf<int> flag(N);
+        DevBuf<long long> pos((size_t)N + 1);
+        RLAUNCH(k_root_flags, N, order.p, parent.p, N, flag.p);
+        exclusive_sum<int, long long>(flag.p, pos.p, N, st);
+        f = (int)read_scalar(pos.p + N, st);
+        RLAUNCH(k_root_list, N, order.p, flag.p, pos.p, N, front.p, lev.p, seq.p);
+    }
+    DevBuf<long long> fdeg(N), fofs((size_t)N + 1);
+    DevBuf<u64> k1(N), k2(N);
+    DevBuf<uint32_t> v1(N), v2(N);
+    DevBuf<int> gflag(N), gstart(N);
+    DevBuf<long long> gpos((size_t)N + 1);
+    int base = f;
+    for (int level = 1; f > 0 && base < N; ++level) {
+        RLAUNCH(k_front_degree, f, front.p, f, head.p, fdeg.p);
+        exclusive_sum<long long, long long>(fdeg.p, fofs.p, f, st);
+        const long long Ef = read_scalar(fofs.p + f, st);
+        if (Ef == 0) break;
+        VCSRMC_HIP(hipMemsetAsync(count.p, 0, sizeof(int), st));
+        RLAUNCH(k_claim, Ef, front.p, fofs.p, f, Ef, head.p, adj.p, lev.p, claim.p, next.p,
+                count.p);
+        const int n = read_scalar(count.p, st);
+        if (n == 0) break;
+        const int cb = std::max(1, bits_for((u64)(f - 1)));
+        RLAUNCH(k_next_keys, n, next.p, n, claim.p, nb, k1.p, v1.p);
+        u64 *ka = k1.p, *kb = k2.p;
+        uint32_t *va = v1.p, *vb = v2.p;
+        radix_sort_pairs<u64>(ka, va, kb, vb, n, nb + cb, st);
+        RLAUNCH(k_group_flags, n, ka, n, nb, gflag.p);
+        exclusive_sum<int, long long>(gflag.p, gpos.p, n, st);
+        const int ngroups = (int)read_scalar(gpos.p + n, st);
+        u64* packed = kb;  // free half of the key double buffer
+        RLAUNCH(k_group_pack, n, gflag.p, gpos.p, va, n, head.p, gstart.p, packed);
+        RLAUNCH(k_group_sort, ngroups, gstart.p, ngroups, n, packed);
+        RLAUNCH(k_level_write, n, packed, n, level, base, front.p, lev.p, seq.p);
+        base += n;
+        f = n;
+    }
+    if (base != N) throw Error(VCSRMC_ERR_STATE, "rcm ordering left vertices unvisited");
+
+    // 5. order
+    {
+        RLAUNCH(k_order_keys, N, parent.p, rank.p, seq.p, N, nb, k1.p, v1.p);
+        u64 *ka = k1.p, *kb = k2.p;
+        uint32_t *va = v1.p, *vb = v2.p;
+        radix_sort_pairs<u64>(ka, va, kb, vb, N, 2 * nb, st);
+        RLAUNCH(k_positions, N, va, N, position);
+    }
+    VCSRMC_HIP(hipStreamSynchronize(st));
+}
+
+void apply_column_permutation_device(const int* rp, int* col, float* val, int M, int N, int nnz,
+                                     const int* position, const float* B, int O, float* B_out,
+                                     hipStream_t st) {
+    if (M < 0 || N < 0 || nnz < 0 || O < 0) throw Error(VCSRMC_ERR_ARG, "negative size");
+    if (!rp || (nnz > 0 && (!col || !val)) || (N > 0 && !position))
+        throw Error(VCSRMC_ERR_ARG, "null pointer");
+    if ((B == nullptr) != (B_out == nullptr))
+        throw Error(VCSRMC_ERR_ARG, "B and B_out must both be given or both be NULL");
+    if (B && B == B_out) throw Error(VCSRMC_ERR_ARG, "B_out must not alias B");
+    DevBuf<int> err(1);
+    check_csr(rp, col, M, N, nnz, err.p, st);
+    if (N > 0) {
+        DevBuf<int> seen(N);
+        VCSRMC_HIP(hipMemsetAsync(seen.p, 0, sizeof(int) * (size_t)N, st));
+        RLAUNCH(k_perm_check, N, position, N, seen.p, err.p);
+        raise_if(err.p, st);
+    }
+    if (nnz > 0) {
+        const int nb = std::max(1, bits_for((u64)N));
+        const int mb = std::max(1, bits_for((u64)M));
+        DevBuf<int> row_of(nnz);
+        row_of_nonzeros(rp, M, nnz, row_of.p, st);
+        DevBuf<u64> k1(nnz), k2(nnz);
+        DevBuf<uint32_t> v1(nnz), v2(nnz);
+        RLAUNCH(k_relabel_keys, nnz, row_of.p, col, position, (long long)nnz, nb, k1.p, v1.p);
+        row_of.release();
+        u64 *ka = k1.p, *kb = k2.p;
+        uint32_t *va = v1.p, *vb = v2.p;
+        radix_sort_pairs<u64>(ka, va, kb, vb, nnz, nb + mb, st);
+        DevBuf<float> vcopy(nnz);
+        VCSRMC_HIP(hipMemcpyAsync(vcopy.p, val, sizeof(float) * (size_t)nnz,
+                                  hipMemcpyDeviceToDevice, st));
+        RLAUNCH(k_relabel_write, nnz, ka, va, vcopy.p, (long long)nnz, nb, col, val, err.p);
+        raise_if(err.p, st);
+    }
+    if (B && N > 0 && O > 0)
+        RLAUNCH(k_permute_rows, (long long)N * O, B, position, N, O, B_out);
+    VCSRMC_HIP(hipStreamSynchronize(st));
+}
+
+}  // namespace vcsrmc

@@ -1,9 +1,11 @@
-// vcsr_formats.hip -- the reference's C++ surface (include/vcsr_formats.hpp) over the C ABI.
+// vcsr_formats.hip -- the reference's C++ surface (include/vcsr_formats.hpp, include/reorder.hpp)
+// over the C ABI.
 #include <cstdio>
 #include <cstdlib>
 #include <stdexcept>
 #include <string>
 
+#include "../../include/reorder.hpp"
 #include "../../include/vcsr_formats.hpp"
 #include "../../include/vcsrmc.h"
 
@@ -38,7 +40,15 @@ struct Dev {
             hip_check(hipMemcpy(p, h.data(), sizeof(T) * h.size(), hipMemcpyHostToDevice),
                       "hipMemcpy");
     }
+    explicit Dev(size_t n) {
+        hip_check(hipMalloc((void**)&p, sizeof(T) * (n ? n : 1)), "hipMalloc");
+    }
     ~Dev() { if (p) (void)hipFree(p); }
+    void to_host(std::vector<T>& h) const {
+        if (!h.empty())
+            hip_check(hipMemcpy(h.data(), p, sizeof(T) * h.size(), hipMemcpyDeviceToHost),
+                      "hipMemcpy");
+    }
 };
 
 }  // namespace
@@ -112,4 +122,36 @@ void destroy_vcsr_mc_device(hipStream_t) {
     if (g_handle) check(vcsrmc_destroy(g_handle), "destroy_vcsr_mc_device");
     g_handle = nullptr;
     g_uploaded = false;
+}
+
+std::vector<int> rcm_column_order(const CSR& csr) {
+    Dev<int> rp(csr.row_ptr), ci(csr.col);
+    Dev<int> pos((size_t)csr.N);
+    check(vcsrmc_rcm_order(rp.p, ci.p, csr.M, csr.N, csr.nnz, pos.p, nullptr), "rcm_column_order");
+    std::vector<int> position((size_t)csr.N);
+    pos.to_host(position);
+    return position;
+}
+
+void apply_column_permutation(CSR& csr, std::vector<float>& hB, int O,
+                              const std::vector<int>& position) {
+    if ((int)position.size() != csr.N)
+        throw std::runtime_error("apply_column_permutation: position must hold N entries");
+    if (!hB.empty() && hB.size() != (size_t)csr.N * (size_t)O)
+        throw std::runtime_error("apply_column_permutation: B must hold N x O values");
+    Dev<int> rp(csr.row_ptr), ci(csr.col), pos(position);
+    Dev<float> vv(csr.val);
+    if (hB.empty()) {
+        check(vcsrmc_apply_column_permutation(rp.p, ci.p, vv.p, csr.M, csr.N, csr.nnz, pos.p,
+                                              nullptr, O, nullptr, nullptr),
+              "apply_column_permutation");
+    } else {
+        Dev<float> b(hB), bout(hB.size());
+        check(vcsrmc_apply_column_permutation(rp.p, ci.p, vv.p, csr.M, csr.N, csr.nnz, pos.p,
+                                              b.p, O, bout.p, nullptr),
+              "apply_column_permutation");
+        bout.to_host(hB);
+    }
+    ci.to_host(csr.col);
+    vv.to_host(csr.val);
 }
