@@ -48,8 +48,8 @@ def test_cli_errors(tmp_path):
     assert r.returncode == 2 and "Unknown algorithm" in r.stderr
     r = run(["--gen", "2:100", "--tileK", "48"])
     assert r.returncode == 2 and "tileK" in r.stderr
-    r = run(["--gen", "2:100", "--reorder", "rcm"])
-    assert r.returncode == 2 and "reordering" in r.stderr
+    r = run(["--gen", "2:100", "--reorder", "amd"])
+    assert r.returncode == 2 and "Unknown reordering" in r.stderr
 
 
 @pytest.mark.gpu
@@ -75,6 +75,12 @@ def test_all_algorithms_pass_cpu_check(tmp_path):
         for x in rows:
             assert x["validation"] == "pass", x
             assert float(x["ms"]) > 0 and float(x["gflops"]) > 0
+    print("[case] driver mtx rcm", flush=True)
+    r = run(["--mtx", str(p), "--O", "64", "--segw", "32", "--tileK", "64", "--reorder", "rcm",
+             "--check", "cpu", "--csv", "--bdist", "normal", "--repeat", "2"])
+    assert r.returncode == 0, r.stderr
+    rows = list(csv.DictReader(io.StringIO(r.stdout)))
+    assert len(rows) == 4 and all(x["validation"] == "pass" for x in rows), rows
     print("[case] driver gen", flush=True)
     r = run(["--gen", "2:3000", "--O", "128", "--segw", "32", "--tileK", "128",
              "--check", "rocsparse", "--csv", "--stat", "median", "--algo", "vcsr_mc,vcsr_mc_fp32"])

@@ -5,8 +5,9 @@
 //   vcsr_mc / vcsr_mc_fp32     through the drop-in C++ surface (include/vcsr_formats.hpp),
 //                              with the reference's call sequence convert -> upload -> run
 //   rocsparse / rocsparse_fp16 hipSPARSE SpMM (libvcsrmc_bench.so)
-// Additive: --gen K[:size] reads a seeded synthetic workload instead of --mtx (configs of
-// include/vcsrmc_bench.h).  Not built here: --reorder rcm.
+// --reorder rcm (main.cpp:182-183) runs the GPU column reordering through the drop-in
+// include/reorder.hpp.  Additive: --gen K[:size] reads a seeded synthetic workload instead of
+// --mtx (configs of include/vcsrmc_bench.h).
 #include <getopt.h>
 #include <hip/hip_runtime.h>
 
@@ -29,6 +30,7 @@
 #include <vector>
 
 #include "csr.hpp"
+#include "reorder.hpp"
 #include "vcsr_formats.hpp"
 #include "vcsrmc_bench.h"
 
@@ -178,7 +180,7 @@ void usage() {
         "Usage: spmm_vcsr (--mtx file.mtx | --gen K[:size]) --O 128 [options]\n"
         "Algorithms: rocsparse, rocsparse_fp16, vcsr_mc (FP16 inputs, MFMA), vcsr_mc_fp32\n"
         "Options: --segw 16 --tileK 64 --repeat 10 --warmup 3 --stat mean|median\n"
-        "         --reorder none --check cpu|rocsparse|none --csv --help\n"
+        "         --reorder none|rcm --check cpu|rocsparse|none --csv --help\n"
         "         --bdist pattern|normal|uniform|wide   (B fill; random ones use a fixed seed)\n"
         "         --lenient   record a failed correctness check as FAIL instead of aborting\n"
         "         --gen K[:size]  seeded synthetic workload K = 1..5 instead of --mtx\n"
@@ -241,8 +243,8 @@ int run(int argc, char** argv) {
     if (check != "cpu" && check != "rocsparse" && check != "none")
         throw std::runtime_error("Unknown reference: " + check);
     if ((mtx.empty() == gen.empty()) || optind != argc) { usage(); return 2; }
-    if (reorder != "none")
-        throw std::runtime_error("Unknown or unsupported reordering: " + reorder);
+    if (reorder != "none" && reorder != "rcm")
+        throw std::runtime_error("Unknown reordering: " + reorder);
     if (stat != "mean" && stat != "median")
         throw std::runtime_error("Unknown --stat: " + stat + " (mean|median)");
     if (tileK != 16 && tileK != 32 && tileK != 64 && tileK != 128)
@@ -278,6 +280,17 @@ int run(int argc, char** argv) {
         } else {
             throw std::runtime_error("Unknown --bdist: " + bdist + " (pattern|normal|uniform|wide)");
         }
+    }
+
+    // Relabelling A's columns and permuting B's rows to match leaves C = A B unchanged; done
+    // once, before every algorithm and the reference result (src/main.cpp:180-183).
+    if (reorder == "rcm" && csr.nnz) {
+        const auto t0 = std::chrono::steady_clock::now();
+        apply_column_permutation(csr, hB, O, rcm_column_order(csr));
+        const double ms =
+            std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+        std::fprintf(stderr, "reorder rcm: %.1f ms (GPU ordering and relabelling, with copies)\n",
+                     ms);
     }
 
     float *dB = nullptr, *dC = nullptr, *dval = nullptr;
