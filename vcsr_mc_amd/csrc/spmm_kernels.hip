@@ -39,43 +39,42 @@ __device__ __forceinline__ int unit_of_block(int bid, int num_units) {
     return (bid & 7) * per + (bid >> 3);
 }
 
-// Raw B values of the 8 tile rows a lane feeds into the MFMA B operand (kept in the storage
-// type until use, so a prefetched load is never waited for early by a conversion).
+// Raw B values of the 8 tile rows a lane feeds into the MFMA B operand, one vector of VEC
+// consecutive output columns per row (kept in the storage type until use, so a prefetched load
+// is never waited for early by a conversion).
 template <int VEC, typename TB>
 struct BRows {
-    TB v[8][VEC];
+    typedef TB vec_t __attribute__((ext_vector_type(VEC)));
+    vec_t r[8];
 };
 
+// Zeros read in place of a B row by padding columns and by lanes past O.  Never written; not
+// `const`, so that it lives in the global address space like B and the loads stay global loads
+// (a constant-space operand would turn them into flat loads, which also count against the LDS
+// wait counter).
+__device__ __attribute__((aligned(16))) float kZeroRow[16];
+
+// Every load is issued unconditionally (padding columns and lanes past O read kZeroRow): the
+// number of loads in flight is then the same on every path, which lets the compiler wait for
+// exactly the older loads it needs, and no select is needed after a load.
 template <int VEC, typename TB, bool ALIGNED>
 __device__ __forceinline__ void load_b_rows(const TB* __restrict__ B, const int (&cols)[8],
                                             long long O, int c0, BRows<VEC, TB>& R) {
+    typedef typename BRows<VEC, TB>::vec_t vec_t;
+    const bool lane_ok = c0 < O;
+    const TB* zero = reinterpret_cast<const TB*>(kZeroRow);
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
         const int col = cols[i];
-        const TB* src = B + (long long)(col < 0 ? 0 : col) * O + c0;
-        if constexpr (ALIGNED) {
-            const bool ok = col >= 0 && c0 < O;
-            if constexpr (sizeof(TB) == 2 && VEC >= 2) {
-                typedef _Float16 hv __attribute__((ext_vector_type(VEC)));
-                hv x = {};
-                if (ok) x = *reinterpret_cast<const hv*>(src);
-#pragma unroll
-                for (int q = 0; q < VEC; ++q) R.v[i][q] = x[q];
-            } else if constexpr (sizeof(TB) == 4 && VEC >= 4) {
-#pragma unroll
-                for (int h = 0; h < VEC; h += 4) {
-                    floatx4 x = {0.f, 0.f, 0.f, 0.f};
-                    if (ok) x = *reinterpret_cast<const floatx4*>(src + h);
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) R.v[i][h + q] = x[q];
-                }
-            } else {
-#pragma unroll
-                for (int q = 0; q < VEC; ++q) R.v[i][q] = ok ? src[q] : (TB)0;
-            }
+        const bool ok = col >= 0 && lane_ok;
+        const TB* src = ok ? B + (long long)col * O + c0 : zero;
+        if constexpr (ALIGNED && VEC * sizeof(TB) >= 4) {
+            R.r[i] = *reinterpret_cast<const vec_t*>(src);
         } else {
+            vec_t x;
 #pragma unroll
-            for (int q = 0; q < VEC; ++q) R.v[i][q] = (col >= 0 && c0 + q < O) ? src[q] : (TB)0;
+            for (int q = 0; q < VEC; ++q) x[q] = (ok && c0 + q < O) ? src[q] : (TB)0;
+            R.r[i] = x;
         }
     }
 }
@@ -175,16 +174,38 @@ __device__ __forceinline__ void merge_into_c(const floatx4 (&acc)[TK / 16], floa
     }
 }
 
-__device__ __forceinline__ uint4 load_a_state(int d, int c, int lane, int a_off,
-                                              const int* __restrict__ chunk_eptr,
-                                              const uint32_t* __restrict__ entries,
-                                              const _Float16* __restrict__ dense_a) {
-    if (d >= 0) return *reinterpret_cast<const uint4*>(dense_a + (long long)d * 512 + a_off);
-    const int eb = chunk_eptr[c], ee = chunk_eptr[c + 1];
-    uint4 s = {0u, 0u, (unsigned)eb, (unsigned)ee};
-    if (eb + lane < ee) s.x = entries[eb + lane];
-    if (eb + 64 + lane < ee) s.y = entries[eb + 64 + lane];
-    return s;
+// Per-tile metadata, wave-uniform: dense copy index (-1 if none) and the entry range.
+struct TileMeta {
+    int d, eb, ee;
+};
+
+__device__ __forceinline__ TileMeta tile_meta(int c, const int* __restrict__ chunk_dense,
+                                              const int* __restrict__ chunk_eptr) {
+    return TileMeta{chunk_dense[c], chunk_eptr[c], chunk_eptr[c + 1]};
+}
+
+// A sparse tile holds at most kDenseMin entries, three per lane.
+static_assert(kDenseMin <= 3 * 64, "a sparse tile must fit three entries per lane");
+
+// A state of an FP16 tile in four words per lane: the dense operand (8 halves), or this lane's
+// entries eb + lane, eb + 64 + lane, eb + 128 + lane (addresses clamped into the tile, so the
+// four loads are always issued; the scatter skips the ones past ee).
+__device__ __forceinline__ uint4 load_a16(const TileMeta& m, int lane, int a_off,
+                                          const uint32_t* __restrict__ entries,
+                                          const _Float16* __restrict__ dense_a) {
+    const uint32_t *p0, *p1, *p2, *p3;
+    if (m.d >= 0) {
+        const uint32_t* base =
+            reinterpret_cast<const uint32_t*>(dense_a + (long long)m.d * 512 + a_off);
+        p0 = base; p1 = base + 1; p2 = base + 2; p3 = base + 3;
+    } else {
+        const int last = m.ee - 1;
+        p0 = entries + min(m.eb + lane, last);
+        p1 = entries + min(m.eb + 64 + lane, last);
+        p2 = entries + min(m.eb + 128 + lane, last);
+        p3 = p2;
+    }
+    return uint4{*p0, *p1, *p2, *p3};
 }
 
 // Schedule of a 4-wave work-group.  Work-groups [0, H8) run the heavy units (H8 = num_heavy
@@ -207,9 +228,43 @@ __device__ __forceinline__ bool schedule(int num_units, int num_heavy, int wave,
     return j < nlw && u < num_units;
 }
 
-// FP16 tiles [first, end) with stride W of one unit, accumulated into acc.  While tile c is
-// multiplied, the B rows and the A state (dense operand, or first nonzeros and entry range) of
-// the wave's next tile and the column indices of the tile after are in flight.
+// One FP16 tile: A operand (dense words, or the entries scattered into the wave's LDS tile),
+// then VEC MFMAs against the B rows.
+template <int VEC, typename TB>
+__device__ __forceinline__ void mma_tile_f16(const TileMeta& m, const uint4& st, int lane,
+                                             _Float16* Aw, _Float16* my_a, const BRows<VEC, TB>& R,
+                                             floatx4 (&acc)[VEC]) {
+    half8 a;
+    if (m.d >= 0) {
+        a = __builtin_bit_cast(half8, st);
+    } else {
+        *reinterpret_cast<half8*>(my_a) = half8{0, 0, 0, 0, 0, 0, 0, 0};
+        wave_lds_sync();
+        if (m.eb + lane < m.ee) scatter_a_f16(Aw, st.x);
+        if (m.eb + 64 + lane < m.ee) scatter_a_f16(Aw, st.y);
+        if (m.eb + 128 + lane < m.ee) scatter_a_f16(Aw, st.z);
+        wave_lds_sync();
+        a = *reinterpret_cast<const half8*>(my_a);
+        wave_lds_sync();
+    }
+#pragma unroll
+    for (int q = 0; q < VEC; ++q) {
+        const half8 b = half8{(_Float16)R.r[0][q], (_Float16)R.r[1][q], (_Float16)R.r[2][q],
+                              (_Float16)R.r[3][q], (_Float16)R.r[4][q], (_Float16)R.r[5][q],
+                              (_Float16)R.r[6][q], (_Float16)R.r[7][q]};
+        acc[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc[q], 0, 0, 0);
+    }
+}
+
+// FP16 tiles first, first + W, ... < end of one unit (wave-uniform indices), accumulated into
+// acc.  While tile c is multiplied, the B rows and A state of the wave's next tile and the
+// column indices of the tile after are in flight.  Three rules keep the prefetch effective
+// (vector loads complete in issue order, and a wait names a count of younger loads):
+//   * the loop is unrolled by two over fixed buffers A and B, so no register that a load is
+//     still filling is ever copied (a copy would wait for the load);
+//   * column indices are loaded before the B rows and A state they lead to, so waiting for
+//     them does not wait for those;
+//   * every iteration issues the same loads (column indices past the last tile are clamped).
 template <int TK, typename TB, bool ALIGNED>
 __device__ __forceinline__ void tiles_f16(int first, int end, int W, int lane, int n, int g,
                                           int c0, long long OL, const int* __restrict__ chunk_eptr,
@@ -220,72 +275,46 @@ __device__ __forceinline__ void tiles_f16(int first, int end, int W, int lane, i
                                           const TB* __restrict__ B, _Float16* Aw,
                                           floatx4 (&acc)[TK / 16]) {
     constexpr int VEC = TK / 16;
+    if (first >= end) return;
     const int a_off = n * 32 + 8 * g;  // this lane's A operand inside a dense tile
     _Float16* my_a = &Aw[n * kApitch + 8 * g];
+    const int last = first + (end - 1 - first) / W * W;
     int c = first;
-    if (c < end) {
-        int cols_next[8];
-        BRows<VEC, TB> R;
-        {
-            int cols[8];
-            load_cols8(chunk_cols, c, g, cols);
-            load_b_rows<VEC, TB, ALIGNED>(B, cols, OL, c0, R);
-        }
-        int d_next = -1;
-        if (c + W < end) {
-            load_cols8(chunk_cols, c + W, g, cols_next);
-            d_next = chunk_dense[c + W];
-        }
-        // A state of a tile in 4 registers: the dense operand (8 halves), or the first two
-        // nonzeros of this lane and the tile's entry range {w0, w1, eb, ee}.
-        int d = chunk_dense[c];
-        uint4 cur = load_a_state(d, c, lane, a_off, chunk_eptr, entries, dense_a);
+    BRows<VEC, TB> RA, RB;
+    int colsA[8], colsB[8];
+    TileMeta mA = tile_meta(c, chunk_dense, chunk_eptr);
+    load_cols8(chunk_cols, c, g, colsA);
+    const int c1 = min(c + W, last);
+    load_cols8(chunk_cols, c1, g, colsB);
+    TileMeta mB = tile_meta(c1, chunk_dense, chunk_eptr);
+    load_b_rows<VEC, TB, ALIGNED>(B, colsA, OL, c0, RA);
+    uint4 sA = load_a16(mA, lane, a_off, entries, dense_a);
+    uint4 sB;
+    // Invariant at the top: tile c in A (B rows, A state, metadata), the column indices and
+    // metadata of tile c + W in B; at least three tiles c, c + W, c + 2 W remain.
+    for (; c + W < last; c += 2 * W) {
+        load_cols8(chunk_cols, c + 2 * W, g, colsA);
+        const TileMeta mA2 = tile_meta(c + 2 * W, chunk_dense, chunk_eptr);
+        load_b_rows<VEC, TB, ALIGNED>(B, colsB, OL, c0, RB);
+        sB = load_a16(mB, lane, a_off, entries, dense_a);
+        mma_tile_f16<VEC, TB>(mA, sA, lane, Aw, my_a, RA, acc);
 
-        for (; c < end; c += W) {
-            const bool has1 = c + W < end;
-            BRows<VEC, TB> Rn;
-            uint4 nxt = {0u, 0u, 0u, 0u};
-            int cols_after[8];
-            int d_after = -1;
-            if (has1) {
-                load_b_rows<VEC, TB, ALIGNED>(B, cols_next, OL, c0, Rn);
-                nxt = load_a_state(d_next, c + W, lane, a_off, chunk_eptr, entries, dense_a);
-                if (c + 2 * W < end) {
-                    load_cols8(chunk_cols, c + 2 * W, g, cols_after);
-                    d_after = chunk_dense[c + 2 * W];
-                }
-            }
-            half8 a;
-            if (d >= 0) {
-                a = __builtin_bit_cast(half8, cur);
-            } else {
-                const int eb = (int)cur.z, ee = (int)cur.w;
-                *reinterpret_cast<half8*>(my_a) = half8{0, 0, 0, 0, 0, 0, 0, 0};
-                wave_lds_sync();
-                if (eb + lane < ee) scatter_a_f16(Aw, cur.x);
-                if (eb + 64 + lane < ee) scatter_a_f16(Aw, cur.y);
-                for (int e = eb + 128 + lane; e < ee; e += 64) scatter_a_f16(Aw, entries[e]);
-                wave_lds_sync();
-                a = *reinterpret_cast<const half8*>(my_a);
-                wave_lds_sync();
-            }
-#pragma unroll
-            for (int q = 0; q < VEC; ++q) {
-                const half8 b = half8{(_Float16)R.v[0][q], (_Float16)R.v[1][q],
-                                      (_Float16)R.v[2][q], (_Float16)R.v[3][q],
-                                      (_Float16)R.v[4][q], (_Float16)R.v[5][q],
-                                      (_Float16)R.v[6][q], (_Float16)R.v[7][q]};
-                acc[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc[q], 0, 0, 0);
-            }
-            if (has1) {
-                R = Rn;
-#pragma unroll
-                for (int i = 0; i < 8; ++i) cols_next[i] = cols_after[i];
-                d = d_next;
-                d_next = d_after;
-                cur = nxt;
-            }
-        }
+        const int c3 = min(c + 3 * W, last);
+        load_cols8(chunk_cols, c3, g, colsB);
+        const TileMeta mB2 = tile_meta(c3, chunk_dense, chunk_eptr);
+        load_b_rows<VEC, TB, ALIGNED>(B, colsA, OL, c0, RA);
+        sA = load_a16(mA2, lane, a_off, entries, dense_a);
+        mma_tile_f16<VEC, TB>(mB, sB, lane, Aw, my_a, RB, acc);
+        mA = mA2;
+        mB = mB2;
+    }
+    if (c < last) {  // two tiles left: c and c + W = last
+        load_b_rows<VEC, TB, ALIGNED>(B, colsB, OL, c0, RB);
+        sB = load_a16(mB, lane, a_off, entries, dense_a);
+        mma_tile_f16<VEC, TB>(mA, sA, lane, Aw, my_a, RA, acc);
+        mma_tile_f16<VEC, TB>(mB, sB, lane, Aw, my_a, RB, acc);
+    } else {
+        mma_tile_f16<VEC, TB>(mA, sA, lane, Aw, my_a, RA, acc);
     }
 }
 
@@ -304,7 +333,10 @@ __global__ __launch_bounds__(64 * kWaves, (f16_min_waves<TB, ALIGNED>())) void k
     constexpr int VEC = TK / 16;
     __shared__ __attribute__((aligned(16))) _Float16 As[kWaves][16 * kApitch];
     __shared__ __attribute__((aligned(16))) float P[kWaves * 16 * TK];
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
+    // The wave index is uniform across the wave: readfirstlane lets the compiler keep the unit
+    // and tile indices in scalar registers and fetch tile metadata with scalar loads.
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
     int u;
     bool heavy;
     if (!schedule(num_units, num_heavy, wave, u, heavy)) return;
