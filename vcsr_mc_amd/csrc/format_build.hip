@@ -306,8 +306,8 @@ __global__ void k_panel_entries(const K* __restrict__ skey, const uint32_t* __re
                                 const int* __restrict__ pin, const int* __restrict__ pstart,
                                 const int* __restrict__ cbase, const int* __restrict__ tcol,
                                 const float* __restrict__ tval, long long n,
-                                uint32_t* __restrict__ entries, float* __restrict__ evals,
-                                int* __restrict__ chunk_cols, int* __restrict__ chunk_eptr,
+                                uint32_t* __restrict__ entries, int* __restrict__ chunk_cols,
+                                int* __restrict__ chunk_eptr,
                                 int* __restrict__ pmask, int* __restrict__ echunk) {
     const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
@@ -320,15 +320,18 @@ __global__ void k_panel_entries(const K* __restrict__ skey, const uint32_t* __re
     echunk[i] = c;
     const float v = tval[src];
     if constexpr (FP32) {
-        entries[i] = (uint32_t)r16 | ((uint32_t)k << 4);
-        evals[i] = v;
+        entries[2 * i] = (uint32_t)r16 | ((uint32_t)k << 4);
+        entries[2 * i + 1] = __float_as_uint(v);
     } else {
         const _Float16 h = (_Float16)v;  // v_cvt_f16_f32, round to nearest even
         entries[i] = (uint32_t)__builtin_bit_cast(unsigned short, h) | ((uint32_t)r16 << 16) |
                      ((uint32_t)k << 20);
     }
     if (hdist[i]) {
-        chunk_cols[(long long)c * kChunkCols + k] = tcol[src];
+        // FP32 formats keep a tile's columns in K-step order: lane group g of the kernel reads
+        // columns 4 s + g (s = 0..7) as eight consecutive words.
+        const int slot = FP32 ? (k & 3) * 8 + (k >> 2) : k;
+        chunk_cols[(long long)c * kChunkCols + slot] = tcol[src];
         if (k == 0) chunk_eptr[c] = (int)i;
     }
     atomicOr(&pmask[j], 1 << r16);
@@ -346,18 +349,19 @@ __global__ void k_dense_index(const int* __restrict__ flag, const int* __restric
 }
 
 template <bool FP32>
-__global__ void k_dense_fill(const uint32_t* __restrict__ entries, const float* __restrict__ evals,
+__global__ void k_dense_fill(const uint32_t* __restrict__ entries,
                              const int* __restrict__ echunk, const int* __restrict__ chunk_dense,
                              long long n, _Float16* __restrict__ a16, float* __restrict__ a32) {
     const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
     const int d = chunk_dense[echunk[i]];
     if (d < 0) return;
-    const uint32_t w = entries[i];
     if constexpr (FP32) {
+        const uint32_t w = entries[2 * i];
         const int r = w & 15, k = (w >> 4) & 31;
-        a32[(long long)d * 512 + (k & 3) * 128 + r * 8 + (k >> 2)] = evals[i];
+        a32[(long long)d * 512 + (k & 3) * 128 + r * 8 + (k >> 2)] = __uint_as_float(entries[2 * i + 1]);
     } else {
+        const uint32_t w = entries[i];
         const int r = (w >> 16) & 15, k = (w >> 20) & 31;
         a16[(long long)d * 512 + r * 32 + k] = __builtin_bit_cast(_Float16, (unsigned short)(w & 0xffffu));
     }
@@ -365,19 +369,12 @@ __global__ void k_dense_fill(const uint32_t* __restrict__ entries, const float* 
 
 // Units.  A panel with at most `light_max` tiles is one light unit (one wave); a larger panel
 // is cut into heavy units of at most kHeavyTiles tiles (the waves of a work-group share them).
-// FP32 panels of at most kHeavyTiles tiles filled below kValuPermille / 1000 run on VALU.
-__device__ __forceinline__ bool valu_panel(int fp32, int ntiles, int nnz) {
-    return fp32 && ntiles <= kHeavyTiles && 1000LL * nnz < (long long)kValuPermille * 512 * ntiles;
-}
-
-__global__ void k_units_per_panel(const int* __restrict__ nch, const int* __restrict__ pstart,
-                                  int NP, int light_max, int fp32, int* __restrict__ nu,
-                                  int* __restrict__ nheavy) {
+__global__ void k_units_per_panel(const int* __restrict__ nch, int NP, int light_max,
+                                  int* __restrict__ nu, int* __restrict__ nheavy) {
     const long long j = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     if (j >= NP) return;
     const bool heavy = nch[j] > light_max;
-    const bool valu = valu_panel(fp32, nch[j], pstart[j + 1] - pstart[j]);
-    const int n = (heavy && !valu) ? (nch[j] + kHeavyTiles - 1) / kHeavyTiles : 1;
+    const int n = heavy ? (nch[j] + kHeavyTiles - 1) / kHeavyTiles : 1;
     nu[j] = n;
     nheavy[j] = heavy ? n : 0;
 }
@@ -386,17 +383,16 @@ __global__ void k_units_per_panel(const int* __restrict__ nch, const int* __rest
 // then light; larger first inside each class (the stable sort keeps panel order on ties).
 __global__ void k_make_units(const int* __restrict__ cbase, const int* __restrict__ ubase,
                              const int* __restrict__ ppanel, const int* __restrict__ pmask,
-                             const int* __restrict__ nch, const int* __restrict__ pstart, int NP,
-                             int light_max, int fp32, int4* __restrict__ units,
-                             uint32_t* __restrict__ key, uint32_t* __restrict__ pay) {
+                             const int* __restrict__ nch, int NP, int light_max,
+                             int4* __restrict__ units, uint32_t* __restrict__ key,
+                             uint32_t* __restrict__ pay) {
     const long long j = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     if (j >= NP) return;
     const int c0 = cbase[j], c1 = cbase[j + 1];
     const int u0 = ubase[j], nu = ubase[j + 1] - u0;
     const bool heavy = nch[j] > light_max;
-    const bool valu = valu_panel(fp32, nch[j], pstart[j + 1] - pstart[j]);
-    const int split = (nu > 1 ? (1 << 16) : 0) | (valu ? (1 << 17) : 0);
-    const int step = (heavy && !valu) ? kHeavyTiles : (c1 - c0);
+    const int split = nu > 1 ? (1 << 16) : 0;
+    const int step = heavy ? kHeavyTiles : (c1 - c0);
     for (int u = 0; u < nu; ++u) {
         const int cb = c0 + u * step;
         const int ce = min(cb + step, c1);
@@ -475,20 +471,17 @@ static void build_exec_layout_k(DeviceFormat& F, const int* trow, const int* tco
 
     F.chunk_eptr.alloc(NC + 1);
     F.chunk_cols.alloc((size_t)NC * kChunkCols);
-    F.entries.alloc(n);
-    if (F.fp32) F.evals.alloc(n);
+    F.entries.alloc(F.fp32 ? 2 * n : n);
     fill<int>(F.chunk_cols.p, (long long)NC * kChunkCols, -1, st);
     fill<int>(F.chunk_eptr.p + NC, 1, (int)n, st);
     VCSRMC_HIP(hipMemsetAsync(pmask.p, 0, sizeof(int) * (size_t)NP, st));
     DevBuf<int> echunk(n);
     if (F.fp32)
         LAUNCH((k_panel_entries<K, true>), n, kp, vp, hdist.p, dc.p, pin.p, pstart.p, cbase.p, tcol,
-               tval, n, F.entries.p, F.evals.p, F.chunk_cols.p, F.chunk_eptr.p, pmask.p,
-               echunk.p);
+               tval, n, F.entries.p, F.chunk_cols.p, F.chunk_eptr.p, pmask.p, echunk.p);
     else
         LAUNCH((k_panel_entries<K, false>), n, kp, vp, hdist.p, dc.p, pin.p, pstart.p, cbase.p,
-               tcol, tval, n, F.entries.p, (float*)nullptr, F.chunk_cols.p, F.chunk_eptr.p,
-               pmask.p, echunk.p);
+               tcol, tval, n, F.entries.p, F.chunk_cols.p, F.chunk_eptr.p, pmask.p, echunk.p);
 
     // dense copies of well-filled tiles
     {
@@ -503,20 +496,20 @@ static void build_exec_layout_k(DeviceFormat& F, const int* trow, const int* tco
             if (F.fp32) {
                 F.dense_a32.alloc((size_t)ND * 512);
                 VCSRMC_HIP(hipMemsetAsync(F.dense_a32.p, 0, sizeof(float) * 512 * (size_t)ND, st));
-                LAUNCH((k_dense_fill<true>), n, F.entries.p, F.evals.p, echunk.p, F.chunk_dense.p,
-                       n, (_Float16*)nullptr, F.dense_a32.p);
+                LAUNCH((k_dense_fill<true>), n, F.entries.p, echunk.p, F.chunk_dense.p, n,
+                       (_Float16*)nullptr, F.dense_a32.p);
             } else {
                 F.dense_a16.alloc((size_t)ND * 512);
                 VCSRMC_HIP(hipMemsetAsync(F.dense_a16.p, 0, sizeof(_Float16) * 512 * (size_t)ND, st));
-                LAUNCH((k_dense_fill<false>), n, F.entries.p, (const float*)nullptr, echunk.p,
-                       F.chunk_dense.p, n, F.dense_a16.p, (float*)nullptr);
+                LAUNCH((k_dense_fill<false>), n, F.entries.p, echunk.p, F.chunk_dense.p, n,
+                       F.dense_a16.p, (float*)nullptr);
             }
         }
     }
 
     const int light_max = light_tile_limit(NC);
     DevBuf<int> nu(NP), ubase(NP + 1), nheavy(NP), hbase(NP + 1);
-    LAUNCH(k_units_per_panel, NP, nch.p, pstart.p, NP, light_max, F.fp32, nu.p, nheavy.p);
+    LAUNCH(k_units_per_panel, NP, nch.p, NP, light_max, nu.p, nheavy.p);
     exclusive_sum<int, int>(nu.p, ubase.p, NP, st);
     exclusive_sum<int, int>(nheavy.p, hbase.p, NP, st);
     const int NU = read_scalar(ubase.p + NP, st);
@@ -524,8 +517,8 @@ static void build_exec_layout_k(DeviceFormat& F, const int* trow, const int* tco
     {
         DevBuf<int4> raw(NU);
         DevBuf<uint32_t> k1(NU), k2(NU), v1(NU), v2(NU);
-        LAUNCH(k_make_units, NP, cbase.p, ubase.p, ppanel.p, pmask.p, nch.p, pstart.p, NP,
-               light_max, F.fp32, raw.p, k1.p, v1.p);
+        LAUNCH(k_make_units, NP, cbase.p, ubase.p, ppanel.p, pmask.p, nch.p, NP, light_max, raw.p,
+               k1.p, v1.p);
         uint32_t *kp2 = k1.p, *ka2 = k2.p, *vp2 = v1.p, *va2 = v2.p;
         radix_sort_pairs<uint32_t>(kp2, vp2, ka2, va2, NU, 17, st);
         F.units.alloc(NU);
@@ -540,52 +533,6 @@ static void build_exec_layout_k(DeviceFormat& F, const int* trow, const int* tco
 }
 
 // CSR of the matrix from triples in any order (FP32 formats keep it for their VALU units).
-template <typename K>
-__global__ void k_csr_keys(const int* __restrict__ trow, const int* __restrict__ tcol, long long n,
-                           int cbits, K* __restrict__ key, uint32_t* __restrict__ pay,
-                           int* __restrict__ rcount) {
-    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= n) return;
-    key[i] = ((K)trow[i] << cbits) | (K)tcol[i];
-    pay[i] = (uint32_t)i;
-    atomicAdd(&rcount[trow[i]], 1);
-}
-
-__global__ void k_csr_gather(const uint32_t* __restrict__ perm, const int* __restrict__ tcol,
-                             const float* __restrict__ tval, long long n, int* __restrict__ col,
-                             float* __restrict__ val) {
-    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= n) return;
-    col[i] = tcol[perm[i]];
-    val[i] = tval[perm[i]];
-}
-
-template <typename K>
-static void csr_from_triples_k(DeviceFormat& F, const int* trow, const int* tcol, const float* tval,
-                               long long n, int cbits, int kbits, hipStream_t st) {
-    DevBuf<K> k1(n), k2(n);
-    DevBuf<uint32_t> v1(n), v2(n);
-    DevBuf<int> rcount(F.M);
-    VCSRMC_HIP(hipMemsetAsync(rcount.p, 0, sizeof(int) * (size_t)F.M, st));
-    LAUNCH((k_csr_keys<K>), n, trow, tcol, n, cbits, k1.p, v1.p, rcount.p);
-    K *kp = k1.p, *ka = k2.p;
-    uint32_t *vp = v1.p, *va = v2.p;
-    radix_sort_pairs<K>(kp, vp, ka, va, n, kbits, st);
-    F.csr_rp.alloc((size_t)F.M + 1);
-    F.csr_col.alloc(n);
-    F.csr_val.alloc(n);
-    exclusive_sum<int, int>(rcount.p, F.csr_rp.p, F.M, st);
-    LAUNCH(k_csr_gather, n, vp, tcol, tval, n, F.csr_col.p, F.csr_val.p);
-}
-
-static void csr_from_triples(DeviceFormat& F, const int* trow, const int* tcol, const float* tval,
-                             long long n, hipStream_t st) {
-    const int cbits = bits_for(F.N > 0 ? (unsigned long long)(F.N - 1) : 0ull);
-    const int rbits = bits_for(F.M > 0 ? (unsigned long long)(F.M - 1) : 0ull);
-    if (cbits + rbits <= 32) csr_from_triples_k<uint32_t>(F, trow, tcol, tval, n, cbits, cbits + rbits, st);
-    else csr_from_triples_k<unsigned long long>(F, trow, tcol, tval, n, cbits, cbits + rbits, st);
-}
-
 static void build_exec_layout(DeviceFormat& F, const int* trow, const int* tcol, const float* tval,
                               long long n, hipStream_t st) {
     F.num_panels = F.num_chunks = F.num_units = 0;
@@ -730,17 +677,6 @@ void build_from_csr(DeviceFormat& F, const int* d_row_ptr, const int* d_col, con
     DevBuf<float> sval(nnz);
     LAUNCH(k_scale_values, nnz, d_val, sval.p, (long long)nnz, inv_scale);
     build_exec_layout(F, row_of.p, d_col, sval.p, nnz, st);
-    if (F.fp32) {
-        F.csr_rp.alloc((size_t)M + 1);
-        F.csr_col.alloc(nnz);
-        F.csr_val.alloc(nnz);
-        VCSRMC_HIP(hipMemcpyAsync(F.csr_rp.p, d_row_ptr, sizeof(int) * ((size_t)M + 1),
-                                  hipMemcpyDeviceToDevice, st));
-        VCSRMC_HIP(hipMemcpyAsync(F.csr_col.p, d_col, sizeof(int) * (size_t)nnz,
-                                  hipMemcpyDeviceToDevice, st));
-        VCSRMC_HIP(hipMemcpyAsync(F.csr_val.p, sval.p, sizeof(float) * (size_t)nnz,
-                                  hipMemcpyDeviceToDevice, st));
-    }
     VCSRMC_HIP(hipStreamSynchronize(st));
     F.ready = true;
 }
@@ -864,7 +800,6 @@ void build_from_host(DeviceFormat& F, const HostArrays& H, hipStream_t st) {
     LAUNCH(k_expand_write, nval, F.group_ptr.p, F.group_seg_base.p, F.group_rows.p, F.lcol.p,
            F.val.p, flag.p, pos.p, H.G, nval, trow.p, tcol.p, tval.p);
     build_exec_layout(F, trow.p, tcol.p, tval.p, n, st);
-    if (F.fp32 && n > 0) csr_from_triples(F, trow.p, tcol.p, tval.p, n, st);
     VCSRMC_HIP(hipStreamSynchronize(st));
     F.ready = true;
 }

@@ -18,8 +18,6 @@ constexpr int kDenseMin = 192;
 // Tiles per heavy unit (shared by the kWaves waves of one work-group).
 constexpr int kHeavyTiles = 64;
 constexpr int kWaves = 4;
-// FP32 panels filled below this many per mille of their tile slots use the VALU row path.
-constexpr int kValuPermille = 0;
 
 // A format on one device.
 //
@@ -34,12 +32,11 @@ constexpr int kValuPermille = 0;
 //                     num_heavy units are heavy (one work-group each, larger first), the rest
 //                     light (one wave each, four per work-group, larger first).
 //   chunk_eptr[c]   = first entry of chunk c (chunk_eptr[num_chunks] = nnz)
-//   chunk_cols[32c+k] = column of the chunk's k-th distinct column, -1 past the end
+//   chunk_cols[32c+k] = column of the chunk's k-th distinct column, -1 past the end (FP32
+//                   formats: slot (k & 3) * 8 + (k >> 2), the order the FP32 kernel's lanes read)
 //   entries[e]      FP16 format: f16 value | row-in-panel << 16 | k << 20
-//                   FP32 format: row-in-panel | k << 4, with the value in evals[e]
-//   units[u].w bit 17 (FP32 formats): the panel is sparse (under 30% of its tile slots filled),
-//                   so the unit runs on VALU FMAs over the panel's rows in csr_rp/csr_col/csr_val
-//                   (the matrix in CSR, value already divided by the scale) instead of MFMA tiles
+//                   FP32 format: two words per entry, entries[2e] = row-in-panel | k << 4 and
+//                   entries[2e+1] = the value's bits
 //   chunk_dense[c]  -1, or the index of the tile's dense copy when more than kDenseMin of its
 //                   512 slots are filled: dense_a16[512 d + 32 row + k] (FP16), or
 //                   dense_a32[512 d + 128 (k & 3) + 8 row + (k >> 2)] (FP32) -- exactly the
@@ -58,13 +55,10 @@ struct DeviceFormat {
     DevBuf<int4> units;
     DevBuf<int> chunk_eptr, chunk_cols;
     DevBuf<uint32_t> entries;
-    DevBuf<float> evals;
     int num_dense = 0;
     DevBuf<int> chunk_dense;
     DevBuf<_Float16> dense_a16;
     DevBuf<float> dense_a32;
-    DevBuf<int> csr_rp, csr_col;  // FP32 formats: the matrix in CSR for the VALU units
-    DevBuf<float> csr_val;
 
     bool ready = false;
     void clear() { *this = DeviceFormat(); }

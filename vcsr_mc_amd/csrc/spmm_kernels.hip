@@ -359,75 +359,85 @@ __global__ __launch_bounds__(64 * kWaves, (f16_min_waves<TB, ALIGNED>())) void k
 // (steps 0-3, then 4-7) so one half is in flight while the other is multiplied.
 template <int VEC>
 struct FRows {
-    float v[4][VEC];
+    typedef float vec_t __attribute__((ext_vector_type(VEC)));
+    vec_t r[4];
 };
 
+// Half a tile of B rows (K steps s0 .. s0 + 3 of the lane's column group): row s holds the VEC
+// output columns c0 .. c0 + VEC - 1 of B row cols[s0 + s].  Loads are unconditional like
+// load_b_rows (padding and lanes past O read kZeroRow).
 template <int VEC, bool ALIGNED>
-__device__ __forceinline__ void load_b_half_f32(const float* __restrict__ B, const int* cols,
-                                                long long O, int c0, FRows<VEC>& R) {
+__device__ __forceinline__ void load_b_half_f32(const float* __restrict__ B, const int (&cols)[8],
+                                                int s0, long long O, int c0, FRows<VEC>& R) {
+    typedef typename FRows<VEC>::vec_t vec_t;
+    const bool lane_ok = c0 < O;
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-        const int col = cols[s];
-        const float* src = B + (long long)(col < 0 ? 0 : col) * O + c0;
-        if constexpr (ALIGNED && VEC >= 4) {
-            const bool ok = col >= 0 && c0 < O;
-#pragma unroll
-            for (int h = 0; h < VEC; h += 4) {
-                floatx4 x = {0.f, 0.f, 0.f, 0.f};
-                if (ok) x = *reinterpret_cast<const floatx4*>(src + h);
-#pragma unroll
-                for (int q = 0; q < 4; ++q) R.v[s][h + q] = x[q];
-            }
+        const int col = cols[s0 + s];
+        const bool ok = col >= 0 && lane_ok;
+        const float* src = ok ? B + (long long)col * O + c0 : kZeroRow;
+        if constexpr (ALIGNED) {
+            R.r[s] = *reinterpret_cast<const vec_t*>(src);
         } else {
+            vec_t x;
 #pragma unroll
-            for (int q = 0; q < VEC; ++q) R.v[s][q] = (col >= 0 && c0 + q < O) ? src[q] : 0.0f;
+            for (int q = 0; q < VEC; ++q) x[q] = (ok && c0 + q < O) ? src[q] : 0.0f;
+            R.r[s] = x;
         }
     }
 }
 
-__device__ __forceinline__ void load_cols_steps(const int* __restrict__ chunk_cols, int c, int g,
-                                                int (&cols)[8]) {
-    const int* cc = chunk_cols + (long long)c * kChunkCols;
-#pragma unroll
-    for (int s = 0; s < 8; ++s) cols[s] = cc[4 * s + g];
-}
-
+// K steps s0 .. s0 + 3 of one tile; steps whose four columns are all padding end the tile.
 template <int VEC>
 __device__ __forceinline__ void mfma_half_f32(const float (&a)[8], int s0, const int (&cols)[8],
                                               const FRows<VEC>& R, floatx4 (&acc)[VEC]) {
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-        if (__ballot(cols[s0 + s] >= 0) == 0) return;  // padding columns end a tile
+        if (__ballot(cols[s0 + s] >= 0) == 0) return;
 #pragma unroll
         for (int q = 0; q < VEC; ++q)
-            acc[q] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s0 + s], R.v[s][q], acc[q], 0, 0, 0);
+            acc[q] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s0 + s], R.r[s][q], acc[q], 0, 0, 0);
     }
 }
 
-// A state of an FP32 tile in 8 registers: the dense operand (8 floats), or the first two
-// nonzeros of this lane (entry words, values) and the tile's entry range.
+// A state of an FP32 tile in eight words per lane, three loads either way: the dense operand
+// (8 floats), or this lane's (entry, value) pairs eb + lane, eb + 64 + lane, eb + 128 + lane
+// (clamped into the tile; the scatter skips the ones past ee).
 struct AState32 {
-    uint4 x, y;
+    uint4 lo, hi;
 };
 
-__device__ __forceinline__ AState32 load_a_state32(int d, int c, int lane, int a_off,
-                                                   const int* __restrict__ chunk_eptr,
-                                                   const uint32_t* __restrict__ entries,
-                                                   const float* __restrict__ evals,
-                                                   const float* __restrict__ dense_a) {
-    AState32 s;
-    if (d >= 0) {
-        s.x = *reinterpret_cast<const uint4*>(dense_a + (long long)d * 512 + a_off);
-        s.y = *reinterpret_cast<const uint4*>(dense_a + (long long)d * 512 + a_off + 4);
-        return s;
+__device__ __forceinline__ AState32 load_a32(const TileMeta& m, int lane, int a_off,
+                                             const uint32_t* __restrict__ entries,
+                                             const float* __restrict__ dense_a) {
+    const uint32_t* p0;
+    const uint32_t* p1;
+    const uint32_t* p2;
+    if (m.d >= 0) {
+        p0 = reinterpret_cast<const uint32_t*>(dense_a + (long long)m.d * 512 + a_off);
+        p1 = p0 + 4;
+        p2 = p0 + 6;
+    } else {
+        const int last = m.ee - 1;
+        p0 = entries + 2 * (long long)min(m.eb + lane, last);
+        p1 = entries + 2 * (long long)min(m.eb + 64 + lane, last);
+        p2 = entries + 2 * (long long)min(m.eb + 128 + lane, last);
     }
-    const int eb = chunk_eptr[c], ee = chunk_eptr[c + 1];
-    s.x = {0u, 0u, 0u, 0u};
-    s.y = {(unsigned)eb, (unsigned)ee, 0u, 0u};
-    if (eb + lane < ee) { s.x.x = entries[eb + lane]; s.x.z = __float_as_uint(evals[eb + lane]); }
-    if (eb + 64 + lane < ee) {
-        s.x.y = entries[eb + 64 + lane];
-        s.x.w = __float_as_uint(evals[eb + 64 + lane]);
+    AState32 s;
+    if (m.d >= 0) {
+        s.lo = *reinterpret_cast<const uint4*>(p0);
+    } else {
+        const uint2 e0 = *reinterpret_cast<const uint2*>(p0);
+        s.lo = uint4{e0.x, e0.y, 0u, 0u};
+    }
+    const uint2 e1 = *reinterpret_cast<const uint2*>(p1);
+    const uint2 e2 = *reinterpret_cast<const uint2*>(p2);
+    if (m.d >= 0) {
+        s.hi = uint4{e1.x, e1.y, e2.x, e2.y};
+    } else {
+        s.lo.z = e1.x;
+        s.lo.w = e1.y;
+        s.hi = uint4{e2.x, e2.y, 0u, 0u};
     }
     return s;
 }
@@ -437,137 +447,104 @@ __device__ __forceinline__ void scatter_a_f32(float* At, uint32_t w, float v) {
     At[(k & 3) * 128 + r * 8 + (k >> 2)] = v;
 }
 
+// This lane's 8 A values of a tile (K steps 0..7): the dense words, or the entries scattered
+// into the wave's LDS tile and read back.
+__device__ __forceinline__ void a_operand_f32(const TileMeta& m, const AState32& st, int lane,
+                                              float* Aw, float* my_a, float (&a)[8]) {
+    floatx4 lo, hi;
+    if (m.d >= 0) {
+        lo = __builtin_bit_cast(floatx4, st.lo);
+        hi = __builtin_bit_cast(floatx4, st.hi);
+    } else {
+        *reinterpret_cast<floatx4*>(my_a) = floatx4{0.f, 0.f, 0.f, 0.f};
+        *reinterpret_cast<floatx4*>(my_a + 4) = floatx4{0.f, 0.f, 0.f, 0.f};
+        wave_lds_sync();
+        if (m.eb + lane < m.ee) scatter_a_f32(Aw, st.lo.x, __uint_as_float(st.lo.y));
+        if (m.eb + 64 + lane < m.ee) scatter_a_f32(Aw, st.lo.z, __uint_as_float(st.lo.w));
+        if (m.eb + 128 + lane < m.ee) scatter_a_f32(Aw, st.hi.x, __uint_as_float(st.hi.y));
+        wave_lds_sync();
+        lo = *reinterpret_cast<const floatx4*>(my_a);
+        hi = *reinterpret_cast<const floatx4*>(my_a + 4);
+        wave_lds_sync();
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        a[i] = lo[i];
+        a[4 + i] = hi[i];
+    }
+}
+
+// FP32 tiles first, first + W, ... < end of one unit, in half tiles (K steps 0-3, then 4-7) so
+// that one half is in flight while the other is multiplied.  Same rules as tiles_f16: the loop
+// runs two tiles per iteration over fixed buffers (X: steps 0-3, Y: steps 4-7; tile sets A and
+// B for the A state and column indices), column indices are issued before the loads they
+// address, and every iteration issues the same loads.  Phases of one iteration (tiles c and
+// d = c + W):
+//   1. load Y (c);               multiply steps 0-3 of c (X)
+//   2. load X (d), A state (d);  multiply steps 4-7 of c (Y); load columns of c + 2W
+//   3. load Y (d);               multiply steps 0-3 of d (X)
+//   4. load X (c + 2W), A state; multiply steps 4-7 of d (Y); load columns of c + 3W
 template <int TK, bool ALIGNED>
 __device__ __forceinline__ void tiles_f32(int first, int end, int W, int lane, int n, int g,
                                           int c0, long long OL, const int* __restrict__ chunk_eptr,
                                           const int* __restrict__ chunk_cols,
                                           const int* __restrict__ chunk_dense,
                                           const uint32_t* __restrict__ entries,
-                                          const float* __restrict__ evals,
                                           const float* __restrict__ dense_a,
                                           const float* __restrict__ B, float* Aw,
                                           floatx4 (&acc)[TK / 16]) {
     constexpr int VEC = TK / 16;
+    if (first >= end) return;
     const int a_off = g * 128 + n * 8;
     float* my_a = &Aw[a_off];
+    const int last = first + (end - 1 - first) / W * W;
     int c = first;
-    if (c < end) {
-        int cols[8], cols_next[8];
-        FRows<VEC> R0, R1;
-        load_cols_steps(chunk_cols, c, g, cols);
-        load_b_half_f32<VEC, ALIGNED>(B, cols, OL, c0, R0);
-        int d_next = -1;
-        if (c + W < end) {
-            load_cols_steps(chunk_cols, c + W, g, cols_next);
-            d_next = chunk_dense[c + W];
-        }
-        int d = chunk_dense[c];
-        AState32 cur = load_a_state32(d, c, lane, a_off, chunk_eptr, entries, evals, dense_a);
-        for (; c < end; c += W) {
-            const bool has1 = c + W < end;
-            load_b_half_f32<VEC, ALIGNED>(B, cols + 4, OL, c0, R1);
-            AState32 nxt = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};
-            if (has1) nxt = load_a_state32(d_next, c + W, lane, a_off, chunk_eptr, entries, evals,
-                                           dense_a);
-            floatx4 a_lo, a_hi;
-            if (d >= 0) {
-                a_lo = __builtin_bit_cast(floatx4, cur.x);
-                a_hi = __builtin_bit_cast(floatx4, cur.y);
-            } else {
-                const int eb = (int)cur.y.x, ee = (int)cur.y.y;
-                *reinterpret_cast<floatx4*>(my_a) = floatx4{0.f, 0.f, 0.f, 0.f};
-                *reinterpret_cast<floatx4*>(my_a + 4) = floatx4{0.f, 0.f, 0.f, 0.f};
-                wave_lds_sync();
-                if (eb + lane < ee) scatter_a_f32(Aw, cur.x.x, __uint_as_float(cur.x.z));
-                if (eb + 64 + lane < ee) scatter_a_f32(Aw, cur.x.y, __uint_as_float(cur.x.w));
-                for (int e = eb + 128 + lane; e < ee; e += 64) scatter_a_f32(Aw, entries[e], evals[e]);
-                wave_lds_sync();
-                a_lo = *reinterpret_cast<const floatx4*>(my_a);
-                a_hi = *reinterpret_cast<const floatx4*>(my_a + 4);
-                wave_lds_sync();
-            }
-            const float a[8] = {a_lo[0], a_lo[1], a_lo[2], a_lo[3],
-                                a_hi[0], a_hi[1], a_hi[2], a_hi[3]};
-            mfma_half_f32<VEC>(a, 0, cols, R0, acc);
-            int cols_after[8];
-            int d_after = -1;
-            if (has1) {
-                load_b_half_f32<VEC, ALIGNED>(B, cols_next, OL, c0, R0);
-                if (c + 2 * W < end) {
-                    load_cols_steps(chunk_cols, c + 2 * W, g, cols_after);
-                    d_after = chunk_dense[c + 2 * W];
-                }
-            }
-            mfma_half_f32<VEC>(a, 4, cols, R1, acc);
-            if (has1) {
-#pragma unroll
-                for (int i = 0; i < 8; ++i) { cols[i] = cols_next[i]; cols_next[i] = cols_after[i]; }
-                d = d_next;
-                d_next = d_after;
-                cur = nxt;
-            }
-        }
-    }
-}
+    FRows<VEC> X, Y;
+    int colsA[8], colsB[8];
+    float a[8];
+    TileMeta mA = tile_meta(c, chunk_dense, chunk_eptr);
+    load_cols8(chunk_cols, c, g, colsA);
+    const int c1 = min(c + W, last);
+    load_cols8(chunk_cols, c1, g, colsB);
+    TileMeta mB = tile_meta(c1, chunk_dense, chunk_eptr);
+    load_b_half_f32<VEC, ALIGNED>(B, colsA, 0, OL, c0, X);
+    AState32 sA = load_a32(mA, lane, a_off, entries, dense_a), sB;
+    for (; c + W < last; c += 2 * W) {
+        load_b_half_f32<VEC, ALIGNED>(B, colsA, 4, OL, c0, Y);
+        a_operand_f32(mA, sA, lane, Aw, my_a, a);
+        mfma_half_f32<VEC>(a, 0, colsA, X, acc);
 
-// Sparse FP32 panel on VALU: rows [r_first, r_first + r_count) of the panel, one row at a time
-// from the CSR.  Lane l owns CPL consecutive output columns k0 + CPL l (CPL = 2 at tileK = 128),
-// so every nonzero is one coalesced load of its B row slice plus CPL FMAs; the column index and
-// value are wave-uniform (scalar loads).  The row is added to C once; rows outside the mask
-// are skipped.
-template <int TK, bool ALIGNED>
-__device__ __forceinline__ void rows_f32_valu(const int4& U, int r_first, int r_count, int lane,
-                                              int k0, int O, const int* __restrict__ rp,
-                                              const int* __restrict__ col,
-                                              const float* __restrict__ val,
-                                              const float* __restrict__ B, float* __restrict__ C) {
-    constexpr int CPL = TK >= 64 ? TK / 64 : 1;
-    const int cc = k0 + CPL * lane;
-    const bool active = (TK >= 64 || lane < TK) && cc < O;
-    const long long OL = O;
-    const bool vec = ALIGNED && CPL == 2 && cc + 1 < O;
-    for (int rl = r_first; rl < r_first + r_count; ++rl) {
-        if (!((U.w >> rl) & 1)) continue;
-        const int r = U.x + rl;
-        const int p0 = rp[r], p1 = rp[r + 1];
-        float acc[CPL];
-#pragma unroll
-        for (int q = 0; q < CPL; ++q) acc[q] = 0.0f;
-        auto fma_row = [&](int c, float v) {
-            const float* src = B + (long long)c * OL + cc;
-            if (vec) {
-                const float2 b = *reinterpret_cast<const float2*>(src);
-                acc[0] += v * b.x;
-                acc[CPL - 1] += v * b.y;
-            } else {
-#pragma unroll
-                for (int q = 0; q < CPL; ++q)
-                    if (cc + q < O) acc[q] += v * src[q];
-            }
-        };
-        int p = p0;
-        if (active) {
-            for (; p + 4 <= p1; p += 4) {
-                const int ca = col[p], cb = col[p + 1], ccx = col[p + 2], cd = col[p + 3];
-                const float va = val[p], vb = val[p + 1], vc = val[p + 2], vd = val[p + 3];
-                fma_row(ca, va);
-                fma_row(cb, vb);
-                fma_row(ccx, vc);
-                fma_row(cd, vd);
-            }
-            for (; p < p1; ++p) fma_row(col[p], val[p]);
-            float* crow = C + (long long)r * OL + cc;
-            if (vec) {
-                float2 cv = *reinterpret_cast<float2*>(crow);
-                cv.x += acc[0];
-                cv.y += acc[CPL - 1];
-                *reinterpret_cast<float2*>(crow) = cv;
-            } else {
-#pragma unroll
-                for (int q = 0; q < CPL; ++q)
-                    if (cc + q < O) crow[q] += acc[q];
-            }
-        }
+        load_b_half_f32<VEC, ALIGNED>(B, colsB, 0, OL, c0, X);
+        sB = load_a32(mB, lane, a_off, entries, dense_a);
+        mfma_half_f32<VEC>(a, 4, colsA, Y, acc);
+        load_cols8(chunk_cols, c + 2 * W, g, colsA);
+        const TileMeta mA2 = tile_meta(c + 2 * W, chunk_dense, chunk_eptr);
+
+        load_b_half_f32<VEC, ALIGNED>(B, colsB, 4, OL, c0, Y);
+        a_operand_f32(mB, sB, lane, Aw, my_a, a);
+        mfma_half_f32<VEC>(a, 0, colsB, X, acc);
+
+        load_b_half_f32<VEC, ALIGNED>(B, colsA, 0, OL, c0, X);
+        sA = load_a32(mA2, lane, a_off, entries, dense_a);
+        mfma_half_f32<VEC>(a, 4, colsB, Y, acc);
+        const int c3 = min(c + 3 * W, last);
+        load_cols8(chunk_cols, c3, g, colsB);
+        mB = tile_meta(c3, chunk_dense, chunk_eptr);
+        mA = mA2;
+    }
+    load_b_half_f32<VEC, ALIGNED>(B, colsA, 4, OL, c0, Y);
+    a_operand_f32(mA, sA, lane, Aw, my_a, a);
+    mfma_half_f32<VEC>(a, 0, colsA, X, acc);
+    if (c < last) {  // two tiles left: c and c + W = last
+        load_b_half_f32<VEC, ALIGNED>(B, colsB, 0, OL, c0, X);
+        sB = load_a32(mB, lane, a_off, entries, dense_a);
+        mfma_half_f32<VEC>(a, 4, colsA, Y, acc);
+        load_b_half_f32<VEC, ALIGNED>(B, colsB, 4, OL, c0, Y);
+        a_operand_f32(mB, sB, lane, Aw, my_a, a);
+        mfma_half_f32<VEC>(a, 0, colsB, X, acc);
+        mfma_half_f32<VEC>(a, 4, colsB, Y, acc);
+    } else {
+        mfma_half_f32<VEC>(a, 4, colsA, Y, acc);
     }
 }
 
@@ -576,31 +553,25 @@ __global__ __launch_bounds__(64 * kWaves, 3) void k_spmm_f32(
     const int4* __restrict__ units, int num_units, int num_heavy,
     const int* __restrict__ chunk_eptr, const int* __restrict__ chunk_cols,
     const int* __restrict__ chunk_dense, const uint32_t* __restrict__ entries,
-    const float* __restrict__ evals, const float* __restrict__ dense_a,
-    const int* __restrict__ csr_rp, const int* __restrict__ csr_col,
-    const float* __restrict__ csr_val, const float* __restrict__ B, int O, bool c4,
+    const float* __restrict__ dense_a, const float* __restrict__ B, int O, bool c4,
     float* __restrict__ C) {
     constexpr int VEC = TK / 16;
     __shared__ __attribute__((aligned(16))) float At[kWaves][4 * 16 * 8];
     __shared__ __attribute__((aligned(16))) float P[kWaves * 16 * TK];
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
     int u;
     bool heavy;
     if (!schedule(num_units, num_heavy, wave, u, heavy)) return;
     const int4 U = units[u];
     const int k0 = blockIdx.y * TK;
-    if ((U.w >> 17) & 1) {  // sparse panel: VALU over its rows (a heavy one: 4 rows per wave)
-        rows_f32_valu<TK, ALIGNED>(U, heavy ? 4 * wave : 0, heavy ? 4 : 16, lane, k0, O, csr_rp,
-                                   csr_col, csr_val, B, C);
-        return;
-    }
     const int c0 = k0 + VEC * n;
     floatx4 acc[VEC];
 #pragma unroll
     for (int q = 0; q < VEC; ++q) acc[q] = floatx4{0.f, 0.f, 0.f, 0.f};
     tiles_f32<TK, ALIGNED>(heavy ? U.y + wave : U.y, U.z, heavy ? kWaves : 1, lane, n, g, c0,
-                           (long long)O, chunk_eptr, chunk_cols, chunk_dense, entries, evals,
-                           dense_a, B, At[wave], acc);
+                           (long long)O, chunk_eptr, chunk_cols, chunk_dense, entries, dense_a, B,
+                           At[wave], acc);
     if (heavy) merge_into_c<TK, kWaves>(acc, 1.0f, U, k0, O, c4, C, P);
     else merge_into_c<TK, 1>(acc, 1.0f, U, k0, O, c4, C, P);
 }
@@ -622,13 +593,11 @@ static void launch_tk(const DeviceFormat& F, const void* dB, bool b_f16, int O, 
         if (aligned)
             hipLaunchKernelGGL((k_spmm_f32<TK, true>), grid, block, 0, st, F.units.p, NU, NH,
                                F.chunk_eptr.p, F.chunk_cols.p, F.chunk_dense.p, F.entries.p,
-                               F.evals.p, F.dense_a32.p, F.csr_rp.p, F.csr_col.p, F.csr_val.p, B,
-                               O, c4, dC);
+                               F.dense_a32.p, B, O, c4, dC);
         else
             hipLaunchKernelGGL((k_spmm_f32<TK, false>), grid, block, 0, st, F.units.p, NU, NH,
                                F.chunk_eptr.p, F.chunk_cols.p, F.chunk_dense.p, F.entries.p,
-                               F.evals.p, F.dense_a32.p, F.csr_rp.p, F.csr_col.p, F.csr_val.p, B,
-                               O, c4, dC);
+                               F.dense_a32.p, B, O, c4, dC);
     } else if (b_f16) {
         const _Float16* B = static_cast<const _Float16*>(dB);
         if (aligned)
