@@ -433,11 +433,11 @@ static void check_err(const int* d_err, hipStream_t st) {
 
 // Panels of at most this many tiles are light units (one wave each, four per work-group);
 // larger panels become heavy units that the four waves of a work-group share and merge in LDS.
-// Small problems make every multi-tile panel heavy so that enough waves are in flight; large
-// ones keep panels of up to 16 tiles on a single wave.
-static int light_tile_limit(long long num_chunks) {
-    return (int)std::max(1LL, std::min(16LL, num_chunks / 8192));
-}
+// With fewer than 2048 panels one wave per panel leaves most of the 1024 SIMDs idle, so every
+// multi-tile panel is shared by a work-group; otherwise panels of up to 8 tiles stay on one
+// wave (measured on gfx950: 6 to 12 tiles are equally good for stencil and R-MAT matrices;
+// 4 starves the stencil of waves, 16 leaves R-MAT with long single-wave units).
+static int light_tile_limit(int num_panels) { return num_panels >= 2048 ? 8 : 1; }
 
 template <typename K>
 static void build_exec_layout_k(DeviceFormat& F, const int* trow, const int* tcol,
@@ -507,7 +507,7 @@ static void build_exec_layout_k(DeviceFormat& F, const int* trow, const int* tco
         }
     }
 
-    const int light_max = light_tile_limit(NC);
+    const int light_max = light_tile_limit(NP);
     DevBuf<int> nu(NP), ubase(NP + 1), nheavy(NP), hbase(NP + 1);
     LAUNCH(k_units_per_panel, NP, nch.p, NP, light_max, nu.p, nheavy.p);
     exclusive_sum<int, int>(nu.p, ubase.p, NP, st);
