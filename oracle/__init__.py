@@ -77,6 +77,7 @@ def lib():
         L.orc_cpu_spmm_f64_omp.argtypes = [i32p, i32p, f32p, C.c_int, C.c_int, f32p, C.c_int, f64p,
                                            C.c_int]
         L.orc_std_sort_by_key.argtypes = [i32p, C.c_longlong, i32p]
+        L.orc_heap_sort_by_key.argtypes = [i32p, C.c_longlong, i32p]
         L.orc_rcm_order.restype = C.c_int
         L.orc_rcm_order.argtypes = [i32p, i32p, C.c_int, C.c_int, i32p]
         L.orc_apply_column_permutation.restype = C.c_int
@@ -102,6 +103,8 @@ def ref_lib():
         R.ref_half_scale.argtypes = [C.POINTER(C.c_float), C.c_int]
         i32p, f32p = C.POINTER(C.c_int), C.POINTER(C.c_float)
         R.ref_std_sort_by_key.argtypes = [i32p, C.c_longlong, i32p]
+        R.ref_partial_sort_by_key.argtypes = [i32p, C.c_longlong, i32p]
+        R.ref_sort_adversary.argtypes = [C.c_int, i32p]
         R.ref_rcm_order.argtypes = [i32p, i32p, C.c_int, C.c_int, i32p]
         R.ref_apply_column_permutation.argtypes = [i32p, i32p, f32p, C.c_int, C.c_int, i32p, f32p,
                                                    C.c_int]
@@ -318,6 +321,26 @@ def apply_column_permutation(row_ptr, col, val, M: int, N: int, position, B=None
     if st != 0:
         raise MemoryError("orc_apply_column_permutation")
     return ci, vv, Bo
+
+
+def heap_sort_by_key(a, key) -> np.ndarray:
+    out = _i32(a).copy()
+    k = _i32(key)
+    lib().orc_heap_sort_by_key(_p(out, C.c_int), len(out), _p(k, C.c_int))
+    return out
+
+
+def ref_partial_sort_by_key(a, key) -> np.ndarray:
+    out = _i32(a).copy()
+    k = _i32(key)
+    ref_lib().ref_partial_sort_by_key(_p(out, C.c_int), len(out), _p(k, C.c_int))
+    return out
+
+
+def ref_sort_adversary(n: int) -> np.ndarray:
+    keys = np.zeros(max(n, 1), np.int32)
+    ref_lib().ref_sort_adversary(int(n), _p(keys, C.c_int))
+    return keys[:n]
 
 
 def ref_std_sort_by_key(a, key) -> np.ndarray:

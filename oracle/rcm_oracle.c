@@ -14,9 +14,12 @@
  *   orc_apply_column_permutation
  *                         apply_column_permutation (reorder.hpp:82-108)
  *
+ *   orc_heap_sort_by_key  the heapsort step alone (std::partial_sort(a, a + n, a + n))
+ *
  * Pinned by tests/test_oracle_rcm.py: orc_std_sort_by_key against the C++ std::sort of the
- * compiler here (oracle/_ref) on random inputs with many ties and on sizes around the
- * 16-element threshold; orc_rcm_order against the reference's rcm_column_order compiled from
+ * compiler here (oracle/_ref) on random inputs with many ties, on sizes around the 16-element
+ * threshold and on adversarial inputs that force the heapsort fallback (with ties);
+ * orc_heap_sort_by_key against std::partial_sort with ties; orc_rcm_order against the reference's rcm_column_order compiled from
  * its header (oracle/_ref) and the committed fixtures made by it; closed forms (a path
  * graph, a star, isolated columns, M > N rows that only add self-loops); the permutation
  * property and C = (A P)(P^T B) = A B.
@@ -136,6 +139,10 @@ static void ss_introsort(int *a, long lo, long hi, int depth, const int *key) {
         ss_introsort(a, cut, hi, depth, key);
         hi = cut;
     }
+}
+
+void orc_heap_sort_by_key(int *a, long long n, const int *key) {
+    if (n > 0) ss_heapsort(a, 0, (long)n, key);
 }
 
 void orc_std_sort_by_key(int *a, long long n, const int *key) {

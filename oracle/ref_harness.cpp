@@ -74,6 +74,36 @@ void ref_std_sort_by_key(int* a, long long n, const int* key) {
     std::sort(a, a + n, [&](int x, int y) { return key[x] < key[y]; });
 }
 
+// Keys that drive std::sort into its heapsort fallback: McIlroy's adversary ("A Killer
+// Adversary for Quicksort", Software: Practice and Experience 29(4), 1999) answers the sort's
+// comparisons lazily, freezing values so that every pivot is bad.  Running std::sort again on
+// the frozen keys takes the same path.  keys[n] receives a permutation of 0..n-1.
+void ref_sort_adversary(int n, int* keys) {
+    std::vector<int> val(n), a(n);
+    const int gas = n;
+    int nsolid = 0, candidate = 0;
+    for (int i = 0; i < n; ++i) { val[i] = gas; a[i] = i; }
+    std::sort(a.begin(), a.end(), [&](int x, int y) {
+        if (val[x] == gas && val[y] == gas) {
+            if (x == candidate) val[x] = nsolid++;
+            else val[y] = nsolid++;
+        }
+        if (val[x] == gas) candidate = x;
+        else if (val[y] == gas) candidate = y;
+        return val[x] < val[y];
+    });
+    for (int i = 0; i < n; ++i) {
+        if (val[i] == gas) val[i] = nsolid++;
+        keys[i] = val[i];
+    }
+}
+
+// std::partial_sort(a, a + n, a + n) with the same comparator: the heapsort step std::sort
+// falls back to.
+void ref_partial_sort_by_key(int* a, long long n, const int* key) {
+    std::partial_sort(a, a + n, a + n, [&](int x, int y) { return key[x] < key[y]; });
+}
+
 static CSR make_csr(const int* row_ptr, const int* col, const float* val, int M, int N) {
     CSR csr;
     csr.M = M; csr.N = N; csr.nnz = M ? row_ptr[M] : 0;

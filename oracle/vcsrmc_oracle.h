@@ -92,6 +92,8 @@ void orc_cpu_spmm_f64_omp(const int *row_ptr, const int *col, const float *val, 
 /* Column reordering (rcm_oracle.c; include/reorder.hpp:17-108). */
 /* std::sort(a, a + n, key[x] < key[y]) with the steps of GCC 11's libstdc++. */
 void orc_std_sort_by_key(int *a, long long n, const int *key);
+/* The heapsort step alone: std::partial_sort(a, a + n, a + n, key[x] < key[y]). */
+void orc_heap_sort_by_key(int *a, long long n, const int *key);
 /* rcm_column_order: position[N] = new position of each old column. */
 int orc_rcm_order(const int *row_ptr, const int *col, int M, int N, int *position);
 /* apply_column_permutation: relabels col in place and re-sorts each row (with val); if B and

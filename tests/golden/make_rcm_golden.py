@@ -1,8 +1,8 @@
 """Writes tests/golden/rcm_golden.npz: small CSR inputs with the positions that the reference's
 own rcm_column_order returns for them, the CSR and B that its apply_column_permutation makes
 (MuuSeoTia/VCSR_MC include/reorder.hpp:17-108, compiled from the header where it lies by
-oracle/Makefile into oracle/_ref), and std::sort results for tie-heavy inputs (the call the
-reference makes at reorder.hpp:67-68, as compiled here).
+oracle/Makefile into oracle/_ref), and std::sort results for tie-heavy and adversarial inputs
+(the call the reference makes at reorder.hpp:67-68, as compiled here).
 
 Run from the repository root:  python tests/golden/make_rcm_golden.py
 Needs oracle/_ref (built only where the reference sources are present).
@@ -62,6 +62,29 @@ def cases():
     return out
 
 
+def adversary_star(keys):
+    """Vertex 0 is a leaf of hub 1; hub 1's children are 2 .. n+1, child 2+i with keys[i]
+    private leaves, so its degree is keys[i] + 1.  The BFS starts at leaf 0 (the lowest id of
+    degree 1), reaches the hub, and sorts the hub's children by degree: the comparisons of an
+    adversarial std::sort input, which end in the heapsort fallback."""
+    n = len(keys)
+    N = 2 + n + int(np.sum(keys))
+    adj = [[] for _ in range(N)]
+
+    def edge(u, v):
+        adj[u].append(v)
+        adj[v].append(u)
+    edge(0, 1)
+    nxt = 2 + n
+    for i, k in enumerate(keys):
+        edge(1, 2 + i)
+        for _ in range(int(k)):
+            edge(2 + i, nxt)
+            nxt += 1
+    rp, col = csr_from_rows([sorted(a) for a in adj], N)
+    return rp, col, N
+
+
 def main():
     oracle.build(ref=True)
     if not oracle.ref_available():
@@ -69,10 +92,13 @@ def main():
     rng = np.random.default_rng(7)
     data = {}
     names = []
-    for name, rp, col, M, N in cases():
+    all_cases = cases()
+    rp, col, N = adversary_star(oracle.ref_sort_adversary(200) // 2)
+    all_cases.append(("adversary_star200", rp, col, N, N))
+    for name, rp, col, M, N in all_cases:
         pos = oracle.ref_rcm_order(rp, col, M, N)
         val = rng.uniform(-1, 1, col.size).astype(np.float32)
-        O = 3
+        O = 3 if N <= 2000 else 1
         B = rng.uniform(-1, 1, (N, O)).astype(np.float32)
         c2, v2, B2 = oracle.ref_apply_column_permutation(rp, col, val, M, N, pos, B.reshape(-1), O)
         data.update({f"{name}/row_ptr": rp, f"{name}/col": col, f"{name}/val": val,
@@ -89,6 +115,16 @@ def main():
         data[f"sort{i}/key"] = key
         data[f"sort{i}/sorted"] = oracle.ref_std_sort_by_key(a, key)
         sorts.append(f"sort{i}")
+    # adversarial keys (McIlroy) drive std::sort into its heapsort fallback; halving them makes
+    # pairs of equal keys while the fallback is still reached
+    for n in (200, 1000, 5000):
+        key = oracle.ref_sort_adversary(n) // 2
+        a = np.arange(n, dtype=np.int32)
+        name = f"adversary{n}"
+        data[f"{name}/a"] = a
+        data[f"{name}/key"] = key.astype(np.int32)
+        data[f"{name}/sorted"] = oracle.ref_std_sort_by_key(a, key)
+        sorts.append(name)
     data["cases"] = np.array(names)
     data["sorts"] = np.array(sorts)
     np.savez_compressed(OUT, **data)

@@ -57,6 +57,21 @@ def test_std_sort_against_compiled(orc):
         assert np.array_equal(orc.std_sort_by_key(a, key), orc.ref_std_sort_by_key(a, key)), t
 
 
+def test_heap_sort_step(orc):
+    rng = np.random.default_rng(5)
+    for n in range(0, 40):
+        key = rng.integers(0, 3, size=n).astype(np.int32)
+        got = orc.heap_sort_by_key(np.arange(n, dtype=np.int32), key)
+        assert sorted(got.tolist()) == list(range(n)) and np.all(np.diff(key[got]) >= 0)
+    if not orc.ref_available():
+        pytest.skip("oracle/_ref not built (reference sources absent)")
+    for t in range(300):
+        n = int(rng.integers(0, 500))
+        key = rng.integers(0, int(rng.integers(1, 6)), size=n + 3).astype(np.int32)
+        a = rng.permutation(n + 3)[:n].astype(np.int32)
+        assert np.array_equal(orc.heap_sort_by_key(a, key), orc.ref_partial_sort_by_key(a, key))
+
+
 def test_rcm_fixtures(orc, gold):
     for name in gold["cases"]:
         rp, col = gold[f"{name}/row_ptr"], gold[f"{name}/col"]
@@ -64,7 +79,7 @@ def test_rcm_fixtures(orc, gold):
         pos = orc.rcm_order(rp, col, M, N)
         assert np.array_equal(pos, gold[f"{name}/position"]), name
         c2, v2, B2 = orc.apply_column_permutation(rp, col, gold[f"{name}/val"], M, N, pos,
-                                                  gold[f"{name}/B"], 3)
+                                                  gold[f"{name}/B"], gold[f"{name}/B"].shape[1])
         assert np.array_equal(c2, gold[f"{name}/new_col"]), name
         assert np.array_equal(v2, gold[f"{name}/new_val"]), name
         assert np.array_equal(B2, gold[f"{name}/new_B"]), name
