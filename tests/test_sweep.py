@@ -1,0 +1,179 @@
+"""The corpus sweep protocol (vcsr_mc_amd/sweep.py; the reference's bench200/run200.py,
+rerun_noisy.py, analyze.py, orig_table.py): statistics against closed forms, and the run /
+rerun / table logic against a stub driver whose timings are known, so no GPU is needed.  The
+GPU test runs the real spmm_vcsr over a small corpus."""
+import csv
+import io
+import math
+import os
+import stat
+import sys
+
+import numpy as np
+import pytest
+
+from vcsr_mc_amd import sweep
+
+STUB = r'''#!/usr/bin/env python3
+# Stand-in for spmm_vcsr: one CSV row per call.  ms = base[matrix] * factor[algo]; a matrix
+# named noisy* is 10x slower on the first call of each algorithm (a slow process); algo "bad"
+# fails.  Calls are counted in a state file next to this script.
+import json, os, sys
+args = sys.argv[1:]
+opt = {args[i]: args[i + 1] for i in range(0, len(args) - 1) if args[i].startswith("--")}
+mtx, algo = opt["--mtx"], opt["--algo"]
+name = os.path.basename(mtx)[:-4]
+if algo == "bad":
+    sys.stderr.write("Unknown algorithm: bad\n"); sys.exit(2)
+state = os.path.join(os.path.dirname(os.path.abspath(__file__)), "calls.json")
+calls = json.load(open(state)) if os.path.exists(state) else {}
+key = name + "/" + algo
+calls[key] = calls.get(key, 0) + 1
+json.dump(calls, open(state, "w"))
+base = {"a": 1.0, "b": 2.0, "noisy": 4.0}[name]
+factor = {"rocsparse": 1.0, "rocsparse_fp16": 1.2, "vcsr_mc": 0.25, "vcsr_mc_fp32": 0.5}[algo]
+ms = base * factor * (10.0 if name == "noisy" and calls[key] == 1 else 1.0)
+mflop = 100.0 * base
+O = opt.get("--O", "128"); tk = opt.get("--tileK", "64")
+print("gpu,sm,mtx,O,segw,bundle,tileK,repeat,algo,ms,gflops,validation,rel_l2,setup_ms,"
+      "ms_mean,ms_median,convert_ms,upload_ms")
+print(f"stub,gfx950,{mtx},{O},32,16,{tk},10,{algo},{ms},{mflop / ms},pass,{1e-7 * factor},0,"
+      f"{ms * 1.1},{ms},0.5,0.25")
+'''
+
+
+@pytest.fixture
+def stub(tmp_path):
+    p = tmp_path / "bin" / "spmm_stub"
+    p.parent.mkdir()
+    p.write_text(STUB.replace("/usr/bin/env python3", sys.executable, 1))
+    p.chmod(p.stat().st_mode | stat.S_IEXEC)
+    return p
+
+
+@pytest.fixture
+def corpus(tmp_path):
+    d = tmp_path / "mtx"
+    d.mkdir()
+    for n in ("a", "b", "noisy"):
+        (d / f"{n}.mtx").write_text("%%MatrixMarket matrix coordinate real general\n1 1 1\n1 1 1\n")
+    c = tmp_path / "corpus.csv"
+    c.write_text("group,name,rows,cols,nnz\ng,a,1,1,10\ng,b,1,1,20\ng,noisy,1,1,30\n"
+                 "g,absent,1,1,40\n")
+    return c, d
+
+
+def rows_of(path):
+    with open(path, newline="") as fh:
+        return list(csv.DictReader(fh))
+
+
+def test_statistics_closed_forms():
+    assert sweep.median([3, 1, 2]) == 2 and sweep.median([4, 1, 3, 2]) == 2.5
+    gm, gs = sweep.geo_gstd([2.0, 8.0])  # logs ln2, ln8: mean ln4, sigma ln2
+    assert math.isclose(gm, 4.0) and math.isclose(gs, 2.0)
+    gm, gs = sweep.geo_gstd([5.0] * 7)
+    assert math.isclose(gm, 5.0) and math.isclose(gs, 1.0)
+    assert all(math.isnan(x) for x in sweep.geo_gstd([]))
+    assert sweep.matrix_name("/x/y/cop20k_A.mtx") == "cop20k_A"
+
+
+def test_run_writes_reference_columns(stub, corpus, tmp_path):
+    c, d = corpus
+    out = tmp_path / "r.csv"
+    log = io.StringIO()
+    n = sweep.run(stub, c, d, out, algos=["rocsparse", "vcsr_mc", "bad"], reps=2,
+                  extra=["--O", "64", "--tileK", "64"], log=log)
+    rows = rows_of(out)
+    assert n == len(rows) == 3 * 2 * 2  # 3 present matrices x 2 reps x 2 working algos
+    assert list(rows[0].keys()) == sweep.FIELDS
+    assert {r["rep"] for r in rows} == {"0", "1"}
+    assert {r["nnz"] for r in rows if sweep.matrix_name(r["mtx"]) == "b"} == {"20"}
+    assert all(r["O"] == "64" for r in rows)
+    text = log.getvalue()
+    assert "missing" in text and "absent.mtx" in text
+    assert "fail a bad rep0: Unknown algorithm: bad" in text
+
+
+def test_load_medians_and_gflops(stub, corpus, tmp_path):
+    c, d = corpus
+    out = tmp_path / "r.csv"
+    sweep.run(stub, c, d, out, algos=["rocsparse", "vcsr_mc"], reps=3, log=io.StringIO())
+    g, t, e, nnz = sweep.load(out, "ms")
+    assert t["a"]["vcsr_mc"] == 0.25 and t["b"]["rocsparse"] == 2.0
+    # noisy: first call 10x slower, median of three is the normal time
+    assert t["noisy"]["vcsr_mc"] == 1.0
+    assert math.isclose(g["b"]["vcsr_mc"], 200.0 / 0.5)
+    _, tm, _, _ = sweep.load(out, "ms_mean")
+    assert math.isclose(tm["a"]["rocsparse"], 1.1)
+    g2, _, _, _ = sweep.load(out, "ms_mean")
+    assert math.isclose(g2["a"]["rocsparse"], 100.0 / 1.1)
+    assert math.isclose(e["a"]["vcsr_mc"], 0.25e-7) and nnz["noisy"] == 30
+
+
+def test_rerun_replaces_noisy_rows(stub, corpus, tmp_path):
+    c, d = corpus
+    out = tmp_path / "results_O128.csv"
+    sweep.run(stub, c, d, out, algos=["rocsparse", "vcsr_mc"], reps=2, log=io.StringIO())
+    before = rows_of(out)
+    assert sweep.noisy_matrices(before) == ["noisy"]
+    done = sweep.rerun_noisy(stub, c, d, [out], algos=["rocsparse", "vcsr_mc"],
+                             extra=["--O", "999", "--repeat", "10"], log=io.StringIO())
+    assert done[str(out)] == ["noisy"]
+    after = rows_of(out)
+    raw = rows_of(tmp_path / "results_O128_raw.csv")
+    assert raw == before
+    noisy_rows = [r for r in after if sweep.matrix_name(r["mtx"]) == "noisy"]
+    assert len(noisy_rows) == sweep.RERUN_REPS * 2
+    assert all(float(r["ms"]) < 10 for r in noisy_rows)  # later calls are not slow
+    assert all(r["O"] == "128" for r in noisy_rows)  # --O comes from the results file
+    assert [r for r in after if sweep.matrix_name(r["mtx"]) != "noisy"] == \
+        [r for r in before if sweep.matrix_name(r["mtx"]) != "noisy"]
+    assert not (tmp_path / "results_O128_rerun_corpus.csv").exists()
+
+
+def test_table_speedups(stub, corpus, tmp_path):
+    c, d = corpus
+    paths = []
+    for O in (64, 128):
+        p = tmp_path / f"res_O{O}.csv"
+        sweep.run(stub, c, d, p, algos=sweep.DEFAULT_ALGOS, reps=3,
+                  extra=["--O", str(O)], log=io.StringIO())
+        paths.append(str(p))
+    buf = io.StringIO()
+    res = sweep.table(paths, out=buf)
+    s = res[("ms_median", 64, "vcsr_mc")]
+    assert s["n"] == 3 and math.isclose(s["geomean"], 4.0) and math.isclose(s["gstd"], 1.0)
+    assert s["wins"] == 3 and math.isclose(s["max_rel_l2"], 0.25e-7)
+    assert math.isclose(res[("ms_median", "all", "vcsr_mc_fp32")]["geomean"], 2.0)
+    assert res[("ms_median", "all", "vcsr_mc_fp32")]["n"] == 6
+    assert "Speedup over rocSPARSE default" in buf.getvalue()
+
+
+@pytest.mark.gpu
+def test_sweep_real_driver(tmp_path):
+    """The whole protocol with the real driver over three small Matrix Market files."""
+    rng = np.random.default_rng(8)
+    d = tmp_path / "mtx"
+    d.mkdir()
+    lines = ["group,name,rows,cols,nnz"]
+    for i, n in enumerate((200, 350, 500)):
+        ent = set()
+        while len(ent) < 6 * n:
+            ent.add((int(rng.integers(1, n + 1)), int(rng.integers(1, n + 1))))
+        with open(d / f"m{i}.mtx", "w") as fh:
+            fh.write(f"%%MatrixMarket matrix coordinate real general\n{n} {n} {len(ent)}\n")
+            for r, cc in sorted(ent):
+                fh.write(f"{r} {cc} {rng.uniform(-1, 1):.6f}\n")
+        lines.append(f"g,m{i},{n},{n},{len(ent)}")
+    c = tmp_path / "corpus.csv"
+    c.write_text("\n".join(lines) + "\n")
+    print("[case] sweep over 3 matrices", flush=True)
+    csvs, res = sweep.sweep(c, d, tag="t", widths=(32,), tileK=128, reps=2,
+                            logdir=tmp_path / "logs", outdir=tmp_path)
+    rows = rows_of(csvs[0])
+    assert len(rows) == 3 * 2 * len(sweep.DEFAULT_ALGOS)
+    assert all(r["validation"] == "pass" for r in rows)
+    assert all(r["tileK"] == "32" for r in rows)
+    for k in sweep.KERNELS:
+        assert res[("ms_median", 32, k)]["n"] == 3
