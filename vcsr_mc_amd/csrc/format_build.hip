@@ -380,7 +380,8 @@ __global__ void k_units_per_panel(const int* __restrict__ nch, int NP, int light
 }
 
 // Writes the units of panel j (in panel order) with their schedule keys: heavy units first,
-// then light; larger first inside each class (the stable sort keeps panel order on ties).
+// larger first; then light units in panel order (the stable sort keeps it), so that the
+// contiguous range of light units an XCD walks holds neighbouring panels.
 __global__ void k_make_units(const int* __restrict__ cbase, const int* __restrict__ ubase,
                              const int* __restrict__ ppanel, const int* __restrict__ pmask,
                              const int* __restrict__ nch, int NP, int light_max,
@@ -397,7 +398,7 @@ __global__ void k_make_units(const int* __restrict__ cbase, const int* __restric
         const int cb = c0 + u * step;
         const int ce = min(cb + step, c1);
         units[u0 + u] = make_int4(ppanel[j] * kPanelRows, cb, ce, (pmask[j] & 0xffff) | split);
-        key[u0 + u] = ((heavy ? 0u : 1u) << 16) | (uint32_t)(0xffff - min(ce - cb, 0xffff));
+        key[u0 + u] = heavy ? (uint32_t)(0xffff - min(ce - cb, 0xffff)) : (1u << 16);
         pay[u0 + u] = (uint32_t)(u0 + u);
     }
 }
@@ -406,6 +407,30 @@ __global__ void k_gather_units(const int4* __restrict__ in, const uint32_t* __re
                                int NU, int4* __restrict__ out) {
     const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     if (i < NU) out[i] = in[perm[i]];
+}
+
+// Tiles of light unit i (units sorted: heavy first).
+__global__ void k_light_tiles(const int4* __restrict__ units, int NH, int NL, int* __restrict__ nt) {
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < NL) nt[i] = units[NH + i].z - units[NH + i].y;
+}
+
+// xcd_start[x] = first light unit of XCD x: the cut where the running tile count reaches
+// x / 8 of the total (lower bound in the inclusive prefix `csum`).
+__global__ void k_xcd_cuts(const long long* __restrict__ csum, int NL, int* __restrict__ cut) {
+    const int x = threadIdx.x;
+    if (x > 8) return;
+    if (x == 0) { cut[0] = 0; return; }
+    if (x == 8) { cut[8] = NL; return; }
+    const long long total = csum[NL];
+    const long long target = total * x / 8;
+    int lo = 0, hi = NL;  // first i with csum[i] >= target (csum[i] = tiles of units < i)
+    while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        if (csum[mid] < target) lo = mid + 1;
+        else hi = mid;
+    }
+    cut[x] = lo;
 }
 
 static inline unsigned blocks(long long n) { return grid_for(n, 256); }
@@ -523,6 +548,17 @@ static void build_exec_layout_k(DeviceFormat& F, const int* trow, const int* tco
         radix_sort_pairs<uint32_t>(kp2, vp2, ka2, va2, NU, 17, st);
         F.units.alloc(NU);
         LAUNCH(k_gather_units, NU, raw.p, vp2, NU, F.units.p);
+    }
+    // Light units are split into eight contiguous ranges of about equal tile count, one per XCD.
+    {
+        const int NL = NU - NH;
+        DevBuf<int> nt(NL > 0 ? NL : 1), cut(9);
+        DevBuf<long long> csum((size_t)NL + 1);
+        LAUNCH(k_light_tiles, NL, F.units.p, NH, NL, nt.p);
+        exclusive_sum<int, long long>(nt.p, csum.p, NL, st);
+        hipLaunchKernelGGL(k_xcd_cuts, dim3(1), dim3(64), 0, st, csum.p, NL, cut.p);
+        VCSRMC_HIP(hipGetLastError());
+        VCSRMC_HIP(hipMemcpyAsync(F.xcd_start, cut.p, sizeof(int) * 9, hipMemcpyDeviceToHost, st));
         VCSRMC_HIP(hipStreamSynchronize(st));
     }
     F.num_panels = NP;
@@ -532,7 +568,6 @@ static void build_exec_layout_k(DeviceFormat& F, const int* trow, const int* tco
     F.light_max = light_max;
 }
 
-// CSR of the matrix from triples in any order (FP32 formats keep it for their VALU units).
 static void build_exec_layout(DeviceFormat& F, const int* trow, const int* tcol, const float* tval,
                               long long n, hipStream_t st) {
     F.num_panels = F.num_chunks = F.num_units = 0;

@@ -19,6 +19,11 @@ constexpr int kDenseMin = 192;
 constexpr int kHeavyTiles = 64;
 constexpr int kWaves = 4;
 
+// Light-unit ranges per XCD, passed to the multiply kernels by value.
+struct XcdSplit {
+    int start[9];
+};
+
 // A format on one device.
 //
 // Boundary arrays (the reference's VCSRMC, include/vcsr_formats.hpp:14-21, built or uploaded
@@ -30,7 +35,8 @@ constexpr int kWaves = 4;
 //                     a run of chunks of one 16-row panel; split = the panel has several
 //                     units, whose partial sums meet in C through atomics.  The first
 //                     num_heavy units are heavy (one work-group each, larger first), the rest
-//                     light (one wave each, four per work-group, larger first).
+//                     light (one wave each, four per work-group, in panel order; XCD x runs
+//                     the range starting at xcd_start[x], cut for equal tile counts).
 //   chunk_eptr[c]   = first entry of chunk c (chunk_eptr[num_chunks] = nnz)
 //   chunk_cols[32c+k] = column of the chunk's k-th distinct column, -1 past the end (FP32
 //                   formats: slot (k & 3) * 8 + (k >> 2), the order the FP32 kernel's lanes read)
@@ -52,6 +58,8 @@ struct DeviceFormat {
     DevBuf<float> val;
 
     int num_panels = 0, num_chunks = 0, num_units = 0, num_heavy = 0, light_max = 0;
+    // Light units [num_heavy + xcd_start[x], num_heavy + xcd_start[x + 1]) run on XCD x.
+    int xcd_start[9] = {0, 0, 0, 0, 0, 0, 0, 0, 0};
     DevBuf<int4> units;
     DevBuf<int> chunk_eptr, chunk_cols;
     DevBuf<uint32_t> entries;

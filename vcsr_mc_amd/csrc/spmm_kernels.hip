@@ -32,13 +32,6 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 constexpr int kApitch = 40;  // FP16 A tile row pitch in halves (80 B: conflict-free b128 reads)
 
-// Map a linear work-group id to a unit so that each XCD (work-groups are dealt to the 8 XCDs
-// round robin) walks a contiguous range of panels: neighbouring panels share B rows in L2.
-__device__ __forceinline__ int unit_of_block(int bid, int num_units) {
-    const int per = (num_units + 7) >> 3;
-    return (bid & 7) * per + (bid >> 3);
-}
-
 // Raw B values of the 8 tile rows a lane feeds into the MFMA B operand, one vector of VEC
 // consecutive output columns per row (kept in the storage type until use, so a prefetched load
 // is never waited for early by a conversion).
@@ -210,9 +203,11 @@ __device__ __forceinline__ uint4 load_a16(const TileMeta& m, int lane, int a_off
 
 // Schedule of a 4-wave work-group.  Work-groups [0, H8) run the heavy units (H8 = num_heavy
 // rounded up to a multiple of 8): the four waves share one unit's tiles.  The others run light
-// units, one per wave, mapped so that each XCD walks a contiguous range of them (work-groups
-// are dealt to the 8 XCDs round robin).  Returns false if this wave has nothing to do.
-__device__ __forceinline__ bool schedule(int num_units, int num_heavy, int wave, int& u,
+// units, one per wave.  Work-groups are dealt to the 8 XCDs round robin, so light work-group j
+// runs on XCD j mod 8 and takes the next four units of that XCD's range: each XCD walks
+// neighbouring panels (shared B rows stay in its L2) and the ranges hold equal tile counts.
+// Returns false if this wave has nothing to do.
+__device__ __forceinline__ bool schedule(int num_heavy, const XcdSplit& xs, int wave, int& u,
                                          bool& heavy) {
     const int h8 = (num_heavy + 7) & ~7;
     const int b = blockIdx.x;
@@ -222,10 +217,9 @@ __device__ __forceinline__ bool schedule(int num_units, int num_heavy, int wave,
         return b < num_heavy;
     }
     heavy = false;
-    const int nlw = (num_units - num_heavy + kWaves - 1) / kWaves;
-    const int j = unit_of_block(b - h8, nlw);
-    u = num_heavy + j * kWaves + wave;
-    return j < nlw && u < num_units;
+    const int j = b - h8, x = j & 7;
+    u = num_heavy + xs.start[x] + (j >> 3) * kWaves + wave;
+    return u < num_heavy + xs.start[x + 1];
 }
 
 // One FP16 tile: A operand (dense words, or the entries scattered into the wave's LDS tile),
@@ -325,7 +319,7 @@ constexpr int f16_min_waves() { return (sizeof(TB) == 2 && ALIGNED) ? 3 : 2; }
 
 template <int TK, typename TB, bool ALIGNED>
 __global__ __launch_bounds__(64 * kWaves, (f16_min_waves<TB, ALIGNED>())) void k_spmm_f16(
-    const int4* __restrict__ units, int num_units, int num_heavy,
+    const int4* __restrict__ units, int num_heavy, XcdSplit xs,
     const int* __restrict__ chunk_eptr, const int* __restrict__ chunk_cols,
     const int* __restrict__ chunk_dense, const uint32_t* __restrict__ entries,
     const _Float16* __restrict__ dense_a, const TB* __restrict__ B, int O, float scale, bool c4,
@@ -339,7 +333,7 @@ __global__ __launch_bounds__(64 * kWaves, (f16_min_waves<TB, ALIGNED>())) void k
     const int lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
     int u;
     bool heavy;
-    if (!schedule(num_units, num_heavy, wave, u, heavy)) return;
+    if (!schedule(num_heavy, xs, wave, u, heavy)) return;
     const int4 U = units[u];
     const int k0 = blockIdx.y * TK;
     const int c0 = k0 + VEC * n;
@@ -550,7 +544,7 @@ __device__ __forceinline__ void tiles_f32(int first, int end, int W, int lane, i
 
 template <int TK, bool ALIGNED>
 __global__ __launch_bounds__(64 * kWaves, 3) void k_spmm_f32(
-    const int4* __restrict__ units, int num_units, int num_heavy,
+    const int4* __restrict__ units, int num_heavy, XcdSplit xs,
     const int* __restrict__ chunk_eptr, const int* __restrict__ chunk_cols,
     const int* __restrict__ chunk_dense, const uint32_t* __restrict__ entries,
     const float* __restrict__ dense_a, const float* __restrict__ B, int O, bool c4,
@@ -562,7 +556,7 @@ __global__ __launch_bounds__(64 * kWaves, 3) void k_spmm_f32(
     const int lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
     int u;
     bool heavy;
-    if (!schedule(num_units, num_heavy, wave, u, heavy)) return;
+    if (!schedule(num_heavy, xs, wave, u, heavy)) return;
     const int4 U = units[u];
     const int k0 = blockIdx.y * TK;
     const int c0 = k0 + VEC * n;
@@ -584,39 +578,43 @@ static void launch_tk(const DeviceFormat& F, const void* dB, bool b_f16, int O, 
     const bool aligned = (O % VEC) == 0 && ((uintptr_t)dB % 16) == 0;
     const bool c4 = (O % 4) == 0 && ((uintptr_t)dC % 16) == 0;
     const int h8 = (F.num_heavy + 7) & ~7;
-    const int nlw = (F.num_units - F.num_heavy + kWaves - 1) / kWaves;
-    const dim3 grid((unsigned)(h8 + 8 * ((nlw + 7) / 8)), (unsigned)((O + TK - 1) / TK));
+    XcdSplit xs;
+    int per_xcd = 0;  // light work-groups per XCD
+    for (int x = 0; x < 9; ++x) xs.start[x] = F.xcd_start[x];
+    for (int x = 0; x < 8; ++x)
+        per_xcd = std::max(per_xcd, (xs.start[x + 1] - xs.start[x] + kWaves - 1) / kWaves);
+    const dim3 grid((unsigned)(h8 + 8 * per_xcd), (unsigned)((O + TK - 1) / TK));
     const dim3 block(64 * kWaves);
-    const int NU = F.num_units, NH = F.num_heavy;
+    const int NH = F.num_heavy;
     if (F.fp32) {
         const float* B = static_cast<const float*>(dB);
         if (aligned)
-            hipLaunchKernelGGL((k_spmm_f32<TK, true>), grid, block, 0, st, F.units.p, NU, NH,
+            hipLaunchKernelGGL((k_spmm_f32<TK, true>), grid, block, 0, st, F.units.p, NH, xs,
                                F.chunk_eptr.p, F.chunk_cols.p, F.chunk_dense.p, F.entries.p,
                                F.dense_a32.p, B, O, c4, dC);
         else
-            hipLaunchKernelGGL((k_spmm_f32<TK, false>), grid, block, 0, st, F.units.p, NU, NH,
+            hipLaunchKernelGGL((k_spmm_f32<TK, false>), grid, block, 0, st, F.units.p, NH, xs,
                                F.chunk_eptr.p, F.chunk_cols.p, F.chunk_dense.p, F.entries.p,
                                F.dense_a32.p, B, O, c4, dC);
     } else if (b_f16) {
         const _Float16* B = static_cast<const _Float16*>(dB);
         if (aligned)
-            hipLaunchKernelGGL((k_spmm_f16<TK, _Float16, true>), grid, block, 0, st, F.units.p, NU,
-                               NH, F.chunk_eptr.p, F.chunk_cols.p, F.chunk_dense.p, F.entries.p,
+            hipLaunchKernelGGL((k_spmm_f16<TK, _Float16, true>), grid, block, 0, st, F.units.p, NH,
+                               xs, F.chunk_eptr.p, F.chunk_cols.p, F.chunk_dense.p, F.entries.p,
                                F.dense_a16.p, B, O, F.scale, c4, dC);
         else
-            hipLaunchKernelGGL((k_spmm_f16<TK, _Float16, false>), grid, block, 0, st, F.units.p, NU,
-                               NH, F.chunk_eptr.p, F.chunk_cols.p, F.chunk_dense.p, F.entries.p,
+            hipLaunchKernelGGL((k_spmm_f16<TK, _Float16, false>), grid, block, 0, st, F.units.p, NH,
+                               xs, F.chunk_eptr.p, F.chunk_cols.p, F.chunk_dense.p, F.entries.p,
                                F.dense_a16.p, B, O, F.scale, c4, dC);
     } else {
         const float* B = static_cast<const float*>(dB);
         if (aligned)
-            hipLaunchKernelGGL((k_spmm_f16<TK, float, true>), grid, block, 0, st, F.units.p, NU,
-                               NH, F.chunk_eptr.p, F.chunk_cols.p, F.chunk_dense.p, F.entries.p,
+            hipLaunchKernelGGL((k_spmm_f16<TK, float, true>), grid, block, 0, st, F.units.p, NH,
+                               xs, F.chunk_eptr.p, F.chunk_cols.p, F.chunk_dense.p, F.entries.p,
                                F.dense_a16.p, B, O, F.scale, c4, dC);
         else
-            hipLaunchKernelGGL((k_spmm_f16<TK, float, false>), grid, block, 0, st, F.units.p, NU,
-                               NH, F.chunk_eptr.p, F.chunk_cols.p, F.chunk_dense.p, F.entries.p,
+            hipLaunchKernelGGL((k_spmm_f16<TK, float, false>), grid, block, 0, st, F.units.p, NH,
+                               xs, F.chunk_eptr.p, F.chunk_cols.p, F.chunk_dense.p, F.entries.p,
                                F.dense_a16.p, B, O, F.scale, c4, dC);
     }
     VCSRMC_HIP(hipGetLastError());
