@@ -93,15 +93,65 @@ __device__ __forceinline__ void wave_lds_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// C of a unit's output tile, read ahead of the merge (C += A.B needs it) so that its latency
+// overlaps the tile loop.  W == 1 (light): lane (n, g) reads rows 4g..4g+3 at columns
+// k0 + VEC n .. + VEC - 1 (VEC / 4 float4 per row), just before the wave's last tile is multiplied.
+// W > 1 (heavy): thread t reads the float4 at t*4 + 256 W j of the 16 x TK tile (the layout of
+// the merge) when the unit starts.  The loads are always issued -- rows outside the mask, split
+// panels, unaligned C and columns past O read kZeroRow instead -- so their number is fixed and a
+// wait for an older load never has to cover them.
+template <int TK, int W>
+struct CAhead {
+    static constexpr int VEC = TK / 16;
+    static constexpr int N = W == 1 ? (VEC >= 4 ? VEC : 0) : (16 * TK + 256 * W - 1) / (256 * W);
+    floatx4 v[N > 0 ? N : 1];
+};
+
+template <int TK, int W>
+__device__ __forceinline__ void read_c_ahead(CAhead<TK, W>& ca, const int4& U, int k0, int O,
+                                             bool c4, const float* __restrict__ C) {
+    constexpr int VEC = TK / 16;
+    constexpr int N = CAhead<TK, W>::N;
+    const int lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
+    const bool ok = c4 && !((U.w >> 16) & 1);
+    const long long OL = O;
+    if constexpr (W == 1) {
+        if constexpr (N > 0) {
+            const int c0 = k0 + VEC * n;
+            const bool lane_ok = ok && c0 + VEC <= O;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int rl = 4 * g + i;
+                const bool in = lane_ok && ((U.w >> rl) & 1);
+                const float* src = in ? C + (long long)(U.x + rl) * OL + c0 : kZeroRow;
+#pragma unroll
+                for (int h = 0; h < VEC / 4; ++h)
+                    ca.v[i * (VEC / 4) + h] = *reinterpret_cast<const floatx4*>(src + 4 * h);
+            }
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < N; ++j) {
+            const int e = threadIdx.x * 4 + j * 256 * W;
+            const int row = (e / TK) & 15, cc = k0 + e % TK;
+            const bool in = ok && e < 16 * TK && ((U.w >> row) & 1) && cc + 4 <= O;
+            const float* src = in ? C + (long long)(U.x + row) * OL + cc : kZeroRow;
+            ca.v[j] = *reinterpret_cast<const floatx4*>(src);
+        }
+    }
+}
+
 // Adds the unit's 16 x TK result into C.  W == 1: straight from the accumulators (lane (n, g)
 // owns rows 4g..4g+3, columns k0 + VEC n .. + VEC - 1).  W > 1: every wave parks its partial
 // tile in LDS, then the work-group sums the W partials and writes each row with consecutive
 // threads on consecutive columns.  Split panels merge through atomics; other rows are a
-// read-modify-write (C += A.B).  Rows outside the panel's row mask are never touched.
+// read-modify-write (C += A.B) whose read, on the vector path, came from read_c_ahead.  Rows
+// outside the panel's row mask are never touched.
 template <int TK, int W>
 __device__ __forceinline__ void merge_into_c(const floatx4 (&acc)[TK / 16], float scale,
                                              const int4& U, int k0, int O, bool c4,
-                                             float* __restrict__ C, float* P) {
+                                             float* __restrict__ C, float* P,
+                                             const CAhead<TK, W>& ca) {
     constexpr int VEC = TK / 16;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, n = lane & 15, g = lane >> 4;
     const bool split = (U.w >> 16) & 1;
@@ -120,7 +170,7 @@ __device__ __forceinline__ void merge_into_c(const floatx4 (&acc)[TK / 16], floa
             } else if (VEC >= 4 && c4 && c0 + VEC <= O) {
 #pragma unroll
                 for (int h = 0; h < VEC; h += 4) {
-                    floatx4 v = *reinterpret_cast<floatx4*>(crow + h);
+                    floatx4 v = ca.v[(i * (VEC / 4) + h / 4) % CAhead<TK, W>::N];
 #pragma unroll
                     for (int q = 0; q < 4; ++q) v[q] += acc[(h + q) % VEC][i] * scale;
                     *reinterpret_cast<floatx4*>(crow + h) = v;
@@ -138,7 +188,10 @@ __device__ __forceinline__ void merge_into_c(const floatx4 (&acc)[TK / 16], floa
 #pragma unroll
             for (int q = 0; q < VEC; ++q) Pw[(4 * g + i) * TK + VEC * n + q] = acc[q][i];
         __syncthreads();
-        for (int e = threadIdx.x * 4; e < 16 * TK; e += 64 * W * 4) {
+#pragma unroll
+        for (int j = 0; j < CAhead<TK, W>::N; ++j) {
+            const int e = threadIdx.x * 4 + j * 256 * W;
+            if (e >= 16 * TK) break;
             const int row = e / TK, col = e % TK;
             if (!((U.w >> row) & 1)) continue;
             floatx4 sum = *reinterpret_cast<const floatx4*>(P + e);
@@ -152,16 +205,16 @@ __device__ __forceinline__ void merge_into_c(const floatx4 (&acc)[TK / 16], floa
             float* crow = C + (long long)(U.x + row) * OL + cc;
             if (split) {
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    if (cc + j < O) atomicAdd(crow + j, sum[j] * scale);
+                for (int jj = 0; jj < 4; ++jj)
+                    if (cc + jj < O) atomicAdd(crow + jj, sum[jj] * scale);
             } else if (c4 && cc + 4 <= O) {
-                floatx4 v = *reinterpret_cast<floatx4*>(crow);
+                floatx4 v = ca.v[j];
                 v += sum * scale;
                 *reinterpret_cast<floatx4*>(crow) = v;
             } else {
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    if (cc + j < O) crow[j] += sum[j] * scale;
+                for (int jj = 0; jj < 4; ++jj)
+                    if (cc + jj < O) crow[jj] += sum[jj] * scale;
             }
         }
     }
@@ -259,7 +312,7 @@ __device__ __forceinline__ void mma_tile_f16(const TileMeta& m, const uint4& st,
 //   * column indices are loaded before the B rows and A state they lead to, so waiting for
 //     them does not wait for those;
 //   * every iteration issues the same loads (column indices past the last tile are clamped).
-template <int TK, typename TB, bool ALIGNED>
+template <int TK, typename TB, bool ALIGNED, typename Pre>
 __device__ __forceinline__ void tiles_f16(int first, int end, int W, int lane, int n, int g,
                                           int c0, long long OL, const int* __restrict__ chunk_eptr,
                                           const int* __restrict__ chunk_cols,
@@ -267,7 +320,7 @@ __device__ __forceinline__ void tiles_f16(int first, int end, int W, int lane, i
                                           const uint32_t* __restrict__ entries,
                                           const _Float16* __restrict__ dense_a,
                                           const TB* __restrict__ B, _Float16* Aw,
-                                          floatx4 (&acc)[TK / 16]) {
+                                          floatx4 (&acc)[TK / 16], Pre&& pre) {
     constexpr int VEC = TK / 16;
     if (first >= end) return;
     const int a_off = n * 32 + 8 * g;  // this lane's A operand inside a dense tile
@@ -302,12 +355,17 @@ __device__ __forceinline__ void tiles_f16(int first, int end, int W, int lane, i
         mA = mA2;
         mB = mB2;
     }
+    // `pre` runs before the last multiply when a single tile is left and the other B buffer is
+    // free (see read_c_ahead); with two tiles left, after them (holding both buffers and the C
+    // values at once would spill registers).
     if (c < last) {  // two tiles left: c and c + W = last
         load_b_rows<VEC, TB, ALIGNED>(B, colsB, OL, c0, RB);
         sB = load_a16(mB, lane, a_off, entries, dense_a);
         mma_tile_f16<VEC, TB>(mA, sA, lane, Aw, my_a, RA, acc);
         mma_tile_f16<VEC, TB>(mB, sB, lane, Aw, my_a, RB, acc);
+        pre();
     } else {
+        pre();
         mma_tile_f16<VEC, TB>(mA, sA, lane, Aw, my_a, RA, acc);
     }
 }
@@ -340,11 +398,22 @@ __global__ __launch_bounds__(64 * kWaves, (f16_min_waves<TB, ALIGNED>())) void k
     floatx4 acc[VEC];
 #pragma unroll
     for (int q = 0; q < VEC; ++q) acc[q] = floatx4{0.f, 0.f, 0.f, 0.f};
-    tiles_f16<TK, TB, ALIGNED>(heavy ? U.y + wave : U.y, U.z, heavy ? kWaves : 1, lane, n, g, c0,
-                               (long long)O, chunk_eptr, chunk_cols, chunk_dense, entries, dense_a,
-                               B, As[wave], acc);
-    if (heavy) merge_into_c<TK, kWaves>(acc, scale, U, k0, O, c4, C, P);
-    else merge_into_c<TK, 1>(acc, scale, U, k0, O, c4, C, P);
+    // Heavy and light units take separate copies of the tile loop, so that the compiler's load
+    // counting sees one fixed sequence of loads on each.
+    if (heavy) {
+        CAhead<TK, kWaves> ca;
+        read_c_ahead<TK, kWaves>(ca, U, k0, O, c4, C);
+        tiles_f16<TK, TB, ALIGNED>(U.y + wave, U.z, kWaves, lane, n, g, c0, (long long)O,
+                                   chunk_eptr, chunk_cols, chunk_dense, entries, dense_a, B,
+                                   As[wave], acc, [] {});
+        merge_into_c<TK, kWaves>(acc, scale, U, k0, O, c4, C, P, ca);
+    } else {
+        CAhead<TK, 1> ca;
+        tiles_f16<TK, TB, ALIGNED>(U.y, U.z, 1, lane, n, g, c0, (long long)O, chunk_eptr,
+                                   chunk_cols, chunk_dense, entries, dense_a, B, As[wave], acc,
+                                   [&] { read_c_ahead<TK, 1>(ca, U, k0, O, c4, C); });
+        merge_into_c<TK, 1>(acc, scale, U, k0, O, c4, C, P, ca);
+    }
 }
 
 // FP32 format: eight K steps of v_mfma_f32_16x16x4_f32 per tile; lane (n, g) feeds tile
@@ -478,7 +547,7 @@ __device__ __forceinline__ void a_operand_f32(const TileMeta& m, const AState32&
 //   2. load X (d), A state (d);  multiply steps 4-7 of c (Y); load columns of c + 2W
 //   3. load Y (d);               multiply steps 0-3 of d (X)
 //   4. load X (c + 2W), A state; multiply steps 4-7 of d (Y); load columns of c + 3W
-template <int TK, bool ALIGNED>
+template <int TK, bool ALIGNED, typename Pre>
 __device__ __forceinline__ void tiles_f32(int first, int end, int W, int lane, int n, int g,
                                           int c0, long long OL, const int* __restrict__ chunk_eptr,
                                           const int* __restrict__ chunk_cols,
@@ -486,7 +555,7 @@ __device__ __forceinline__ void tiles_f32(int first, int end, int W, int lane, i
                                           const uint32_t* __restrict__ entries,
                                           const float* __restrict__ dense_a,
                                           const float* __restrict__ B, float* Aw,
-                                          floatx4 (&acc)[TK / 16]) {
+                                          floatx4 (&acc)[TK / 16], Pre&& pre) {
     constexpr int VEC = TK / 16;
     if (first >= end) return;
     const int a_off = g * 128 + n * 8;
@@ -529,6 +598,7 @@ __device__ __forceinline__ void tiles_f32(int first, int end, int W, int lane, i
     load_b_half_f32<VEC, ALIGNED>(B, colsA, 4, OL, c0, Y);
     a_operand_f32(mA, sA, lane, Aw, my_a, a);
     mfma_half_f32<VEC>(a, 0, colsA, X, acc);
+    // `pre` runs before the last half tile is multiplied, once X is free (see read_c_ahead).
     if (c < last) {  // two tiles left: c and c + W = last
         load_b_half_f32<VEC, ALIGNED>(B, colsB, 0, OL, c0, X);
         sB = load_a32(mB, lane, a_off, entries, dense_a);
@@ -536,8 +606,10 @@ __device__ __forceinline__ void tiles_f32(int first, int end, int W, int lane, i
         load_b_half_f32<VEC, ALIGNED>(B, colsB, 4, OL, c0, Y);
         a_operand_f32(mB, sB, lane, Aw, my_a, a);
         mfma_half_f32<VEC>(a, 0, colsB, X, acc);
+        pre();
         mfma_half_f32<VEC>(a, 4, colsB, Y, acc);
     } else {
+        pre();
         mfma_half_f32<VEC>(a, 4, colsA, Y, acc);
     }
 }
@@ -563,11 +635,19 @@ __global__ __launch_bounds__(64 * kWaves, 3) void k_spmm_f32(
     floatx4 acc[VEC];
 #pragma unroll
     for (int q = 0; q < VEC; ++q) acc[q] = floatx4{0.f, 0.f, 0.f, 0.f};
-    tiles_f32<TK, ALIGNED>(heavy ? U.y + wave : U.y, U.z, heavy ? kWaves : 1, lane, n, g, c0,
-                           (long long)O, chunk_eptr, chunk_cols, chunk_dense, entries, dense_a, B,
-                           At[wave], acc);
-    if (heavy) merge_into_c<TK, kWaves>(acc, 1.0f, U, k0, O, c4, C, P);
-    else merge_into_c<TK, 1>(acc, 1.0f, U, k0, O, c4, C, P);
+    if (heavy) {
+        CAhead<TK, kWaves> ca;
+        read_c_ahead<TK, kWaves>(ca, U, k0, O, c4, C);
+        tiles_f32<TK, ALIGNED>(U.y + wave, U.z, kWaves, lane, n, g, c0, (long long)O, chunk_eptr,
+                               chunk_cols, chunk_dense, entries, dense_a, B, At[wave], acc, [] {});
+        merge_into_c<TK, kWaves>(acc, 1.0f, U, k0, O, c4, C, P, ca);
+    } else {
+        CAhead<TK, 1> ca;
+        tiles_f32<TK, ALIGNED>(U.y, U.z, 1, lane, n, g, c0, (long long)O, chunk_eptr, chunk_cols,
+                               chunk_dense, entries, dense_a, B, At[wave], acc,
+                               [&] { read_c_ahead<TK, 1>(ca, U, k0, O, c4, C); });
+        merge_into_c<TK, 1>(acc, 1.0f, U, k0, O, c4, C, P, ca);
+    }
 }
 
 template <int TK>
