@@ -48,6 +48,8 @@ def parse():
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--no-rocsparse", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
+    p.add_argument("--b-fp32", action="store_true",
+                   help="FP16 format with B left in FP32 (the reference's run_vcsr_mc_spmm_gpu path)")
     p.add_argument("--graph", action="store_true",
                    help="replay the timed steps from a captured HIP graph")
     p.add_argument("--copy-probe-mib", type=int, default=0,
@@ -100,7 +102,7 @@ def main():
     d_col = torch.from_numpy(A.col).to(dev)
     d_val = torch.from_numpy(A.val).to(dev)
     dB32 = torch.from_numpy(Bh).to(dev)
-    dB = dB32 if fp32 else dB32.half()
+    dB = dB32 if (fp32 or args.b_fp32) else dB32.half()
     C = torch.zeros((A.M, O), dtype=torch.float32, device=dev)
     torch.cuda.synchronize()
 
@@ -197,7 +199,7 @@ def main():
         "data": "synthetic",
         "config": {"workload": f"{w['name']}-{A.M} (config {cfg})", "M": A.M, "N": A.N,
                    "nnz": A.nnz, "O": O, "segw": SEGW, "tileK": args.tileK,
-                   "precision": prec, "B": "fp32" if fp32 else "fp16 in HBM",
+                   "precision": prec, "B": "fp32" if (fp32 or args.b_fp32) else "fp16 in HBM",
                    "accumulate": "C += A.B"},
         "kernel_ms": round(kernel_ms, 6),
         "kernel_ms_single_launch_median": round(ms_single_median, 6),

@@ -68,6 +68,9 @@ struct DeviceFormat {
     DevBuf<_Float16> dense_a16;
     DevBuf<float> dense_a32;
 
+    // FP32 B converted to binary16 for an FP16 format (spmm_launch), reused across calls.
+    mutable DevBuf<_Float16> b_half;
+
     bool ready = false;
     void clear() { *this = DeviceFormat(); }
 };

@@ -700,6 +700,20 @@ static void launch_tk(const DeviceFormat& F, const void* dB, bool b_f16, int O, 
     VCSRMC_HIP(hipGetLastError());
 }
 
+// B (n floats) to binary16, round to nearest even -- the conversion the FP16 kernel applies to
+// an FP32 operand, done once per call instead of once per gathered row.
+__global__ void k_b_to_half(const float* __restrict__ B, _Float16* __restrict__ out, long long n) {
+    const long long i = ((long long)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+    if (i + 4 <= n) {
+        const floatx4 v = *reinterpret_cast<const floatx4*>(B + i);
+        typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+        *reinterpret_cast<half4*>(out + i) =
+            half4{(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
+    } else {
+        for (long long j = i; j < n; ++j) out[j] = (_Float16)B[j];
+    }
+}
+
 void spmm_launch(const DeviceFormat& F, const void* dB, bool b_f16, int O, int tileK, float* dC,
                  hipStream_t st) {
     if (tileK != 16 && tileK != 32 && tileK != 64 && tileK != 128)
@@ -709,6 +723,19 @@ void spmm_launch(const DeviceFormat& F, const void* dB, bool b_f16, int O, int t
     if (F.fp32 && b_f16) throw Error(VCSRMC_ERR_ARG, "an FP32 format takes an FP32 B");
     if (F.num_units == 0 || O == 0) return;
     if (!dB || !dC) throw Error(VCSRMC_ERR_ARG, "null B or C");
+    // FP16 format, FP32 B: when B rows are used at least twice on average, converting B once
+    // (6 bytes per element) costs less than gathering FP32 rows, and the FP16-B kernel holds
+    // fewer registers (3 waves per SIMD instead of 2).  Same values: the kernel converts with
+    // the same rounding.
+    if (!F.fp32 && !b_f16 && F.nnz >= 2LL * F.N && ((uintptr_t)dB % 16) == 0) {
+        const long long n = (long long)F.N * O;
+        if ((long long)F.b_half.n < n) F.b_half.alloc((size_t)n);
+        hipLaunchKernelGGL(k_b_to_half, dim3(grid_for((n + 3) / 4, 256)), dim3(256), 0, st,
+                           static_cast<const float*>(dB), F.b_half.p, n);
+        VCSRMC_HIP(hipGetLastError());
+        dB = F.b_half.p;
+        b_f16 = true;
+    }
     switch (tileK) {
         case 16: launch_tk<16>(F, dB, b_f16, O, dC, st); break;
         case 32: launch_tk<32>(F, dB, b_f16, O, dC, st); break;
