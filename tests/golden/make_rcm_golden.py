@@ -19,6 +19,9 @@ sys.path.insert(0, ROOT)
 
 import oracle  # noqa: E402
 
+sys.path.insert(0, os.path.join(ROOT, "tests"))
+from golden_io import adversary_hub  # noqa: E402
+
 OUT = os.path.join(os.path.dirname(os.path.abspath(__file__)), "rcm_golden.npz")
 
 
@@ -125,6 +128,12 @@ def main():
         data[f"{name}/key"] = key.astype(np.int32)
         data[f"{name}/sorted"] = oracle.ref_std_sort_by_key(a, key)
         sorts.append(name)
+    # a 2000-child hub whose degrees are adversarial std::sort keys: the sort of that group is
+    # partitioned by work-groups on the GPU and reaches the heapsort fallback on a large range
+    keys = (oracle.ref_sort_adversary(2000) // 2).astype(np.int32)
+    rp, col, N = adversary_hub(keys)
+    data["hub2000/keys"] = keys
+    data["hub2000/position"] = oracle.ref_rcm_order(rp, col, N, N)
     data["cases"] = np.array(names)
     data["sorts"] = np.array(sorts)
     np.savez_compressed(OUT, **data)

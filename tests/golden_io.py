@@ -27,3 +27,29 @@ def load_cases():
         case["ref"] = ref
         out.append(case)
     return out
+
+
+def adversary_hub(keys):
+    """Symmetric pattern whose BFS sorts one large child group by the given degrees.
+
+    Vertex 0 is a leaf of hub 1 and, with the lowest (degree, id), the BFS root; the hub's
+    children are 2 .. n+1; child 2+i is joined to donors 0 .. keys[i]-1 of a shared pool
+    (vertices n+2 ...), so its degree is keys[i] + 1 and the hub's children are sorted by keys.
+    Returns (row_ptr, col, N)."""
+    keys = np.asarray(keys, np.int64)
+    n = len(keys)
+    donors = int(keys.max()) if n else 0
+    N = 2 + n + donors
+    src = [np.array([0, 1]), np.full(n, 1), 2 + np.arange(n)]
+    dst = [np.array([1, 0]), 2 + np.arange(n), np.full(n, 1)]
+    child = np.repeat(2 + np.arange(n), keys)
+    donor = 2 + n + (np.arange(int(keys.sum())) - np.repeat(np.cumsum(keys) - keys, keys))
+    src += [child, donor]
+    dst += [donor, child]
+    r = np.concatenate(src)
+    c = np.concatenate(dst)
+    order = np.lexsort((c, r))
+    r, c = r[order], c[order]
+    rp = np.zeros(N + 1, np.int64)
+    np.add.at(rp, r + 1, 1)
+    return np.cumsum(rp).astype(np.int32), c.astype(np.int32), N

@@ -48,6 +48,16 @@ def test_rcm_fixtures_gpu():
         assert np.array_equal(B2, gold[f"{name}/new_B"]), name
 
 
+def test_rcm_adversarial_hub_gpu():
+    """A 2000-child group sorted by adversarial degrees: work-group partition passes, then the
+    heapsort fallback on a 1960-element range, must give the reference's order."""
+    from golden_io import adversary_hub
+    gold = np.load(GOLDEN)
+    rp, col, N = adversary_hub(gold["hub2000/keys"])
+    say("rcm adversarial hub", N, col.size)
+    assert np.array_equal(gpu_rcm(rp, col, N, N), gold["hub2000/position"])
+
+
 def test_rcm_random_gpu(orc):
     rng = np.random.default_rng(11)
     for t in range(40):

@@ -85,6 +85,12 @@ def test_rcm_fixtures(orc, gold):
         assert np.array_equal(B2, gold[f"{name}/new_B"]), name
 
 
+def test_rcm_adversarial_hub(orc, gold):
+    from golden_io import adversary_hub
+    rp, col, N = adversary_hub(gold["hub2000/keys"])
+    assert np.array_equal(orc.rcm_order(rp, col, N, N), gold["hub2000/position"])
+
+
 def test_rcm_against_compiled(orc):
     if not orc.ref_available():
         pytest.skip("oracle/_ref not built (reference sources absent)")

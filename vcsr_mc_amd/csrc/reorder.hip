@@ -15,8 +15,9 @@
 //      belongs to the earliest level-L vertex adjacent to it (the one that pops it from the
 //      reference's queue, reorder.hpp:63-66).  A level is ordered by that parent's index, then
 //      inside one parent's children as the reference orders them: ascending id, then
-//      std::sort by degree (reorder.hpp:67-69), whose steps (libstdc++ introsort) one thread per
-//      child group carries out exactly, since equal degrees make the result depend on them.
+//      std::sort by degree (reorder.hpp:67-69), whose steps (libstdc++ introsort) are carried
+//      out exactly, since equal degrees make the result depend on them: large groups a
+//      partition step at a time by work-groups, pieces of up to 256 elements by one thread.
 //   5. order: vertices sorted by (component rank, level, index in level) give the
 //      Cuthill-McKee order; position = N - 1 - that index (reorder.hpp:72-76).
 #include <algorithm>
@@ -366,13 +367,16 @@ struct SortRange {
     int lo, hi, depth;
 };
 
-__device__ void ls_std_sort(u64* a, int n) {
-    if (n <= 1) return;
-    int lg = 0;
-    while ((2ll << lg) <= n) ++lg;
+// std::sort's introsort loop on a[lo, hi) from partition depth `depth`, then its insertion
+// pass over the same range.  Ranges that the loop leaves untouched are independent, so any
+// subrange the partitions produce can be finished on its own: the insertion pass never moves
+// an element across a partition boundary (left part <= pivot <= right part, and it only moves
+// past strictly greater keys).
+__device__ void ls_sort_range(u64* a, int lo0, int hi0, int depth0) {
+    if (hi0 - lo0 <= 1) return;
     SortRange stack[64];
     int sp = 0;
-    stack[sp++] = {0, n, 2 * lg};
+    stack[sp++] = {lo0, hi0, depth0};
     while (sp > 0) {
         const SortRange r = stack[--sp];
         long long lo = r.lo, hi = r.hi;
@@ -389,17 +393,124 @@ __device__ void ls_std_sort(u64* a, int n) {
             hi = cut;
         }
     }
-    const int head = n > 16 ? 16 : n;
-    for (int i = 1; i < head; ++i) ls_insert(a, 0, i);
-    for (int i = 16; i < n; ++i) ls_insert(a, 0, i);
+    for (int i = lo0 + 1; i < hi0; ++i) ls_insert(a, lo0, i);
 }
 
-__global__ void k_group_sort(const int* __restrict__ gstart, int ngroups, int n,
-                             u64* __restrict__ packed) {
+__device__ __forceinline__ int lg_floor(int n) {
+    int lg = 0;
+    while ((2ll << lg) <= n) ++lg;
+    return lg;
+}
+
+// Ranges of at most this many elements are sorted by one thread; larger ones are partitioned by
+// a work-group first.
+constexpr int kSortSmall = 256;
+
+// One job per child group: (begin, end, partition depth 2 floor(lg n)).
+__global__ void k_group_jobs(const int* __restrict__ gstart, int ngroups, int n,
+                             int4* __restrict__ big, int* __restrict__ nbig,
+                             int4* __restrict__ small, int* __restrict__ nsmall) {
     const long long g = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     if (g >= ngroups) return;
     const int b = gstart[g], e = g + 1 < ngroups ? gstart[g + 1] : n;
-    ls_std_sort(packed + b, e - b);
+    if (e - b <= 1) return;
+    const int4 job = make_int4(b, e, 2 * lg_floor(e - b), 0);
+    if (e - b > kSortSmall) big[atomicAdd(nbig, 1)] = job;
+    else small[atomicAdd(nsmall, 1)] = job;
+}
+
+__global__ void k_small_sort(const int4* __restrict__ jobs, int njobs, u64* __restrict__ a) {
+    const long long j = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (j < njobs) ls_sort_range(a, jobs[j].x, jobs[j].y, jobs[j].z);
+}
+
+// One step of the introsort loop on a large range, by a whole work-group, with the same result
+// as the library's sequential step.  After the median of three is moved to a[lo], the Hoare
+// scans over a[lo+1, hi) stop, from the left, at elements whose key is not below the pivot's
+// (l_1 < l_2 < ...) and, from the right, at elements whose key is not above it
+// (r_1 > r_2 > ...); the k-th swap exchanges a[l_k] and a[r_k] while l_k < r_k, so K = the
+// number of left stops x with at least rank(x) right stops after x; the cut is l_1 when K = 0,
+// else min(l_{K+1}, r_K).  Both parts continue with depth - 1; a range at depth 0 is heapsorted.
+__global__ __launch_bounds__(256) void k_partition_pass(
+    const int4* __restrict__ jobs, int4* __restrict__ next, int* __restrict__ nnext,
+    int4* __restrict__ small, int* __restrict__ nsmall, u64* a, int* __restrict__ lpos,
+    int* __restrict__ rpos) {
+    __shared__ int wsum[4];
+    __shared__ int sh_lnext;
+    const int4 job = jobs[blockIdx.x];
+    const int lo = job.x, hi = job.y, depth = job.z;
+    const int t = threadIdx.x;
+    if (depth == 0) {
+        if (t == 0) ls_heapsort(a, lo, hi);  // sorted: the insertion pass would change nothing
+        return;
+    }
+    if (t == 0) {
+        ls_median_to_first(a, lo, lo + 1, lo + (hi - lo) / 2, hi - 1);
+        sh_lnext = INT_MAX;
+    }
+    __syncthreads();
+    const uint32_t kp = skey(a[lo]);
+    const int first = lo + 1, n = hi - first;
+    const int per = (n + 255) / 256;
+    const int b0 = min(first + t * per, hi), b1 = min(b0 + per, hi);
+    int cge = 0, cle = 0;
+    for (int p = b0; p < b1; ++p) {
+        const uint32_t k = skey(a[p]);
+        cge += !(k < kp);
+        cle += !(kp < k);
+    }
+    int GE, LE;
+    const int ge_before = block_scan_256(cge, OpAdd{}, 0, wsum, GE) - cge;
+    const int le_before = block_scan_256(cle, OpAdd{}, 0, wsum, LE) - cle;
+    (void)GE;
+    // K: left stops x (rank r) with LE - (right stops at or before x) >= r.
+    int kc = 0;
+    {
+        int rank = ge_before, le_incl = le_before;
+        for (int p = b0; p < b1; ++p) {
+            const uint32_t k = skey(a[p]);
+            le_incl += !(kp < k);
+            if (!(k < kp)) {
+                ++rank;
+                kc += (LE - le_incl >= rank);
+            }
+        }
+    }
+    int K;
+    block_scan_256(kc, OpAdd{}, 0, wsum, K);
+    // Pair positions: lpos[lo + r - 1] = l_r, rpos[lo + r - 1] = r_r for r <= K; and l_{K+1}.
+    {
+        int rank = ge_before, le_excl = le_before;
+        for (int p = b0; p < b1; ++p) {
+            const uint32_t k = skey(a[p]);
+            if (!(k < kp)) {
+                ++rank;
+                if (rank <= K) lpos[lo + rank - 1] = p;
+                else if (rank == K + 1) sh_lnext = p;
+            }
+            if (!(kp < k)) {
+                const int rr = LE - le_excl;  // right stops in [p, hi)
+                if (rr <= K) rpos[lo + rr - 1] = p;
+                ++le_excl;
+            }
+        }
+    }
+    __syncthreads();
+    for (int r = t; r < K; r += 256) {
+        const int x = lpos[lo + r], y = rpos[lo + r];
+        const u64 ax = a[x], ay = a[y];
+        a[x] = ay;
+        a[y] = ax;
+    }
+    if (t == 0) {
+        const int cut = K == 0 ? sh_lnext : min(sh_lnext, rpos[lo + K - 1]);
+        const int d = depth - 1;
+        const int4 left = make_int4(lo, cut, d, 0), right = make_int4(cut, hi, d, 0);
+        if (cut - lo > kSortSmall) next[atomicAdd(nnext, 1)] = left;
+        else small[atomicAdd(nsmall, 1)] = left;
+        if (hi - cut > kSortSmall) next[atomicAdd(nnext, 1)] = right;
+        else small[atomicAdd(nsmall, 1)] = right;
+    }
 }
 
 __global__ void k_level_write(const u64* __restrict__ packed, int n, int level, int base,
@@ -480,6 +591,44 @@ void row_of_nonzeros(const int* rp, int M, int nnz, int* row_of, hipStream_t st)
     fill<int>(headmark.p, nnz, (int)0x80000000, st);
     RLAUNCH(k_mark_heads, M, rp, M, headmark.p);
     inclusive_max(headmark.p, row_of, nnz, st);
+}
+
+// Work lists of the child-group sort, sized for the largest level (a range never holds fewer
+// than one element, so there are at most N ranges of each kind).
+struct SortJobs {
+    DevBuf<int4> big0, big1, small;
+    DevBuf<int> lpos, rpos, counts;  // counts: {big0, big1, small}
+    explicit SortJobs(int N)
+        : big0(N), big1(N), small(N), lpos(N), rpos(N), counts(3) {}
+};
+
+// Each child group of one level sorted by degree with std::sort's steps: large ranges are
+// partitioned a step at a time by work-groups until every piece holds at most kSortSmall
+// elements (or reached heapsort), then one thread per piece finishes it.
+void sort_groups(const int* gstart, int ngroups, int n, u64* packed, SortJobs& J, hipStream_t st) {
+    VCSRMC_HIP(hipMemsetAsync(J.counts.p, 0, sizeof(int) * 3, st));
+    RLAUNCH(k_group_jobs, ngroups, gstart, ngroups, n, J.big0.p, J.counts.p, J.small.p,
+            J.counts.p + 2);
+    int4* cur = J.big0.p;
+    int4* nxt = J.big1.p;
+    int* ccur = J.counts.p;
+    int* cnxt = J.counts.p + 1;
+    int counts[3];
+    VCSRMC_HIP(hipMemcpyAsync(counts, J.counts.p, sizeof(counts), hipMemcpyDeviceToHost, st));
+    VCSRMC_HIP(hipStreamSynchronize(st));
+    int nbig = counts[0], nsmall = counts[2];
+    const bool passes = nbig > 0;
+    while (nbig > 0) {
+        VCSRMC_HIP(hipMemsetAsync(cnxt, 0, sizeof(int), st));
+        hipLaunchKernelGGL(k_partition_pass, dim3(nbig), dim3(256), 0, st, cur, nxt, cnxt,
+                           J.small.p, J.counts.p + 2, packed, J.lpos.p, J.rpos.p);
+        VCSRMC_HIP(hipGetLastError());
+        nbig = read_scalar(cnxt, st);
+        std::swap(cur, nxt);
+        std::swap(ccur, cnxt);
+    }
+    if (passes) nsmall = read_scalar(J.counts.p + 2, st);
+    RLAUNCH(k_small_sort, nsmall, J.small.p, nsmall, packed);
 }
 
 }  // namespace
@@ -563,6 +712,7 @@ void rcm_order_device(const int* rp, const int* col, int M, int N, int nnz, int*
     DevBuf<uint32_t> v1(N), v2(N);
     DevBuf<int> gflag(N), gstart(N);
     DevBuf<long long> gpos((size_t)N + 1);
+    SortJobs jobs(N);
     int base = f;
     for (int level = 1; f > 0 && base < N; ++level) {
         RLAUNCH(k_front_degree, f, front.p, f, head.p, fdeg.p);
@@ -584,7 +734,7 @@ void rcm_order_device(const int* rp, const int* col, int M, int N, int nnz, int*
         const int ngroups = (int)read_scalar(gpos.p + n, st);
         u64* packed = kb;  // free half of the key double buffer
         RLAUNCH(k_group_pack, n, gflag.p, gpos.p, va, n, head.p, gstart.p, packed);
-        RLAUNCH(k_group_sort, ngroups, gstart.p, ngroups, n, packed);
+        sort_groups(gstart.p, ngroups, n, packed, jobs, st);
         RLAUNCH(k_level_write, n, packed, n, level, base, front.p, lev.p, seq.p);
         base += n;
         f = n;
