@@ -73,9 +73,8 @@ def main():
     args = parse()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
-        print("bench.py measures one GPU: every box in this build has a single MI355X and the "
-              "VCSR-MC path runs on one device (see DESIGN.md for how it would shard).",
-              file=sys.stderr)
+        print("bench.py measures one GPU (--gpus 1): the VCSR-MC path runs on one device; "
+              "splitting it across GPUs by output columns is not implemented.", file=sys.stderr)
         sys.exit(2)
 
     import numpy as np
