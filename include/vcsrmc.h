@@ -96,7 +96,9 @@ int vcsrmc_download(vcsrmc_t h, int *group_ptr, int *group_depth, int *group_seg
  * `stream`, the call waits for it and *ms is the elapsed time (the reference's protocol);
  * if ms is NULL the launch is asynchronous.  An FP16 format given FP32 B with nnz >= 2 N
  * converts B to binary16 once per call into a buffer the handle keeps (N x O halves, allocated
- * on first use), so calls on one handle from several streams at once must not overlap.
+ * on first use), so calls on one handle from several streams at once must not overlap.  The
+ * launch itself allocates and clears nothing, so it can be captured in a HIP graph (make that
+ * first FP32-B call before capturing).
  * Replaces run_vcsr_mc_spmm_gpu (include/vcsr_formats.hpp:24-25, src/vcsr_mc.cu:352-394). */
 int vcsrmc_spmm(vcsrmc_t h, const void *dB, int b_dtype, int O, int tileK, float *dC,
                 void *stream, float *ms);
