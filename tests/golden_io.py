@@ -1,5 +1,6 @@
 """Loader for tests/golden/vcsrmc_golden.npz (written by tests/golden/make_golden.py from the
-reference's own csr_to_vcsr_mc)."""
+reference's own csr_to_vcsr_mc), and builders of the structured patterns the reordering tests
+share."""
 import json
 import os
 
@@ -53,3 +54,26 @@ def adversary_hub(keys):
     rp = np.zeros(N + 1, np.int64)
     np.add.at(rp, r + 1, 1)
     return np.cumsum(rp).astype(np.int32), c.astype(np.int32), N
+
+
+def banded(N, bw):
+    """N x N pattern with columns r - bw .. r + bw in row r."""
+    r = np.repeat(np.arange(N), 2 * bw + 1)
+    c = r + np.tile(np.arange(-bw, bw + 1), N)
+    keep = (c >= 0) & (c < N)
+    rp = np.zeros(N + 1, np.int64)
+    np.add.at(rp, r[keep] + 1, 1)
+    return np.cumsum(rp).astype(np.int32), c[keep].astype(np.int32)
+
+
+def grid5(nx, ny):
+    """5-point stencil on an nx x ny grid, vertex x * ny + y."""
+    rows = []
+    for x in range(nx):
+        for y in range(ny):
+            v = x * ny + y
+            rows.append(sorted(w for w, ok in ((v - ny, x > 0), (v - 1, y > 0), (v, True),
+                                               (v + 1, y < ny - 1), (v + ny, x < nx - 1)) if ok))
+    rp = np.zeros(len(rows) + 1, np.int32)
+    rp[1:] = np.cumsum([len(r) for r in rows])
+    return rp, np.concatenate(rows).astype(np.int32)

@@ -9,6 +9,7 @@ import pytest
 import vcsr_mc_amd as vm
 from conftest import random_csr
 from gpu_util import dev, say, row_l1_parity
+from golden_io import banded, grid5
 
 pytestmark = pytest.mark.gpu
 
@@ -81,6 +82,27 @@ def test_rcm_workloads_gpu(orc, config, size):
     c2, v2, B2 = gpu_apply(A.row_ptr, A.col, A.val, A.M, A.N, pos, B, O)
     e2, w2, D2 = orc.apply_column_permutation(A.row_ptr, A.col, A.val, A.M, A.N, pos, B, O)
     assert np.array_equal(c2, e2) and np.array_equal(v2, w2) and np.array_equal(B2, D2)
+
+
+@pytest.mark.parametrize("N", [1100, 2000, 20000])
+def test_rcm_path_gpu(N):
+    """Deep walks: the levels run inside one work-group.  Vertex 0 has the lowest (degree, id),
+    the walk is 0, 1, ..., N - 1, so position[c] = N - 1 - c.  Long union-find chains here once
+    left non-root parents behind (a path-halving store landing after the final root)."""
+    rp, col = banded(N, 1)
+    say("rcm path", N)
+    assert np.array_equal(gpu_rcm(rp, col, N, N), N - 1 - np.arange(N))
+
+
+@pytest.mark.parametrize("shape", [("band", 100000, 10), ("grid", 400, 400), ("grid", 90, 700)])
+def test_rcm_banded_and_grid_gpu(orc, shape):
+    """Frontiers that grow past one work-group (grids: anti-diagonals up to 400 vertices with
+    up to 5 edges each) switch between the work-group levels and the multi-kernel levels."""
+    kind, a, b = shape
+    rp, col = banded(a, b) if kind == "band" else grid5(a, b)
+    N = rp.size - 1
+    say("rcm", kind, a, b, N, col.size)
+    assert np.array_equal(gpu_rcm(rp, col, N, N), orc.rcm_order(rp, col, N, N))
 
 
 def test_rcm_no_nonzeros_gpu():

@@ -102,6 +102,16 @@ def test_rcm_against_compiled(orc):
         assert np.array_equal(orc.rcm_order(rp, col, M, N), orc.ref_rcm_order(rp, col, M, N)), t
 
 
+def test_rcm_band_and_grid_against_compiled(orc):
+    """Structured patterns (deep walks, wide anti-diagonal levels) beside the random ones."""
+    if not orc.ref_available():
+        pytest.skip("oracle/_ref not built (reference sources absent)")
+    from golden_io import banded, grid5
+    for rp, col in (banded(3000, 1), banded(2500, 4), grid5(40, 70), grid5(1, 300)):
+        N = rp.size - 1
+        assert np.array_equal(orc.rcm_order(rp, col, N, N), orc.ref_rcm_order(rp, col, N, N))
+
+
 def test_rcm_path_graph(orc):
     # tridiagonal: vertex 0 has the lowest (degree, id), the BFS walks 0, 1, ..., N-1
     N = 50

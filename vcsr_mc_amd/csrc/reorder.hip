@@ -180,19 +180,19 @@ __global__ void k_uf_hook(const int* __restrict__ adj_u, const int* __restrict__
     }
 }
 
-__global__ void k_uf_flatten(int* parent, int N) {
+// comp[v] = the root of v's tree.  No hook runs any more, so every walk ends at the true root;
+// the walks still halve paths in parent[], and a halving store may land after another thread
+// has written a shorter path there, so the roots go to their own array rather than parent[].
+__global__ void k_uf_components(int* parent, int N, int* __restrict__ comp) {
     const long long v = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (v < N) {
-        const int r = uf_root(parent, (int)v);
-        __hip_atomic_store(parent + v, r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
+    if (v < N) comp[v] = uf_root(parent, (int)v);
 }
 
 // ---- 4. levels ---------------------------------------------------------------------------
-__global__ void k_root_flags(const uint32_t* __restrict__ order, const int* __restrict__ parent,
+__global__ void k_root_flags(const uint32_t* __restrict__ order, const int* __restrict__ comp,
                              int N, int* __restrict__ flag) {
     const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < N) flag[i] = parent[order[i]] == (int)order[i] ? 1 : 0;
+    if (i < N) flag[i] = comp[order[i]] == (int)order[i] ? 1 : 0;
 }
 
 __global__ void k_root_list(const uint32_t* __restrict__ order, const int* __restrict__ flag,
@@ -524,13 +524,119 @@ __global__ void k_level_write(const u64* __restrict__ packed, int n, int level, 
     seq[u] = base + (int)i;
 }
 
+// ---- 4b. small levels in one work-group ---------------------------------------------------
+// While a level has at most kBfsThreads frontier vertices and frontier edges, one work-group
+// runs level after level with no host round trip: one thread per frontier edge claims (atomic
+// minimum of the frontier index, as k_claim), then an edge holds a child when its frontier
+// vertex won the claim.  Frontier vertices are in level order and each adjacency list is in
+// ascending id, so an exclusive scan over the edges places the children in (parent index,
+// ascending id) order directly; each parent's children are then sorted by degree with
+// std::sort's steps, one thread per parent, in LDS.  The work-group stops at the first level
+// that does not fit (state.w = 0: the frontier is left in front[]) or when the walk ends
+// (state.w = 1).  state = {frontier size, vertices placed, level, finished}.
+constexpr int kBfsThreads = 1024;
+
+template <int NW>
+__device__ __forceinline__ int block_scan_int(int x, int* wsum /* LDS[NW] */, int& total) {
+    const int t = threadIdx.x, w = t >> 6;
+    const int incl = wave_scan(x, OpAdd{}, 0);
+    if ((t & 63) == 63) wsum[w] = incl;
+    __syncthreads();
+    int before = 0, all = 0;
+    for (int i = 0; i < NW; ++i) {
+        const int s = wsum[i];
+        if (i < w) before += s;
+        all += s;
+    }
+    total = all;
+    __syncthreads();
+    return before + incl;
+}
+
+__global__ __launch_bounds__(kBfsThreads) void k_bfs_levels(
+    int* __restrict__ front, const long long* __restrict__ head, const int* __restrict__ adj,
+    int* __restrict__ lev, int* __restrict__ seq, int* claim, int N, int4* __restrict__ state) {
+    constexpr int NW = kBfsThreads / 64;
+    __shared__ int s_front[kBfsThreads];
+    __shared__ int s_ofs[kBfsThreads + 1];  // edge offset of each frontier vertex
+    __shared__ int s_ex[kBfsThreads + 1];   // children before each edge
+    __shared__ u64 s_packed[kBfsThreads];   // degree << 32 | id of the next level
+    __shared__ int s_wsum[NW];
+    const int t = threadIdx.x;
+    const int4 s0 = *state;
+    int f = s0.x, base = s0.y, level = s0.z;
+    bool finished = false, moved = false;
+    if (t < f) s_front[t] = front[t];
+    for (;;) {
+        __syncthreads();
+        if (f == 0 || base >= N) {
+            finished = true;
+            break;
+        }
+        int deg = 0;
+        if (t < f) {
+            const int v = s_front[t];
+            deg = (int)min(head[v + 1] - head[v], (long long)kBfsThreads + 1);
+        }
+        int Ef;
+        const int ofs = block_scan_int<NW>(deg, s_wsum, Ef) - deg;
+        if (Ef == 0) {
+            finished = true;
+            break;
+        }
+        if (Ef > kBfsThreads) break;
+        if (t < f) s_ofs[t] = ofs;
+        if (t == 0) s_ofs[f] = Ef;
+        __syncthreads();
+        int u = -1, lo = 0;
+        if (t < Ef) {
+            int hi = f;  // largest lo with s_ofs[lo] <= t
+            while (hi - lo > 1) {
+                const int mid = (lo + hi) >> 1;
+                if (s_ofs[mid] <= t) lo = mid;
+                else hi = mid;
+            }
+            const int v = s_front[lo];
+            u = adj[head[v] + (t - s_ofs[lo])];
+            if (lev[u] < 0) atomicMin(&claim[u], lo);
+            else u = -1;
+        }
+        __syncthreads();
+        const int child =
+            u >= 0 && __hip_atomic_load(claim + u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == lo;
+        int n;
+        const int pos = block_scan_int<NW>(child, s_wsum, n) - child;
+        s_ex[t] = pos;
+        if (t == 0) s_ex[kBfsThreads] = n;
+        if (child) s_packed[pos] = (u64)(head[u + 1] - head[u]) << 32 | (u64)(uint32_t)u;
+        __syncthreads();
+        if (t < f) {
+            const int b = s_ex[s_ofs[t]], e = s_ex[s_ofs[t + 1]];
+            if (e - b > 1) ls_sort_range(s_packed, b, e, 2 * lg_floor(e - b));
+        }
+        __syncthreads();
+        if (t < n) {
+            const int w = (int)(uint32_t)s_packed[t];
+            s_front[t] = w;
+            lev[w] = level;
+            seq[w] = base + t;
+        }
+        base += n;
+        f = n;
+        ++level;
+        moved = true;
+    }
+    if (moved && t < f) front[t] = s_front[t];
+    if (t == 0) *state = make_int4(f, base, level, finished ? 1 : 0);
+}
+
 // ---- 5. order ----------------------------------------------------------------------------
-__global__ void k_order_keys(const int* __restrict__ parent, const int* __restrict__ rank,
+__global__ void k_order_keys(const int* __restrict__ comp, const int* __restrict__ rank,
                              const int* __restrict__ seq, int N, int nb, u64* __restrict__ key,
                              uint32_t* __restrict__ val) {
     const long long v = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     if (v >= N) return;
-    key[v] = (u64)rank[parent[v]] << nb | (u64)seq[v];
+    key[v] = (u64)rank[comp[v]] << nb | (u64)seq[v];
     val[v] = (uint32_t)v;
 }
 
@@ -688,10 +794,13 @@ void rcm_order_device(const int* rp, const int* col, int M, int N, int nnz, int*
     }
 
     // 3. components
-    DevBuf<int> parent(N);
-    RLAUNCH(k_uf_init, N, parent.p, N);
-    RLAUNCH(k_uf_hook, E, adj_u.p, adj.p, E, rank.p, parent.p);
-    RLAUNCH(k_uf_flatten, N, parent.p, N);
+    DevBuf<int> comp(N);
+    {
+        DevBuf<int> parent(N);
+        RLAUNCH(k_uf_init, N, parent.p, N);
+        RLAUNCH(k_uf_hook, E, adj_u.p, adj.p, E, rank.p, parent.p);
+        RLAUNCH(k_uf_components, N, parent.p, N, comp.p);
+    }
     adj_u.release();
 
     // 4. levels
@@ -702,7 +811,7 @@ void rcm_order_device(const int* rp, const int* col, int M, int N, int nnz, int*
     {
         DevBuf<int> flag(N);
         DevBuf<long long> pos((size_t)N + 1);
-        RLAUNCH(k_root_flags, N, order.p, parent.p, N, flag.p);
+        RLAUNCH(k_root_flags, N, order.p, comp.p, N, flag.p);
         exclusive_sum<int, long long>(flag.p, pos.p, N, st);
         f = (int)read_scalar(pos.p + N, st);
         RLAUNCH(k_root_list, N, order.p, flag.p, pos.p, N, front.p, lev.p, seq.p);
@@ -713,8 +822,22 @@ void rcm_order_device(const int* rp, const int* col, int M, int N, int nnz, int*
     DevBuf<int> gflag(N), gstart(N);
     DevBuf<long long> gpos((size_t)N + 1);
     SortJobs jobs(N);
-    int base = f;
-    for (int level = 1; f > 0 && base < N; ++level) {
+    DevBuf<int4> bfs_state(1);
+    int base = f, level = 1;
+    while (f > 0 && base < N) {
+        if (f <= kBfsThreads) {  // run levels inside one work-group while they are small
+            const int4 s0 = make_int4(f, base, level, 0);
+            VCSRMC_HIP(hipMemcpyAsync(bfs_state.p, &s0, sizeof(s0), hipMemcpyHostToDevice, st));
+            hipLaunchKernelGGL(k_bfs_levels, dim3(1), dim3(kBfsThreads), 0, st, front.p, head.p,
+                               adj.p, lev.p, seq.p, claim.p, N, bfs_state.p);
+            VCSRMC_HIP(hipGetLastError());
+            const int4 s1 = read_scalar(bfs_state.p, st);
+            f = s1.x;
+            base = s1.y;
+            level = s1.z;
+            if (s1.w || f == 0 || base >= N) break;
+        }
+        // a level whose frontier or edge count exceeds one work-group
         RLAUNCH(k_front_degree, f, front.p, f, head.p, fdeg.p);
         exclusive_sum<long long, long long>(fdeg.p, fofs.p, f, st);
         const long long Ef = read_scalar(fofs.p + f, st);
@@ -738,12 +861,13 @@ void rcm_order_device(const int* rp, const int* col, int M, int N, int nnz, int*
         RLAUNCH(k_level_write, n, packed, n, level, base, front.p, lev.p, seq.p);
         base += n;
         f = n;
+        ++level;
     }
     if (base != N) throw Error(VCSRMC_ERR_STATE, "rcm ordering left vertices unvisited");
 
     // 5. order
     {
-        RLAUNCH(k_order_keys, N, parent.p, rank.p, seq.p, N, nb, k1.p, v1.p);
+        RLAUNCH(k_order_keys, N, comp.p, rank.p, seq.p, N, nb, k1.p, v1.p);
         u64 *ka = k1.p, *kb = k2.p;
         uint32_t *va = v1.p, *vb = v2.p;
         radix_sort_pairs<u64>(ka, va, kb, vb, N, 2 * nb, st);
