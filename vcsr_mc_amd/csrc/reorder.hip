@@ -525,16 +525,19 @@ __global__ void k_level_write(const u64* __restrict__ packed, int n, int level, 
 }
 
 // ---- 4b. small levels in one work-group ---------------------------------------------------
-// While a level has at most kBfsThreads frontier vertices and frontier edges, one work-group
-// runs level after level with no host round trip: one thread per frontier edge claims (atomic
+// While a level has at most kBfsCap frontier vertices and frontier edges, one work-group runs
+// level after level with no host round trip: each frontier edge claims its neighbour (atomic
 // minimum of the frontier index, as k_claim), then an edge holds a child when its frontier
 // vertex won the claim.  Frontier vertices are in level order and each adjacency list is in
 // ascending id, so an exclusive scan over the edges places the children in (parent index,
 // ascending id) order directly; each parent's children are then sorted by degree with
-// std::sort's steps, one thread per parent, in LDS.  The work-group stops at the first level
-// that does not fit (state.w = 0: the frontier is left in front[]) or when the walk ends
-// (state.w = 1).  state = {frontier size, vertices placed, level, finished}.
+// std::sort's steps, one thread per parent, in LDS.  Thread t owns a contiguous run of up to
+// kBfsPer vertices or edges, so each phase needs one block scan.  The work-group stops at the
+// first level that does not fit (state.w = 0: the frontier is left in front[]) or when the walk
+// ends (state.w = 1).  state = {frontier size, vertices placed, level, finished}.
 constexpr int kBfsThreads = 1024;
+constexpr int kBfsPer = 8;
+constexpr int kBfsCap = kBfsThreads * kBfsPer;
 
 template <int NW>
 __device__ __forceinline__ int block_scan_int(int x, int* wsum /* LDS[NW] */, int& total) {
@@ -557,76 +560,120 @@ __global__ __launch_bounds__(kBfsThreads) void k_bfs_levels(
     int* __restrict__ front, const long long* __restrict__ head, const int* __restrict__ adj,
     int* __restrict__ lev, int* __restrict__ seq, int* claim, int N, int4* __restrict__ state) {
     constexpr int NW = kBfsThreads / 64;
-    __shared__ int s_front[kBfsThreads];
-    __shared__ int s_ofs[kBfsThreads + 1];  // edge offset of each frontier vertex
-    __shared__ int s_ex[kBfsThreads + 1];   // children before each edge
-    __shared__ u64 s_packed[kBfsThreads];   // degree << 32 | id of the next level
+    __shared__ int s_ofs[kBfsCap + 1];    // edge offset of each frontier vertex
+    __shared__ int s_fx[kBfsCap + 1];     // the frontier; then children before each edge
+    __shared__ u64 s_packed[kBfsCap];     // degree << 32 | id of the next level
     __shared__ int s_wsum[NW];
+    int* const s_front = s_fx;
+    int* const s_ex = s_fx;
     const int t = threadIdx.x;
     const int4 s0 = *state;
     int f = s0.x, base = s0.y, level = s0.z;
     bool finished = false, moved = false;
-    if (t < f) s_front[t] = front[t];
+    for (int i = t; i < f; i += kBfsThreads) s_front[i] = front[i];
     for (;;) {
         __syncthreads();
         if (f == 0 || base >= N) {
             finished = true;
             break;
         }
-        int deg = 0;
-        if (t < f) {
-            const int v = s_front[t];
-            deg = (int)min(head[v + 1] - head[v], (long long)kBfsThreads + 1);
+        // edge offsets of the frontier vertices [v0, v1) of this thread
+        const int pf = (f + kBfsThreads - 1) / kBfsThreads;
+        const int v0 = min(t * pf, f), v1 = min(v0 + pf, f);
+        int deg[kBfsPer];
+        int dsum = 0;
+#pragma unroll
+        for (int i = 0; i < kBfsPer; ++i) {
+            deg[i] = 0;
+            if (v0 + i < v1) {
+                const int v = s_front[v0 + i];
+                deg[i] = (int)min(head[v + 1] - head[v], (long long)kBfsCap + 1);
+                dsum += deg[i];
+            }
         }
         int Ef;
-        const int ofs = block_scan_int<NW>(deg, s_wsum, Ef) - deg;
+        int ofs = block_scan_int<NW>(dsum, s_wsum, Ef) - dsum;
         if (Ef == 0) {
             finished = true;
             break;
         }
-        if (Ef > kBfsThreads) break;
-        if (t < f) s_ofs[t] = ofs;
+        if (Ef > kBfsCap) break;
+#pragma unroll
+        for (int i = 0; i < kBfsPer; ++i)
+            if (v0 + i < v1) {
+                s_ofs[v0 + i] = ofs;
+                ofs += deg[i];
+            }
         if (t == 0) s_ofs[f] = Ef;
         __syncthreads();
-        int u = -1, lo = 0;
-        if (t < Ef) {
-            int hi = f;  // largest lo with s_ofs[lo] <= t
+        // claims of the edges [e0, e1) of this thread
+        const int pe = (Ef + kBfsThreads - 1) / kBfsThreads;
+        const int e0 = min(t * pe, Ef), e1 = min(e0 + pe, Ef);
+        int us[kBfsPer], los[kBfsPer];
+        {
+            int lo = 0, hi = f;  // largest lo with s_ofs[lo] <= e0
             while (hi - lo > 1) {
                 const int mid = (lo + hi) >> 1;
-                if (s_ofs[mid] <= t) lo = mid;
+                if (s_ofs[mid] <= e0) lo = mid;
                 else hi = mid;
             }
-            const int v = s_front[lo];
-            u = adj[head[v] + (t - s_ofs[lo])];
-            if (lev[u] < 0) atomicMin(&claim[u], lo);
-            else u = -1;
+#pragma unroll
+            for (int i = 0; i < kBfsPer; ++i) {
+                us[i] = -1;
+                los[i] = 0;
+                const int e = e0 + i;
+                if (e < e1) {
+                    while (s_ofs[lo + 1] <= e) ++lo;
+                    const int v = s_front[lo];
+                    const int u = adj[head[v] + (e - s_ofs[lo])];
+                    if (lev[u] < 0) {
+                        atomicMin(&claim[u], lo);
+                        us[i] = u;
+                        los[i] = lo;
+                    }
+                }
+            }
         }
         __syncthreads();
-        const int child =
-            u >= 0 && __hip_atomic_load(claim + u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == lo;
+        int child = 0, nchild = 0;
+#pragma unroll
+        for (int i = 0; i < kBfsPer; ++i) {
+            const bool c = us[i] >= 0 && __hip_atomic_load(claim + us[i], __ATOMIC_RELAXED,
+                                                           __HIP_MEMORY_SCOPE_AGENT) == los[i];
+            child |= (int)c << i;
+            nchild += c;
+        }
         int n;
-        const int pos = block_scan_int<NW>(child, s_wsum, n) - child;
-        s_ex[t] = pos;
-        if (t == 0) s_ex[kBfsThreads] = n;
-        if (child) s_packed[pos] = (u64)(head[u + 1] - head[u]) << 32 | (u64)(uint32_t)u;
+        int pos = block_scan_int<NW>(nchild, s_wsum, n) - nchild;
+#pragma unroll
+        for (int i = 0; i < kBfsPer; ++i)
+            if (e0 + i < e1) {
+                s_ex[e0 + i] = pos;
+                if ((child >> i) & 1) {
+                    const int u = us[i];
+                    s_packed[pos++] = (u64)(head[u + 1] - head[u]) << 32 | (u64)(uint32_t)u;
+                }
+            }
+        if (t == 0) s_ex[Ef] = n;
         __syncthreads();
-        if (t < f) {
-            const int b = s_ex[s_ofs[t]], e = s_ex[s_ofs[t + 1]];
+        for (int lo = v0; lo < v1; ++lo) {
+            const int b = s_ex[s_ofs[lo]], e = s_ex[s_ofs[lo + 1]];
             if (e - b > 1) ls_sort_range(s_packed, b, e, 2 * lg_floor(e - b));
         }
         __syncthreads();
-        if (t < n) {
-            const int w = (int)(uint32_t)s_packed[t];
-            s_front[t] = w;
+        for (int i = t; i < n; i += kBfsThreads) {
+            const int w = (int)(uint32_t)s_packed[i];
+            s_front[i] = w;
             lev[w] = level;
-            seq[w] = base + t;
+            seq[w] = base + i;
         }
         base += n;
         f = n;
         ++level;
         moved = true;
     }
-    if (moved && t < f) front[t] = s_front[t];
+    if (moved)
+        for (int i = t; i < f; i += kBfsThreads) front[i] = s_front[i];
     if (t == 0) *state = make_int4(f, base, level, finished ? 1 : 0);
 }
 
@@ -825,7 +872,7 @@ void rcm_order_device(const int* rp, const int* col, int M, int N, int nnz, int*
     DevBuf<int4> bfs_state(1);
     int base = f, level = 1;
     while (f > 0 && base < N) {
-        if (f <= kBfsThreads) {  // run levels inside one work-group while they are small
+        if (f <= kBfsCap) {  // run levels inside one work-group while they are small
             const int4 s0 = make_int4(f, base, level, 0);
             VCSRMC_HIP(hipMemcpyAsync(bfs_state.p, &s0, sizeof(s0), hipMemcpyHostToDevice, st));
             hipLaunchKernelGGL(k_bfs_levels, dim3(1), dim3(kBfsThreads), 0, st, front.p, head.p,
