@@ -22,6 +22,7 @@ constexpr int kWaves = 4;
 // Light-unit ranges per XCD, passed to the multiply kernels by value.
 struct XcdSplit {
     int start[9];
+    int lgp;  // log2 of the row parts per O group: the O tiles are dealt to 8 >> lgp XCD groups
 };
 
 // A format on one device.

@@ -254,25 +254,30 @@ __device__ __forceinline__ uint4 load_a16(const TileMeta& m, int lane, int a_off
     return uint4{*p0, *p1, *p2, *p3};
 }
 
-// Schedule of a 4-wave work-group.  Work-groups [0, H8) run the heavy units (H8 = num_heavy
-// rounded up to a multiple of 8): the four waves share one unit's tiles.  The others run light
-// units, one per wave.  Work-groups are dealt to the 8 XCDs round robin, so light work-group j
-// runs on XCD j mod 8 and takes the next four units of that XCD's range: each XCD walks
-// neighbouring panels (shared B rows stay in its L2) and the ranges hold equal tile counts.
-// Returns false if this wave has nothing to do.
+// Schedule of a 4-wave work-group.  Work-groups are dealt to the 8 XCDs round robin (the grid's
+// x extent is a multiple of 8, so work-group b runs on XCD b mod 8).  The O tiles of one launch
+// row (blockIdx.y) go to G = 8 >> lgp groups of P = 1 << lgp XCDs: XCD x computes O tile x / P
+// for row part x mod P, so each XCD's L2 holds only its slice of the B rows, and each B row
+// slice is fetched by at most P XCDs.  Heavy work-groups come first (8 per P heavy units): the
+// four waves share one unit's tiles.  The others run light units, one per wave; light
+// work-group j takes the next four units of its row part, a range of units in panel order
+// (neighbouring panels share B rows) cut for equal tile counts.  Sets `ot`, the O tile within
+// the launch row.  Returns false if this wave has nothing to do.
 __device__ __forceinline__ bool schedule(int num_heavy, const XcdSplit& xs, int wave, int& u,
-                                         bool& heavy) {
-    const int h8 = (num_heavy + 7) & ~7;
-    const int b = blockIdx.x;
-    if (b < h8) {
+                                         bool& heavy, int& ot) {
+    const int lgp = xs.lgp, parts = 1 << lgp;
+    const int hwg = ((num_heavy + parts - 1) >> lgp) << 3;
+    const int b = blockIdx.x, x = b & 7, r = x & (parts - 1);
+    ot = x >> lgp;
+    if (b < hwg) {
         heavy = true;
-        u = b;
-        return b < num_heavy;
+        u = ((b >> 3) << lgp) + r;
+        return u < num_heavy;
     }
     heavy = false;
-    const int j = b - h8, x = j & 7;
-    u = num_heavy + xs.start[x] + (j >> 3) * kWaves + wave;
-    return u < num_heavy + xs.start[x + 1];
+    const int j = b - hwg, G = 8 >> lgp;
+    u = num_heavy + xs.start[r * G] + (j >> 3) * kWaves + wave;
+    return u < num_heavy + xs.start[(r + 1) * G];
 }
 
 // One FP16 tile: A operand (dense words, or the entries scattered into the wave's LDS tile),
@@ -389,11 +394,11 @@ __global__ __launch_bounds__(64 * kWaves, (f16_min_waves<TB, ALIGNED>())) void k
     // and tile indices in scalar registers and fetch tile metadata with scalar loads.
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
-    int u;
+    int u, ot;
     bool heavy;
-    if (!schedule(num_heavy, xs, wave, u, heavy)) return;
+    if (!schedule(num_heavy, xs, wave, u, heavy, ot)) return;
     const int4 U = units[u];
-    const int k0 = blockIdx.y * TK;
+    const int k0 = ((blockIdx.y << (3 - xs.lgp)) + ot) * TK;
     const int c0 = k0 + VEC * n;
     floatx4 acc[VEC];
 #pragma unroll
@@ -626,11 +631,11 @@ __global__ __launch_bounds__(64 * kWaves, 3) void k_spmm_f32(
     __shared__ __attribute__((aligned(16))) float P[kWaves * 16 * TK];
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
-    int u;
+    int u, ot;
     bool heavy;
-    if (!schedule(num_heavy, xs, wave, u, heavy)) return;
+    if (!schedule(num_heavy, xs, wave, u, heavy, ot)) return;
     const int4 U = units[u];
-    const int k0 = blockIdx.y * TK;
+    const int k0 = ((blockIdx.y << (3 - xs.lgp)) + ot) * TK;
     const int c0 = k0 + VEC * n;
     floatx4 acc[VEC];
 #pragma unroll
@@ -657,13 +662,20 @@ static void launch_tk(const DeviceFormat& F, const void* dB, bool b_f16, int O, 
     // Vector loads of B need O % VEC == 0 and a 16-byte aligned base.
     const bool aligned = (O % VEC) == 0 && ((uintptr_t)dB % 16) == 0;
     const bool c4 = (O % 4) == 0 && ((uintptr_t)dC % 16) == 0;
-    const int h8 = (F.num_heavy + 7) & ~7;
+    // O tiles: G = the largest power of two <= 8 dividing their count go to separate XCD
+    // groups; the rest are launch rows (blockIdx.y).
+    const int otiles = (O + TK - 1) / TK;
+    int G = 8;
+    while (otiles % G) G >>= 1;
     XcdSplit xs;
-    int per_xcd = 0;  // light work-groups per XCD
+    xs.lgp = G == 8 ? 0 : G == 4 ? 1 : G == 2 ? 2 : 3;
+    const int parts = 1 << xs.lgp;
     for (int x = 0; x < 9; ++x) xs.start[x] = F.xcd_start[x];
-    for (int x = 0; x < 8; ++x)
-        per_xcd = std::max(per_xcd, (xs.start[x + 1] - xs.start[x] + kWaves - 1) / kWaves);
-    const dim3 grid((unsigned)(h8 + 8 * per_xcd), (unsigned)((O + TK - 1) / TK));
+    int per_xcd = 0;  // light work-groups per XCD
+    for (int r = 0; r < parts; ++r)
+        per_xcd = std::max(per_xcd, (xs.start[(r + 1) * G] - xs.start[r * G] + kWaves - 1) / kWaves);
+    const int hwg = 8 * ((F.num_heavy + parts - 1) / parts);
+    const dim3 grid((unsigned)(hwg + 8 * per_xcd), (unsigned)(otiles / G));
     const dim3 block(64 * kWaves);
     const int NH = F.num_heavy;
     if (F.fp32) {
