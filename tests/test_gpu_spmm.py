@@ -149,10 +149,10 @@ def test_empty_matrix():
 
 @pytest.mark.parametrize("config", [1, 2, 3, 4, 5])
 def test_workloads_row_sample(orc, config):
-    """Full-size workloads (config 2 at its benchmark size, the larger ones scaled to fit a test),
-    checked on a seeded sample of rows against the oracle."""
+    """The five workloads at their full benchmark sizes, checked on a seeded sample of 3000 rows
+    against the oracle."""
     import torch
-    size = {1: 0, 2: 0, 3: 40, 4: 1024, 5: 16}[config]
+    size = 0
     w = vm.WORKLOADS[config]
     fp32 = w["precision"] == "fp32"
     A = vm.generate(config, size)
@@ -172,6 +172,39 @@ def test_workloads_row_sample(orc, config):
     R, L1 = orc.spmm_csr(srp, sc, sv, len(rows), B, mode=0 if fp32 else 1, scale=scale)
     ok, worst, row = row_l1_parity(Cn[rows], R, L1, TAU[fp32])
     assert ok, f"row {rows[row]}: {worst:.3g}"
+
+
+@pytest.mark.parametrize("config,tileK", [(1, 128), (2, 128), (3, 128), (4, 128), (4, 64),
+                                           (2, 32)])
+def test_workloads_full_size_accumulate_twice(config, tileK):
+    """At the full benchmark sizes, a property exact at any size: with no split panel (no
+    atomics) every output is one rounding of the same deterministic sum into C, so from
+    C = -0.0 one call leaves s and a second exactly 2 s; rows without nonzeros are never
+    written, so they keep the sign of -0.0."""
+    import torch
+    w = vm.WORKLOADS[config]
+    fp32 = w["precision"] == "fp32"
+    A = vm.generate(config, 0)
+    O = w["O"]
+    say("full-size accumulate twice", config, tileK, A.M, A.nnz, O)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(config)
+    B = torch.rand((A.N, O), generator=g, device="cuda") * 2 - 1
+    dB = B if fp32 else B.half()
+    with vm.DeviceFormat.from_device_csr(dev(A.row_ptr), dev(A.col), dev(A.val), A.M, A.N,
+                                         fp32, 32) as f:
+        info = f.info()
+        assert info["num_units"] == info["num_panels"]  # no split panel
+        C1 = torch.full((A.M, O), -0.0, dtype=torch.float32, device="cuda")
+        f.spmm(dB, C1, tileK=tileK)
+        C2 = C1.clone()
+        f.spmm(dB, C2, tileK=tileK)
+        torch.cuda.synchronize()
+    assert torch.equal(C2, 2 * C1)
+    empty = torch.from_numpy(np.diff(A.row_ptr) == 0).cuda()
+    assert bool(torch.all(torch.signbit(C2[empty])) and torch.all(C2[empty] == 0))
+    assert bool(torch.isfinite(C1).all())
+    assert int((C1[~empty] != 0).any(dim=1).sum()) == int((~empty).sum())
 
 
 @pytest.mark.parametrize("fp32,b32", [(False, False), (True, True), (False, True)])
