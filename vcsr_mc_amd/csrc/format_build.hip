@@ -459,10 +459,11 @@ static void check_err(const int* d_err, hipStream_t st) {
 // Panels of at most this many tiles are light units (one wave each, four per work-group);
 // larger panels become heavy units that the four waves of a work-group share and merge in LDS.
 // With fewer than 2048 panels one wave per panel leaves most of the 1024 SIMDs idle, so every
-// multi-tile panel is shared by a work-group; otherwise panels of up to 8 tiles stay on one
-// wave (measured on gfx950: 6 to 12 tiles are equally good for stencil and R-MAT matrices;
-// 4 starves the stencil of waves, 16 leaves R-MAT with long single-wave units).
-static int light_tile_limit(int num_panels) { return num_panels >= 2048 ? 8 : 1; }
+// multi-tile panel is shared by a work-group; otherwise panels of up to 6 tiles stay on one
+// wave (measured on gfx950: 6 to 12 tiles are equally good for stencil and R-MAT matrices, 6 is
+// 2% faster than 7 or 8 on the power-law matrix; 4 starves the stencil of waves and slows the
+// power-law one by 6%, 16 leaves R-MAT with long single-wave units).
+static int light_tile_limit(int num_panels) { return num_panels >= 2048 ? 6 : 1; }
 
 template <typename K>
 static void build_exec_layout_k(DeviceFormat& F, const int* trow, const int* tcol,
