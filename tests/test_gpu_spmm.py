@@ -1,7 +1,8 @@
 """GPU SpMM vs the oracle.  Parity gate: per row r,
     ||C_gpu[r,:] - C_ref[r,:]||_1 <= tau * sum_k sum_p |a_rp b_{c_p,k}|,
 tau = 1e-5 for FP32 inputs and 2e-3 for FP16 inputs, with C_ref the oracle's double-precision
-product of the same (FP16-quantised, for vcsr_mc) operands."""
+product of the same (FP16-quantised, for vcsr_mc) operands.  Where C starts non-zero the norm
+also counts what is already in the row, + ||C0[r,:]||_1 (C += A.B rounds the final sum)."""
 import numpy as np
 import pytest
 
@@ -145,6 +146,78 @@ def test_empty_matrix():
     f.spmm(B, C)
     assert torch.all(C == 3.0)
     f.close()
+
+
+def band_csr(rng, M, N, bw, mag):
+    rows = [np.arange(max(0, min(r, N - 1) - bw), min(N, min(r, N - 1) + bw + 1)) for r in range(M)]
+    rp = np.zeros(M + 1, np.int32)
+    rp[1:] = np.cumsum([len(x) for x in rows])
+    c = np.concatenate(rows).astype(np.int32)
+    return rp, c, (rng.uniform(-1, 1, c.size) * mag).astype(np.float32)
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_random_sweep(orc, seed):
+    """Random shapes, patterns (uniform, Poisson rows with heavy rows, bands), value ranges,
+    segw, tileK, O, FP16 / FP32 format and B, B and C base pointers off 16-byte alignment, and
+    C0 = 0 or random: format arrays bit-exact and C = C0 + A.B within the parity norm.  With
+    C0 != 0 the norm is that of everything summed into the row, sum |a||b| + ||C0[r]||_1: the
+    final C0 + s rounds like any other addition (the reference's atomicAdd into C too), which a
+    bound on sum |a||b| alone cannot cover when A's values are tiny."""
+    import torch
+    Os = [1, 3, 4, 7, 8, 16, 31, 33, 64, 65, 100, 127, 128, 129, 200, 256, 257]
+    for t in range(12):
+        rng = np.random.default_rng(7000 + 100 * seed + t)
+        M, N = int(rng.integers(1, 2500)), int(rng.integers(1, 2500))
+        kind = int(rng.integers(0, 3))
+        mag = float(rng.choice([1.0, 1e5, 3e-5]))
+        if kind == 0:
+            rp, c, v = random_csr(rng, M, N, density=float(rng.choice([0.0005, 0.003, 0.03])),
+                                  mag=mag, empty_frac=float(rng.uniform(0, 0.4)))
+        elif kind == 1:
+            rp, c, v = random_csr(rng, M, N, nnz_per_row=float(rng.uniform(0.5, 20)), mag=mag,
+                                  heavy_rows=int(rng.integers(0, 5)),
+                                  heavy_nnz=int(rng.integers(1, N + 1)))
+        else:
+            rp, c, v = band_csr(rng, M, N, int(rng.integers(0, 40)), mag)
+        segw = int(rng.choice([16, 32, 48, 64]))
+        fp32 = bool(rng.integers(0, 2))
+        tileK = int(rng.choice([16, 32, 64, 128]))
+        O = int(rng.choice(Os))
+        b16 = (not fp32) and bool(rng.integers(0, 2))
+        offB, offC = int(rng.random() < 0.3), int(rng.random() < 0.3)
+        with_c0 = bool(rng.integers(0, 2))
+        say("sweep", seed, t, M, N, c.size, kind, mag, segw, fp32, tileK, O, b16, offB, offC,
+            with_c0)
+        B = rng.uniform(-1, 1, (N, O)).astype(np.float32)
+        if not fp32:
+            B = B.astype(np.float16).astype(np.float32)
+        C0 = rng.uniform(-1, 1, (M, O)).astype(np.float32) if with_c0 else \
+            np.zeros((M, O), np.float32)
+        with vm.DeviceFormat.from_device_csr(dev(rp), dev(c), dev(v), M, N, fp32, segw) as f:
+            scale = f.info()["scale"]
+            V = f.download()
+            got = {k: getattr(V, k) for k in ("M", "N", "segw", "bundle", "num_segments",
+                                               "fp32", *vm._FMT_ARRAYS)}
+            got["scale"] = np.float32(V.scale)
+            assert orc.formats_equal(orc.Format(got),
+                                     orc.build_format(rp, c, v, M, N, segw, fp32)) == [], t
+            bt = torch.float16 if b16 else torch.float32
+            dB = torch.empty(N * O + 8, dtype=bt, device="cuda")[offB:offB + N * O].view(N, O)
+            dB.copy_(torch.from_numpy(B).to(bt))
+            dC = torch.empty(M * O + 8, dtype=torch.float32, device="cuda")[offC:offC + M * O]
+            dC = dC.view(M, O)
+            dC.copy_(torch.from_numpy(C0))
+            f.spmm(dB, dC, tileK=tileK)
+            torch.cuda.synchronize()
+            Cg = dC.cpu().numpy()
+        R, L1 = orc.spmm_csr(rp, c, v, M, B, mode=0 if fp32 else 1, scale=scale)
+        R = R + C0.astype(np.float64)
+        L1 = L1 + np.abs(C0.astype(np.float64)).sum(axis=1)
+        ok, worst, row = row_l1_parity(Cg, R, L1, TAU[fp32])
+        assert ok, f"case {t}: row {row}: {worst:.3g}"
+        empty = np.diff(rp) == 0
+        assert Cg[empty].tobytes() == C0[empty].tobytes(), t
 
 
 @pytest.mark.parametrize("config", [1, 2, 3, 4, 5])
