@@ -77,3 +77,17 @@ def grid5(nx, ny):
     rp = np.zeros(len(rows) + 1, np.int32)
     rp[1:] = np.cumsum([len(r) for r in rows])
     return rp, np.concatenate(rows).astype(np.int32)
+
+
+def csr_from_edges(M, N, edges):
+    """CSR pattern (values 1) of the (row, column) pairs that fall inside M x N, duplicates
+    merged."""
+    rows = [[] for _ in range(M)]
+    for r, c in edges:
+        if 0 <= r < M and 0 <= c < N:
+            rows[r].append(c)
+    rows = [np.unique(np.asarray(x, np.int64)) for x in rows]
+    rp = np.zeros(M + 1, np.int32)
+    rp[1:] = np.cumsum([len(x) for x in rows])
+    col = np.concatenate(rows).astype(np.int32) if rp[-1] else np.zeros(0, np.int32)
+    return rp, col

@@ -9,7 +9,7 @@ import pytest
 import vcsr_mc_amd as vm
 from conftest import random_csr
 from gpu_util import dev, say, row_l1_parity
-from golden_io import banded, grid5
+from golden_io import banded, csr_from_edges, grid5
 
 pytestmark = pytest.mark.gpu
 
@@ -103,6 +103,53 @@ def test_rcm_banded_and_grid_gpu(orc, shape):
     N = rp.size - 1
     say("rcm", kind, a, b, N, col.size)
     assert np.array_equal(gpu_rcm(rp, col, N, N), orc.rcm_order(rp, col, N, N))
+
+
+def test_rcm_structured_sweep_gpu(orc):
+    """Shapes the random matrices rarely make: paths glued to hubs (deep walks next to wide
+    levels, child groups beyond the work-group sort), many small components, grids with a few
+    long-range edges, and rows beyond N with isolated columns."""
+    for t in range(24):
+        rng = np.random.default_rng(900 + t)
+        kind = t % 4
+        if kind == 0:
+            N = int(rng.integers(2, 20000))
+            perm = rng.permutation(N)
+            cut = np.sort(rng.choice(np.arange(1, N), size=min(N - 1, int(rng.integers(0, 12))),
+                                     replace=False))
+            e = [(a, b) for seg in np.split(perm, cut) for a, b in zip(seg[:-1], seg[1:])]
+            for _ in range(int(rng.integers(0, 4))):
+                hub = int(rng.integers(0, N))
+                e += [(hub, int(x)) for x in rng.choice(N, size=min(N, int(rng.integers(1, 3000))),
+                                                        replace=False)]
+            e += [(b, a) for a, b in e]
+            M = N
+            rp, col = csr_from_edges(M, N, e)
+        elif kind == 1:
+            N = int(rng.integers(1, 20000))
+            e, start = [], 0
+            while start < N:
+                ids = np.arange(start, min(N, start + int(rng.integers(1, 50))))
+                start += len(ids)
+                for _ in range(2 * len(ids)):
+                    a, b = int(rng.choice(ids)), int(rng.choice(ids))
+                    e += [(a, b), (b, a)]
+            M = N
+            rp, col = csr_from_edges(M, N, e)
+        elif kind == 2:
+            rp, col = grid5(int(rng.integers(1, 250)), int(rng.integers(1, 250)))
+            M = N = rp.size - 1
+            e = [(r, int(c)) for r in range(M) for c in col[rp[r]:rp[r + 1]]]
+            e += [(int(rng.integers(0, N)), int(rng.integers(0, N)))
+                  for _ in range(int(rng.integers(1, 40)))]
+            rp, col = csr_from_edges(M, N, e)
+        else:
+            N = int(rng.integers(1, 3000))
+            M = N + int(rng.integers(0, 3000))
+            rp, col, _ = random_csr(rng, M, N, nnz_per_row=float(rng.uniform(0, 2)),
+                                    empty_frac=0.5)
+        say("rcm structured", t, kind, M, N, col.size)
+        assert np.array_equal(gpu_rcm(rp, col, M, N), orc.rcm_order(rp, col, M, N)), t
 
 
 def test_rcm_no_nonzeros_gpu():
