@@ -14,6 +14,11 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 BIN = os.path.join(ROOT, "vcsr_mc_amd", "spmm_vcsr")
 
 
+# The reference's CSV schema (src/main.cpp:220), which its analysis scripts read by name.
+CSV_HEADER = ("gpu,sm,mtx,O,segw,bundle,tileK,repeat,algo,ms,gflops,validation,rel_l2,setup_ms,"
+              "ms_mean,ms_median,convert_ms,upload_ms")
+
+
 def run(args, timeout=300):
     return subprocess.run([BIN] + args, capture_output=True, text=True, timeout=timeout)
 
@@ -69,6 +74,7 @@ def test_all_algorithms_pass_cpu_check(tmp_path):
         r = run(["--mtx", str(p), "--O", "96", "--segw", str(segw), "--tileK", str(tk),
                  "--check", "cpu", "--csv", "--bdist", "uniform", "--repeat", "3"])
         assert r.returncode == 0, r.stderr
+        assert r.stdout.splitlines()[0] == CSV_HEADER
         rows = list(csv.DictReader(io.StringIO(r.stdout)))
         assert {x["algo"] for x in rows} == {"rocsparse", "rocsparse_fp16", "vcsr_mc",
                                              "vcsr_mc_fp32"}

@@ -68,6 +68,17 @@ def rows_of(path):
         return list(csv.DictReader(fh))
 
 
+# The reference sweep's results columns (bench200/run200.py:22-24), read by name by its
+# rerun and table scripts.
+RESULT_FIELDS = ["gpu", "sm", "mtx", "O", "segw", "bundle", "tileK", "repeat", "algo", "ms",
+                 "gflops", "validation", "rel_l2", "setup_ms", "nnz", "rep", "ms_mean",
+                 "ms_median", "convert_ms", "upload_ms"]
+
+
+def test_result_columns_match_reference():
+    assert sweep.FIELDS == RESULT_FIELDS
+
+
 def test_statistics_closed_forms():
     assert sweep.median([3, 1, 2]) == 2 and sweep.median([4, 1, 3, 2]) == 2.5
     gm, gs = sweep.geo_gstd([2.0, 8.0])  # logs ln2, ln8: mean ln4, sigma ln2
