@@ -129,9 +129,14 @@ def main():
 
     graph = None
     if args.graph:
+        # captured on a side stream (capture is refused on the default one), replayed on
+        # `stream`, where the timing events are recorded
         graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph, stream=stream):
-            step()
+        cap = torch.cuda.Stream()
+        cap.wait_stream(stream)
+        with torch.cuda.graph(graph, stream=cap):
+            fmt.spmm(dB, C, tileK=args.tileK, O=O, stream=cap)
+        stream.wait_stream(cap)
         run = graph.replay
     else:
         run = step
