@@ -136,6 +136,37 @@ def test_upload_path_matches_build_path(orc, fp32):
     check(orc, rp, c, v, 500, 500, B, fp32, upload=V)
 
 
+@pytest.mark.parametrize("fp32", [False, True])
+def test_nonfinite_b_reach(fp32):
+    """An Inf in B reaches exactly the 16-row panels that use its column: row 0 uses column 3
+    (Inf row), row 1 of the same panel does not (0 * Inf = NaN there), row 17 in the next panel
+    never touches column 3 and stays finite; column 9's Inf row is used by no nonzero and
+    reaches nothing."""
+    import torch
+    M, N, O = 40, 12, 32
+    rows = {r: [5] for r in range(M)}
+    rows[0] = [3, 5]
+    rows[17] = [4, 5]
+    rp = np.zeros(M + 1, np.int32)
+    rp[1:] = np.cumsum([len(rows[r]) for r in range(M)])
+    c = np.concatenate([rows[r] for r in range(M)]).astype(np.int32)
+    v = np.full(c.size, 0.5, np.float32)
+    B = np.ones((N, O), np.float32)
+    B[3, :] = np.inf
+    B[9, :] = np.inf
+    say("non-finite B", fp32)
+    with vm.DeviceFormat.from_device_csr(dev(rp), dev(c), dev(v), M, N, fp32, 32) as f:
+        Cd = torch.zeros((M, O), dtype=torch.float32, device="cuda")
+        f.spmm(dev(B) if fp32 else dev(B).half(), Cd, tileK=32)
+        torch.cuda.synchronize()
+        C = Cd.cpu().numpy()
+    assert np.all(np.isposinf(C[0]))
+    assert np.all(np.isnan(C[1:16]))
+    expect = np.full((M - 16, O), 0.5, np.float32)
+    expect[17 - 16] = 1.0  # row 17: columns 4 and 5
+    assert np.array_equal(C[16:], expect)
+
+
 def test_empty_matrix():
     import torch
     say("empty")
