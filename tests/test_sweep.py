@@ -79,6 +79,26 @@ def test_result_columns_match_reference():
     assert sweep.FIELDS == RESULT_FIELDS
 
 
+def test_synth_corpus_files(tmp_path):
+    """The synthetic corpus at a tiny scale: 24 valid Matrix Market files whose header counts,
+    entries and corpus row agree (distinct, in range, row-major)."""
+    from vcsr_mc_amd import synth_corpus
+    path = synth_corpus.make(str(tmp_path), scale=0.002)
+    rows = rows_of(path)
+    assert len(rows) == 24 and len({r["name"] for r in rows}) == 24
+    for r in rows:
+        lines = (tmp_path / "mtx" / f"{r['name']}.mtx").read_text().splitlines()
+        assert lines[0] == "%%MatrixMarket matrix coordinate real general"
+        M, N, nnz = (int(x) for x in lines[1].split())
+        assert (M, N, nnz) == (int(r["rows"]), int(r["cols"]), int(r["nnz"])) and nnz > 0
+        e = np.array([[int(a), int(b)] for a, b, _ in (x.split() for x in lines[2:])])
+        assert len(e) == nnz
+        assert e[:, 0].min() >= 1 and e[:, 0].max() <= M and e[:, 1].min() >= 1
+        assert e[:, 1].max() <= N
+        key = (e[:, 0] - 1) * N + (e[:, 1] - 1)
+        assert np.all(np.diff(key) > 0)
+
+
 def test_statistics_closed_forms():
     assert sweep.median([3, 1, 2]) == 2 and sweep.median([4, 1, 3, 2]) == 2.5
     gm, gs = sweep.geo_gstd([2.0, 8.0])  # logs ln2, ln8: mean ln4, sigma ln2
