@@ -1,9 +1,14 @@
 // spmm_kernels.hip -- C += A.B for the VCSR-MC format on gfx950 MFMA.
 //
 // Work decomposition (atomic-free for all but split panels):
-//   one 64-lane wave = one work unit = a run of compacted tiles of one 16-row panel,
-//   for one tileK-wide slice of the output columns.  The wave keeps the 16 x tileK
-//   accumulator tile in registers across all of its tiles and writes C once.
+//   a work unit is a run of compacted tiles of one 16-row panel, for one tileK-wide slice of
+//   the output columns.  A light unit is one 64-lane wave, which keeps the 16 x tileK
+//   accumulator tile in registers across its tiles and writes C once; a heavy unit is shared by
+//   the four waves of a work-group, which take its tiles round robin and sum their partial tiles
+//   in LDS before writing C.  Panels cut into several heavy units (split) merge through atomics.
+//   Work-groups are dealt to the 8 XCDs round robin; `schedule` maps each one to its units so
+//   that an XCD walks neighbouring panels and, when there are several output slices, only its
+//   slice of B.
 //
 // Per 16 x 32 tile (32 distinct columns of the panel, any segments):
 //   * B operand: lane (n = lane % 16, g = lane / 16) loads, for the 8 tile columns
@@ -12,10 +17,11 @@
 //     256-byte B row, so every load instruction reads four whole rows.  The VEC values are
 //     then transposed in registers: MFMA q (q < VEC) takes the q-th value of each of the 8
 //     rows, i.e. output column k0 + VEC n + q.  No LDS round trip for B.
-//   * A operand: the tile's nonzeros (row, k, value) are scattered into a 16 x 32 LDS tile
-//     that each lane then reads as its 8 contiguous K values (one 128-bit LDS read).
+//   * A operand: a well-filled tile has a dense copy laid out in the order lanes read it (one
+//     load per lane); otherwise the tile's nonzeros (row, k, value) are scattered into a
+//     16 x 32 LDS tile that each lane then reads as its 8 contiguous K values.
 //   * FP16 format: v_mfma_f32_16x16x32_f16, FP32 accumulation.  FP32 format: eight K steps
-//     of v_mfma_f32_16x16x4_f32.
+//     of v_mfma_f32_16x16x4_f32, in two halves.
 //   The K order inside a tile is the same for A and B, so the contraction does not depend
 //   on how the instruction maps lanes to K.
 //
