@@ -10,14 +10,18 @@
 //      (reorder.hpp:47-50).
 //   3. components: lock-free union-find that always hooks the root of larger rank under the
 //      root of smaller rank, so each component ends up represented by its lowest-rank vertex,
-//      the root from which the reference's loop (reorder.hpp:54-57) starts that component.
+//      the root from which the reference's loop (reorder.hpp:54-57) starts that component;
+//      each vertex's root is then written to its own array.
 //   4. levels: level 0 holds every component's root in rank order.  A vertex of level L+1
 //      belongs to the earliest level-L vertex adjacent to it (the one that pops it from the
 //      reference's queue, reorder.hpp:63-66).  A level is ordered by that parent's index, then
 //      inside one parent's children as the reference orders them: ascending id, then
 //      std::sort by degree (reorder.hpp:67-69), whose steps (libstdc++ introsort) are carried
-//      out exactly, since equal degrees make the result depend on them: large groups a
-//      partition step at a time by work-groups, pieces of up to 256 elements by one thread.
+//      out exactly, since equal degrees make the result depend on them.  Levels of up to 8192
+//      frontier edges run inside one work-group, many at a time (k_bfs_levels); larger ones
+//      take several kernels: claims, a radix sort by (parent index, id), and the group sorts
+//      (large groups a partition step at a time by work-groups, pieces of up to 256 elements
+//      by one thread).
 //   5. order: vertices sorted by (component rank, level, index in level) give the
 //      Cuthill-McKee order; position = N - 1 - that index (reorder.hpp:72-76).
 #include <algorithm>
