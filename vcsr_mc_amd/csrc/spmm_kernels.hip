@@ -37,6 +37,12 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 constexpr int kApitch = 40;  // FP16 A tile row pitch in halves (80 B: conflict-free b128 reads)
+// FP32 A tile in LDS: four K groups (k & 3) of 16 rows, each row the 8 values k >> 2 a lane
+// reads with two 128-bit loads.  A row pitch of 12 floats (48 B) puts the 16 rows of a group on
+// 16 distinct 16-byte bank windows (48 n mod 256 covers every multiple of 16), where a pitch of
+// 8 made rows n and n + 8 collide.
+constexpr int kApitch32 = 12;
+constexpr int kAgroup32 = 16 * kApitch32;
 
 // Raw B values of the 8 tile rows a lane feeds into the MFMA B operand, one vector of VEC
 // consecutive output columns per row (kept in the storage type until use, so a prefetched load
@@ -518,7 +524,7 @@ __device__ __forceinline__ AState32 load_a32(const TileMeta& m, int lane, int a_
 
 __device__ __forceinline__ void scatter_a_f32(float* At, uint32_t w, float v) {
     const int r = w & 15, k = (w >> 4) & 31;
-    At[(k & 3) * 128 + r * 8 + (k >> 2)] = v;
+    At[(k & 3) * kAgroup32 + r * kApitch32 + (k >> 2)] = v;
 }
 
 // This lane's 8 A values of a tile (K steps 0..7): the dense words, or the entries scattered
@@ -569,8 +575,8 @@ __device__ __forceinline__ void tiles_f32(int first, int end, int W, int lane, i
                                           floatx4 (&acc)[TK / 16], Pre&& pre) {
     constexpr int VEC = TK / 16;
     if (first >= end) return;
-    const int a_off = g * 128 + n * 8;
-    float* my_a = &Aw[a_off];
+    const int a_off = g * 128 + n * 8;  // in a dense copy
+    float* my_a = &Aw[g * kAgroup32 + n * kApitch32];
     const int last = first + (end - 1 - first) / W * W;
     int c = first;
     FRows<VEC> X, Y;
@@ -633,7 +639,7 @@ __global__ __launch_bounds__(64 * kWaves, 3) void k_spmm_f32(
     const float* __restrict__ dense_a, const float* __restrict__ B, int O, bool c4,
     float* __restrict__ C) {
     constexpr int VEC = TK / 16;
-    __shared__ __attribute__((aligned(16))) float At[kWaves][4 * 16 * 8];
+    __shared__ __attribute__((aligned(16))) float At[kWaves][4 * kAgroup32];
     __shared__ __attribute__((aligned(16))) float P[kWaves * 16 * TK];
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
