@@ -1,7 +1,7 @@
 /*
  * vcsrmc_oracle.h -- CPU restatement of the VCSR-MC SpMM path.
  *
- * TEST INFRASTRUCTURE ONLY.  This library is the checker: only the test suite,
+ * TEST INFRASTRUCTURE ONLY.  This library checks the product: only the test suite,
  * the smoke check and the CPU-baseline leg of the benchmark may load it.  The
  * product (libvcsrmc.so) never links, loads or calls it.
  *

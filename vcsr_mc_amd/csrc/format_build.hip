@@ -6,7 +6,7 @@
 //   2. flag the first nonzero of every (segment, row) run; exclusive scan -> pair index
 //   3. pair keys (segment << 6 | segw - count); a stable radix sort orders each segment's
 //      rows by count, descending, ties by ascending row (the reference's order of equal
-//      counts is std::unordered_map iteration order, :59-66; this build fixes it)
+//      counts is std::unordered_map iteration order, :59-66; here it is fixed)
 //   4. bundles of 16 -> groups: depth, seg_base, rows; group_ptr = scan of 16*depth
 //   5. depth-major, lane-minor scatter of lcol / val * (1/scale), padded with -1 / 0
 //   6. work items: runs of <= chunk groups of one segment, stable sort by work, descending

@@ -1,7 +1,7 @@
 // spmm_vcsr.cpp -- benchmark driver with the reference's command line and CSV.
 //
 // Mirrors MuuSeoTia/VCSR_MC src/main.cpp (CLI :33-43, B fill :161-179, oracle :199-218,
-// measure :239-308, VCSR loop :345-362, CSV :220) on top of this build's libraries:
+// measure :239-308, VCSR loop :345-362, CSV :220) on top of libvcsrmc.so and libvcsrmc_bench.so:
 //   vcsr_mc / vcsr_mc_fp32     through the drop-in C++ surface (include/vcsr_formats.hpp),
 //                              with the reference's call sequence convert -> upload -> run
 //   rocsparse / rocsparse_fp16 hipSPARSE SpMM (libvcsrmc_bench.so)
