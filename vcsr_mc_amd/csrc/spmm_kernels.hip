@@ -738,6 +738,27 @@ __global__ void k_b_to_half(const float* __restrict__ B, _Float16* __restrict__ 
     }
 }
 
+// Width of the O tile a work-group covers.  tileK is the widest allowed (the results do not
+// depend on it).  Narrower, where measured faster on gfx950:
+//   * never wider than O needs (lanes past O would only multiply zeros);
+//   * 64 instead of 128 for formats whose tiles hold few nonzeros (< 48 on average), if the
+//     format is FP32 (each wave's chain of FP32 matrix-core steps halves: uniform 4096^2 8.1 ->
+//     7.0 us, power-law 36,692^2 33.0 -> 30.2, R-MAT scale 22 5.91 -> 5.70 ms) or B is larger
+//     than the 32 MB of L2 on the 8 XCDs (two O halves on separate XCD groups each fetch half of
+//     every B row, over a union of fewer row ranges: FP16 R-MAT 3.05 -> 2.86 ms).  Fuller tiles
+//     keep 128, since every O tile repeats the A side of each tile (27-point stencil 100^3 and
+//     32 x 32 blocks: 2-24% slower at 64), as do FP16 formats with a cache-resident B
+//     (power-law: 15.4 -> 17.4 us at 64).
+static int o_tile_width(const DeviceFormat& F, bool b_f16, int O, int tileK) {
+    int tk = tileK;
+    while (tk > 16 && tk / 2 >= O) tk /= 2;
+    if (tk == 128 && F.num_chunks > 0 && F.nnz < 48LL * F.num_chunks) {
+        const long long b_bytes = (long long)F.N * O * (b_f16 ? 2 : 4);
+        if (F.fp32 || b_bytes > (32LL << 20)) tk = 64;
+    }
+    return tk;
+}
+
 void spmm_launch(const DeviceFormat& F, const void* dB, bool b_f16, int O, int tileK, float* dC,
                  hipStream_t st) {
     if (tileK != 16 && tileK != 32 && tileK != 64 && tileK != 128)
@@ -760,7 +781,7 @@ void spmm_launch(const DeviceFormat& F, const void* dB, bool b_f16, int O, int t
         dB = F.b_half.p;
         b_f16 = true;
     }
-    switch (tileK) {
+    switch (o_tile_width(F, b_f16, O, tileK)) {
         case 16: launch_tk<16>(F, dB, b_f16, O, dC, st); break;
         case 32: launch_tk<32>(F, dB, b_f16, O, dC, st); break;
         case 64: launch_tk<64>(F, dB, b_f16, O, dC, st); break;
