@@ -187,6 +187,30 @@ def band_csr(rng, M, N, bw, mag):
     return rp, c, (rng.uniform(-1, 1, c.size) * mag).astype(np.float32)
 
 
+@pytest.mark.parametrize("fp32", [False, True])
+@pytest.mark.parametrize("tileK", [32, 128])
+def test_mixed_tile_fill(orc, fp32, tileK):
+    """One format holding nearly empty tiles, dense 16 x 32 blocks (dense copies) and three rows
+    of 1500 nonzeros (a full row in every tile of their panels), with C starting non-zero and O
+    past the last full O tile."""
+    rng = np.random.default_rng(40 + tileK)
+    M, N, O = 1000, 3000, 200
+    rows = [np.sort(rng.choice(N, size=int(rng.poisson(3)), replace=False)) for _ in range(M)]
+    for blk in range(0, M, 160):
+        for r in range(blk, min(M, blk + 16)):
+            rows[r] = np.union1d(rows[r], np.arange(64 + blk, 96 + blk))
+    for r in (5, 333, 999):
+        rows[r] = np.sort(rng.choice(N, size=1500, replace=False))
+    rp = np.zeros(M + 1, np.int32)
+    rp[1:] = np.cumsum([len(x) for x in rows])
+    c = np.concatenate(rows).astype(np.int32)
+    v = rng.uniform(-1, 1, c.size).astype(np.float32)
+    B = rng.uniform(-1, 1, (N, O)).astype(np.float32)
+    C0 = rng.uniform(-1, 1, (M, O)).astype(np.float32)
+    say("mixed tile fill", fp32, tileK)
+    check(orc, rp, c, v, M, N, B, fp32, tileK=tileK, C0=C0)
+
+
 @pytest.mark.parametrize("seed", range(4))
 def test_random_sweep(orc, seed):
     """Random shapes, patterns (uniform, Poisson rows with heavy rows, bands), value ranges,
