@@ -8,10 +8,10 @@
 //      (reorder.hpp:21-42).
 //   2. rank: vertices in ascending (degree, id) -- the reference's stable_sort of the roots
 //      (reorder.hpp:47-50).
-//   3. components: lock-free union-find that always hooks the root of larger rank under the
-//      root of smaller rank, so each component ends up represented by its lowest-rank vertex,
-//      the root from which the reference's loop (reorder.hpp:54-57) starts that component;
-//      each vertex's root is then written to its own array.
+//   3. components: rounds of hooking (the parent of larger rank under the parent of smaller
+//      rank, across every edge between two trees) and pointer jumping, until a round changes
+//      nothing; each component ends up represented by its lowest-rank vertex, the root from
+//      which the reference's loop (reorder.hpp:54-57) starts that component.
 //   4. levels: level 0 holds every component's root in rank order.  A vertex of level L+1
 //      belongs to the earliest level-L vertex adjacent to it (the one that pops it from the
 //      reference's queue, reorder.hpp:63-66).  A level is ordered by that parent's index, then
@@ -141,55 +141,41 @@ __global__ void k_scatter_rank(const uint32_t* __restrict__ order, int N, int* _
 }
 
 // ---- 3. components -----------------------------------------------------------------------
-// parent[] only ever points to a vertex of smaller rank (hooks) or to an ancestor (path
-// halving), so chains strictly decrease in rank and every walk ends at a root.  A root's
-// parent changes only through a successful compare-and-swap; a vertex seen as a non-root
-// never becomes a root again, so the halving store never races with a hook of the same slot.
-__device__ __forceinline__ int uf_load(const int* p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-__device__ __forceinline__ int uf_root(int* parent, int x) {
-    for (;;) {
-        const int p = uf_load(parent + x);
-        if (p == x) return x;
-        const int gp = uf_load(parent + p);
-        if (gp == p) return p;
-        __hip_atomic_store(parent + x, gp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        x = gp;
-    }
-}
-
-__global__ void k_uf_init(int* __restrict__ parent, int N) {
+// Rounds of hooking and pointer jumping over plain loads and stores.  A round hooks, for every
+// edge whose ends have different parents, the parent of larger rank under the other one if it
+// is still a root, then moves every vertex to its grandparent.  parent[] only ever points to a
+// vertex of smaller rank, so the trees stay acyclic whatever order the stores land in.  A round
+// that changes nothing leaves every tree a star (each vertex's parent is a root) and no edge
+// between two trees, so parent[v] is then the root of v's component, its lowest-rank vertex:
+// the vertex the reference's loop over roots in rank order starts the component from.
+__global__ void k_cc_init(int* __restrict__ parent, int N) {
     const long long v = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     if (v < N) parent[v] = (int)v;
 }
 
-__global__ void k_uf_hook(const int* __restrict__ adj_u, const int* __restrict__ adj, long long E,
-                          const int* __restrict__ rank, int* parent) {
+__global__ void k_cc_hook(const int* __restrict__ adj_u, const int* __restrict__ adj, long long E,
+                          const int* __restrict__ rank, int* parent, int* __restrict__ changed) {
     const long long e = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     if (e >= E) return;
-    int u = adj_u[e], w = adj[e];
+    const int u = adj_u[e], w = adj[e];
     if (u >= w) return;  // each undirected edge once; self-loops join nothing
-    for (;;) {
-        int a = uf_root(parent, u), b = uf_root(parent, w);
-        if (a == b) return;
-        if (rank[a] > rank[b]) { const int t = a; a = b; b = t; }
-        int expected = b;
-        if (__hip_atomic_compare_exchange_strong(parent + b, &expected, a, __ATOMIC_RELAXED,
-                                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
-            return;
-        u = a;
-        w = b;  // b gained a parent meanwhile: retry from the two old roots
+    int a = parent[u], b = parent[w];
+    if (a == b) return;
+    if (rank[a] > rank[b]) { const int t = a; a = b; b = t; }
+    if (parent[b] == b) {
+        parent[b] = a;
+        *changed = 1;
     }
 }
 
-// comp[v] = the root of v's tree.  No hook runs any more, so every walk ends at the true root;
-// the walks still halve paths in parent[], and a halving store may land after another thread
-// has written a shorter path there, so the roots go to their own array rather than parent[].
-__global__ void k_uf_components(int* parent, int N, int* __restrict__ comp) {
+__global__ void k_cc_jump(int* parent, int N, int* __restrict__ changed) {
     const long long v = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (v < N) comp[v] = uf_root(parent, (int)v);
+    if (v >= N) return;
+    const int p = parent[v], gp = parent[p];
+    if (gp != p) {
+        parent[v] = gp;
+        *changed = 1;
+    }
 }
 
 // ---- 4. levels ---------------------------------------------------------------------------
@@ -423,9 +409,31 @@ __global__ void k_group_jobs(const int* __restrict__ gstart, int ngroups, int n,
     else small[atomicAdd(nsmall, 1)] = job;
 }
 
-__global__ void k_small_sort(const int4* __restrict__ jobs, int njobs, u64* __restrict__ a) {
-    const long long j = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (j < njobs) ls_sort_range(a, jobs[j].x, jobs[j].y, jobs[j].z);
+// One wave per piece: the piece is copied into LDS, one lane runs the library's steps on it
+// there (a chain of a few thousand dependent accesses for 256 elements, each at LDS rather
+// than cache latency), and the wave copies it back.
+constexpr int kSmallSortWaves = 4;
+
+__device__ __forceinline__ void wave_lds_fence() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+__global__ __launch_bounds__(64 * kSmallSortWaves) void k_small_sort(
+    const int4* __restrict__ jobs, int njobs, u64* __restrict__ a) {
+    __shared__ u64 piece[kSmallSortWaves][kSortSmall];
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const long long j = (long long)blockIdx.x * kSmallSortWaves + w;
+    if (j >= njobs) return;  // the same for every lane of the wave
+    const int4 job = jobs[j];
+    const int n = job.y - job.x;  // at most kSortSmall
+    u64* s = piece[w];
+    for (int i = lane; i < n; i += 64) s[i] = a[job.x + i];
+    wave_lds_fence();
+    if (lane == 0) ls_sort_range(s, 0, n, job.z);
+    wave_lds_fence();
+    for (int i = lane; i < n; i += 64) a[job.x + i] = s[i];
 }
 
 // One step of the introsort loop on a large range, by a whole work-group, with the same result
@@ -785,7 +793,12 @@ void sort_groups(const int* gstart, int ngroups, int n, u64* packed, SortJobs& J
         std::swap(ccur, cnxt);
     }
     if (passes) nsmall = read_scalar(J.counts.p + 2, st);
-    RLAUNCH(k_small_sort, nsmall, J.small.p, nsmall, packed);
+    if (nsmall > 0) {
+        hipLaunchKernelGGL(k_small_sort, dim3((unsigned)((nsmall + kSmallSortWaves - 1) /
+                                                          kSmallSortWaves)),
+                           dim3(64 * kSmallSortWaves), 0, st, J.small.p, nsmall, packed);
+        VCSRMC_HIP(hipGetLastError());
+    }
 }
 
 }  // namespace
@@ -847,10 +860,14 @@ void rcm_order_device(const int* rp, const int* col, int M, int N, int nnz, int*
     // 3. components
     DevBuf<int> comp(N);
     {
-        DevBuf<int> parent(N);
-        RLAUNCH(k_uf_init, N, parent.p, N);
-        RLAUNCH(k_uf_hook, E, adj_u.p, adj.p, E, rank.p, parent.p);
-        RLAUNCH(k_uf_components, N, parent.p, N, comp.p);
+        DevBuf<int> changed(1);
+        RLAUNCH(k_cc_init, N, comp.p, N);
+        for (;;) {
+            fill<int>(changed.p, 1, 0, st);
+            RLAUNCH(k_cc_hook, E, adj_u.p, adj.p, E, rank.p, comp.p, changed.p);
+            RLAUNCH(k_cc_jump, N, comp.p, N, changed.p);
+            if (!read_scalar(changed.p, st)) break;
+        }
     }
     adj_u.release();
 
