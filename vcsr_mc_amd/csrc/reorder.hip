@@ -18,10 +18,11 @@
 //      inside one parent's children as the reference orders them: ascending id, then
 //      std::sort by degree (reorder.hpp:67-69), whose steps (libstdc++ introsort) are carried
 //      out exactly, since equal degrees make the result depend on them.  Levels of up to 8192
-//      frontier edges run inside one work-group, many at a time (k_bfs_levels); larger ones
-//      take several kernels: claims, a radix sort by (parent index, id), and the group sorts
-//      (large groups a partition step at a time by work-groups, pieces of up to 256 elements
-//      by one thread).
+//      frontier edges run inside one work-group, many at a time (k_bfs_levels; groups above 64
+//      elements partitioned by the work-group, pieces finished by one thread each); larger
+//      levels take several kernels: claims, a radix sort by (parent index, id), and the group
+//      sorts (large groups a partition step at a time by work-groups, pieces of up to 256
+//      elements by one wave each in LDS).
 //   5. order: vertices sorted by (component rank, level, index in level) give the
 //      Cuthill-McKee order; position = N - 1 - that index (reorder.hpp:72-76).
 #include <algorithm>
@@ -543,13 +544,20 @@ __global__ void k_level_write(const u64* __restrict__ packed, int n, int level, 
 // vertex won the claim.  Frontier vertices are in level order and each adjacency list is in
 // ascending id, so an exclusive scan over the edges places the children in (parent index,
 // ascending id) order directly; each parent's children are then sorted by degree with
-// std::sort's steps, one thread per parent, in LDS.  Thread t owns a contiguous run of up to
+// std::sort's steps in LDS: groups of up to kBfsSortSmall by their parent's thread, larger ones
+// (the children of hub vertices) partitioned by the whole work-group, a step at a time as
+// k_partition_pass does, and the pieces finished by one thread each.  Thread t owns a contiguous run of up to
 // kBfsPer vertices or edges, so each phase needs one block scan.  The work-group stops at the
 // first level that does not fit (state.w = 0: the frontier is left in front[]) or when the walk
 // ends (state.w = 1).  state = {frontier size, vertices placed, level, finished}.
 constexpr int kBfsThreads = 1024;
 constexpr int kBfsPer = 8;
 constexpr int kBfsCap = kBfsThreads * kBfsPer;
+constexpr int kBfsSortSmall = 64;
+constexpr int kBfsMaxBig = kBfsCap / (kBfsSortSmall + 1) + 1;
+// Marks of the piece starts during the work-group sort (one byte per child position): the
+// partition depth a piece continues from, or one of these.
+constexpr unsigned char kMarkNone = 255, kMarkGroupEnd = 254, kMarkHeap = 253;
 
 template <int NW>
 __device__ __forceinline__ int block_scan_int(int x, int* wsum /* LDS[NW] */, int& total) {
@@ -568,6 +576,74 @@ __device__ __forceinline__ int block_scan_int(int x, int* wsum /* LDS[NW] */, in
     return before + incl;
 }
 
+// One step of the introsort loop on a[lo, hi) (depth > 0) by the whole work-group, with the
+// library's result: k_partition_pass's computation on an LDS range.  lpos and rpos hold the
+// pair positions relative to the range (K <= (hi - lo) / 2, as the pairs are disjoint).
+// Returns the cut (the same value in every thread).
+template <int NW>
+__device__ int block_partition_lds(u64* a, int lo, int hi, int* lpos, int* rpos, int* wsum,
+                                   int* lnext) {
+    const int t = threadIdx.x;
+    if (t == 0) {
+        ls_median_to_first(a, lo, lo + 1, lo + (hi - lo) / 2, hi - 1);
+        *lnext = INT_MAX;
+    }
+    __syncthreads();
+    const uint32_t kp = skey(a[lo]);
+    const int first = lo + 1, n = hi - first;
+    const int per = (n + kBfsThreads - 1) / kBfsThreads;
+    const int b0 = min(first + t * per, hi), b1 = min(b0 + per, hi);
+    int cge = 0, cle = 0;
+    for (int p = b0; p < b1; ++p) {
+        const uint32_t k = skey(a[p]);
+        cge += !(k < kp);
+        cle += !(kp < k);
+    }
+    int GE, LE;
+    const int ge_before = block_scan_int<NW>(cge, wsum, GE) - cge;
+    const int le_before = block_scan_int<NW>(cle, wsum, LE) - cle;
+    int kc = 0;
+    {
+        int rank = ge_before, le_incl = le_before;
+        for (int p = b0; p < b1; ++p) {
+            const uint32_t k = skey(a[p]);
+            le_incl += !(kp < k);
+            if (!(k < kp)) {
+                ++rank;
+                kc += (LE - le_incl >= rank);
+            }
+        }
+    }
+    int K;
+    block_scan_int<NW>(kc, wsum, K);
+    {
+        int rank = ge_before, le_excl = le_before;
+        for (int p = b0; p < b1; ++p) {
+            const uint32_t k = skey(a[p]);
+            if (!(k < kp)) {
+                ++rank;
+                if (rank <= K) lpos[rank - 1] = p;
+                else if (rank == K + 1) *lnext = p;
+            }
+            if (!(kp < k)) {
+                const int rr = LE - le_excl;
+                if (rr <= K) rpos[rr - 1] = p;
+                ++le_excl;
+            }
+        }
+    }
+    __syncthreads();
+    for (int r = t; r < K; r += kBfsThreads) {
+        const int x = lpos[r], y = rpos[r];
+        const u64 ax = a[x], ay = a[y];
+        a[x] = ay;
+        a[y] = ax;
+    }
+    const int cut = K == 0 ? *lnext : min(*lnext, rpos[K - 1]);
+    __syncthreads();
+    return cut;
+}
+
 __global__ __launch_bounds__(kBfsThreads) void k_bfs_levels(
     int* __restrict__ front, const long long* __restrict__ head, const int* __restrict__ adj,
     int* __restrict__ lev, int* __restrict__ seq, int* claim, int N, int4* __restrict__ state) {
@@ -576,8 +652,11 @@ __global__ __launch_bounds__(kBfsThreads) void k_bfs_levels(
     __shared__ int s_fx[kBfsCap + 1];     // the frontier; then children before each edge
     __shared__ u64 s_packed[kBfsCap];     // degree << 32 | id of the next level
     __shared__ int s_wsum[NW];
+    __shared__ int2 s_big[kBfsMaxBig];  // child groups larger than kBfsSortSmall
+    __shared__ int s_nbig, s_lnext;
     int* const s_front = s_fx;
     int* const s_ex = s_fx;
+    unsigned char* const s_mark = reinterpret_cast<unsigned char*>(s_fx);  // during the sort
     const int t = threadIdx.x;
     const int4 s0 = *state;
     int f = s0.x, base = s0.y, level = s0.z;
@@ -666,11 +745,61 @@ __global__ __launch_bounds__(kBfsThreads) void k_bfs_levels(
                     s_packed[pos++] = (u64)(head[u + 1] - head[u]) << 32 | (u64)(uint32_t)u;
                 }
             }
-        if (t == 0) s_ex[Ef] = n;
+        if (t == 0) {
+            s_ex[Ef] = n;
+            s_nbig = 0;
+        }
         __syncthreads();
         for (int lo = v0; lo < v1; ++lo) {
             const int b = s_ex[s_ofs[lo]], e = s_ex[s_ofs[lo + 1]];
-            if (e - b > 1) ls_sort_range(s_packed, b, e, 2 * lg_floor(e - b));
+            if (e - b > kBfsSortSmall) s_big[atomicAdd(&s_nbig, 1)] = make_int2(b, e);
+            else if (e - b > 1) ls_sort_range(s_packed, b, e, 2 * lg_floor(e - b));
+        }
+        __syncthreads();
+        const int nbig = s_nbig;
+        if (nbig > 0) {
+            // s_ex and s_ofs are free until the next level: s_mark over s_ex, the pair
+            // positions over s_ofs.  Group ends are marked before any piece start, so a piece
+            // starting where another group ends keeps its mark.
+            for (int i = t; i <= n; i += kBfsThreads) s_mark[i] = kMarkNone;
+            __syncthreads();
+            for (int g = t; g < nbig; g += kBfsThreads) s_mark[s_big[g].y] = kMarkGroupEnd;
+            // Every thread runs the same stack of ranges (lo, hi, depth) in its own registers:
+            // its control flow depends only on values all threads share (the ranges and the
+            // cuts), and no branch taken by one thread alone decides what the others do next
+            // (with the stack in LDS and thread 0 alone updating it, the compiler moved that
+            // update out of the loop for thread 0, and the other threads never saw it).
+            for (int g = 0; g < nbig; ++g) {
+                __syncthreads();
+                const int2 gr = s_big[g];
+                int4 stk[2 * 13 + 2];  // depth 2 floor(lg n) <= 26 for n <= kBfsCap
+                int sp = 1;
+                stk[0] = make_int4(gr.x, gr.y, 2 * lg_floor(gr.y - gr.x), 0);
+                while (sp > 0) {
+                    const int4 r = stk[sp - 1];
+                    if (r.y - r.x <= kBfsSortSmall || r.z == 0) {
+                        // a piece to finish after the loop, by the thread that finds its mark
+                        s_mark[r.x] = r.y - r.x > kBfsSortSmall ? kMarkHeap : (unsigned char)r.z;
+                        --sp;
+                    } else {
+                        const int cut = block_partition_lds<NW>(
+                            s_packed, r.x, r.y, s_ofs, s_ofs + kBfsCap / 2, s_wsum, &s_lnext);
+                        stk[sp - 1] = make_int4(cut, r.y, r.z - 1, 0);
+                        stk[sp] = make_int4(r.x, cut, r.z - 1, 0);
+                        ++sp;
+                    }
+                }
+            }
+            __syncthreads();
+            for (int i = t; i < n; i += kBfsThreads) {
+                const int m = s_mark[i];
+                if (m <= kMarkHeap) {
+                    int e = i + 1;
+                    while (s_mark[e] == kMarkNone) ++e;
+                    if (m == kMarkHeap) ls_heapsort(s_packed, i, e);  // depth exhausted
+                    else if (e - i > 1) ls_sort_range(s_packed, i, e, m);
+                }
+            }
         }
         __syncthreads();
         for (int i = t; i < n; i += kBfsThreads) {
