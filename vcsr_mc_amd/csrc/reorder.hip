@@ -22,7 +22,7 @@
 //      elements partitioned by the work-group, pieces finished by one thread each); larger
 //      levels take several kernels: claims, a radix sort by (parent index, id), and the group
 //      sorts (large groups a partition step at a time by work-groups, pieces of up to 256
-//      elements by one wave each in LDS).
+//      elements by one wave each in LDS, with wave-wide partition steps).
 //   5. order: vertices sorted by (component rank, level, index in level) give the
 //      Cuthill-McKee order; position = N - 1 - that index (reorder.hpp:72-76).
 #include <algorithm>
@@ -410,10 +410,13 @@ __global__ void k_group_jobs(const int* __restrict__ gstart, int ngroups, int n,
     else small[atomicAdd(nsmall, 1)] = job;
 }
 
-// One wave per piece: the piece is copied into LDS, one lane runs the library's steps on it
-// there (a chain of a few thousand dependent accesses for 256 elements, each at LDS rather
-// than cache latency), and the wave copies it back.
+// One wave per piece of at most kSortSmall elements, in LDS.  The wave runs the library's
+// introsort loop with wave-wide partition steps (wave_partition_lds) and marks the pieces it
+// leaves (at most 16 elements, or depth exhausted); then each lane finishes the pieces it finds:
+// the insertion pass, or a heapsort.  As in k_bfs_levels, every lane keeps its own identical
+// copy of the range stack, so no branch taken by one lane alone steers the loop.
 constexpr int kSmallSortWaves = 4;
+constexpr unsigned char kPieceNone = 255, kPieceEnd = 254, kPieceHeap = 253;
 
 __device__ __forceinline__ void wave_lds_fence() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -421,18 +424,113 @@ __device__ __forceinline__ void wave_lds_fence() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// One step of the introsort loop on s[lo, hi) (hi - lo > 16, depth > 0) by one wave: the
+// computation of k_partition_pass on 64 lanes.  lpos and rpos hold the pair positions
+// (K <= (hi - lo) / 2).  Returns the cut in every lane.
+__device__ int wave_partition_lds(u64* s, int lo, int hi, int* lpos, int* rpos, int* lnext) {
+    const int lane = threadIdx.x & 63;
+    if (lane == 0) {
+        ls_median_to_first(s, lo, lo + 1, lo + (hi - lo) / 2, hi - 1);
+        *lnext = INT_MAX;
+    }
+    wave_lds_fence();
+    const uint32_t kp = skey(s[lo]);
+    const int first = lo + 1, n = hi - first;
+    const int per = (n + 63) / 64;
+    const int b0 = min(first + lane * per, hi), b1 = min(b0 + per, hi);
+    int cge = 0, cle = 0;
+    for (int p = b0; p < b1; ++p) {
+        const uint32_t k = skey(s[p]);
+        cge += !(k < kp);
+        cle += !(kp < k);
+    }
+    const int ge_incl = wave_scan(cge, OpAdd{}, 0), le_all = wave_scan(cle, OpAdd{}, 0);
+    const int ge_before = ge_incl - cge, le_before = le_all - cle;
+    const int LE = __builtin_amdgcn_readlane(le_all, 63);
+    int kc = 0;
+    {
+        int rank = ge_before, le_incl = le_before;
+        for (int p = b0; p < b1; ++p) {
+            const uint32_t k = skey(s[p]);
+            le_incl += !(kp < k);
+            if (!(k < kp)) {
+                ++rank;
+                kc += (LE - le_incl >= rank);
+            }
+        }
+    }
+    const int K = __builtin_amdgcn_readlane(wave_scan(kc, OpAdd{}, 0), 63);
+    {
+        int rank = ge_before, le_excl = le_before;
+        for (int p = b0; p < b1; ++p) {
+            const uint32_t k = skey(s[p]);
+            if (!(k < kp)) {
+                ++rank;
+                if (rank <= K) lpos[rank - 1] = p;
+                else if (rank == K + 1) *lnext = p;
+            }
+            if (!(kp < k)) {
+                const int rr = LE - le_excl;
+                if (rr <= K) rpos[rr - 1] = p;
+                ++le_excl;
+            }
+        }
+    }
+    wave_lds_fence();
+    for (int r = lane; r < K; r += 64) {
+        const int x = lpos[r], y = rpos[r];
+        const u64 ax = s[x], ay = s[y];
+        s[x] = ay;
+        s[y] = ax;
+    }
+    wave_lds_fence();
+    return K == 0 ? *lnext : min(*lnext, rpos[K - 1]);
+}
+
 __global__ __launch_bounds__(64 * kSmallSortWaves) void k_small_sort(
     const int4* __restrict__ jobs, int njobs, u64* __restrict__ a) {
     __shared__ u64 piece[kSmallSortWaves][kSortSmall];
+    __shared__ unsigned char marks[kSmallSortWaves][kSortSmall + 4];
+    __shared__ int pairs[kSmallSortWaves][kSortSmall];  // lpos, then rpos
+    __shared__ int lnext[kSmallSortWaves];
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const long long j = (long long)blockIdx.x * kSmallSortWaves + w;
     if (j >= njobs) return;  // the same for every lane of the wave
     const int4 job = jobs[j];
     const int n = job.y - job.x;  // at most kSortSmall
+    if (n <= 1) return;
     u64* s = piece[w];
+    unsigned char* mark = marks[w];
     for (int i = lane; i < n; i += 64) s[i] = a[job.x + i];
+    for (int i = lane; i < n; i += 64) mark[i] = kPieceNone;
+    if (lane == 0) mark[n] = kPieceEnd;
     wave_lds_fence();
-    if (lane == 0) ls_sort_range(s, 0, n, job.z);
+    int4 stk[64];  // depth <= 2 floor(lg n) < 63 for n < 2^31
+    int sp = 1;
+    stk[0] = make_int4(0, n, job.z, 0);
+    while (sp > 0) {
+        const int4 r = stk[sp - 1];
+        if (r.y - r.x <= 16 || r.z == 0) {
+            mark[r.x] = r.y - r.x > 16 ? kPieceHeap : (unsigned char)r.z;
+            --sp;
+        } else {
+            const int cut = wave_partition_lds(s, r.x, r.y, pairs[w], pairs[w] + kSortSmall / 2,
+                                               &lnext[w]);
+            stk[sp - 1] = make_int4(cut, r.y, r.z - 1, 0);
+            stk[sp] = make_int4(r.x, cut, r.z - 1, 0);
+            ++sp;
+        }
+    }
+    wave_lds_fence();
+    for (int i = lane; i < n; i += 64) {
+        const int m = mark[i];
+        if (m <= kPieceHeap) {
+            int e = i + 1;
+            while (mark[e] == kPieceNone) ++e;
+            if (m == kPieceHeap) ls_heapsort(s, i, e);
+            else if (e - i > 1) ls_sort_range(s, i, e, m);
+        }
+    }
     wave_lds_fence();
     for (int i = lane; i < n; i += 64) a[job.x + i] = s[i];
 }
