@@ -108,6 +108,9 @@ def ref_lib():
         R.ref_rcm_order.argtypes = [i32p, i32p, C.c_int, C.c_int, i32p]
         R.ref_apply_column_permutation.argtypes = [i32p, i32p, f32p, C.c_int, C.c_int, i32p, f32p,
                                                    C.c_int]
+        R.ref_spmm_gpu.restype = C.c_int
+        R.ref_spmm_gpu.argtypes = [i32p, i32p, f32p, C.c_int, C.c_int, C.c_int, C.c_int,
+                                   C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_char_p, C.c_int]
         _ref = R
     return _ref
 
@@ -266,6 +269,19 @@ def ref_build_format(row_ptr, col, val, M, N, segw=16, fp32=False) -> Format:
         return _take(f)
     finally:
         lib().orc_free(C.byref(f))
+
+
+def ref_spmm_gpu(row_ptr, col, val, M, N, dB_ptr, O, dC_ptr, segw=32, tileK=128, fp32=False):
+    """C += A.B by the reference's own kernels (oracle/_ref) on the current GPU; dB_ptr (N x O
+    float32) and dC_ptr (M x O float32) are device pointers.  Synchronous."""
+    rp, ci, vv = _i32(row_ptr), _i32(col), _f32(val)
+    if ci.size == 0:
+        ci = np.zeros(1, np.int32); vv = np.zeros(1, np.float32)
+    err = C.create_string_buffer(512)
+    rc = ref_lib().ref_spmm_gpu(_p(rp, C.c_int), _p(ci, C.c_int), _p(vv, C.c_float), M, N, segw,
+                                int(fp32), dB_ptr, O, tileK, dC_ptr, err, 512)
+    if rc != 0:
+        raise OracleError(err.value.decode())
 
 
 def ref_half_scale(val) -> np.float32:

@@ -2,10 +2,12 @@
 //
 // TEST INFRASTRUCTURE ONLY.  oracle/Makefile compiles MuuSeoTia/VCSR_MC's src/vcsr_mc.cu
 // where it lies (with the reference's own HIP flags, CMakeLists.txt:24-27) and links it with
-// this file into oracle/_ref/libvcsrmc_ref.so.  Tests call it on the CPU only (no HIP API is
-// used) to pin the oracle's restatement of csr_to_vcsr_mc (src/vcsr_mc.cu:25-123),
-// half_scale (src/vcsr_mc.cu:14-22) and the column reordering (include/reorder.hpp, a
-// header-only part of the reference), and to write the golden fixtures under tests/golden/.
+// this file into oracle/_ref/libvcsrmc_ref.so.  Tests call it on the CPU to pin the oracle's
+// restatement of csr_to_vcsr_mc (src/vcsr_mc.cu:25-123), half_scale (src/vcsr_mc.cu:14-22)
+// and the column reordering (include/reorder.hpp, a header-only part of the reference), and
+// to write the golden fixtures under tests/golden/; GPU tests call ref_spmm_gpu to check the
+// library's product against the reference's own kernels (src/vcsr_mc.cu:143-394) on the same
+// inputs.
 #include <cstdlib>
 #include <cstring>
 #include <exception>
@@ -54,6 +56,32 @@ int ref_build(const int* row_ptr, const int* col, const float* val, int M, int N
         out->item_gend = dup(V.item_gend);
         out->scale = V.scale;
         out->fp32 = V.fp32 ? 1 : 0;
+        return 0;
+    } catch (const std::exception& e) {
+        if (err && errlen > 0) { std::strncpy(err, e.what(), errlen - 1); err[errlen - 1] = 0; }
+        return 1;
+    }
+}
+
+// C = A.B by the reference's own path on the current GPU: csr_to_vcsr_mc, then
+// upload_vcsr_mc_device and run_vcsr_mc_spmm_gpu (src/vcsr_mc.cu:332-394; its kernels
+// vcsr_mc / vcsr_mc_fp32 accumulate into C with atomicAdd), then destroy_vcsr_mc_device.  dB
+// (N x O floats) and dC (M x O floats, accumulated into) are device pointers.  Returns 0, or 1
+// when the reference threw (message in err).
+int ref_spmm_gpu(const int* row_ptr, const int* col, const float* val, int M, int N, int segw,
+                 int fp32, const float* dB, int O, int tileK, float* dC, char* err, int errlen) {
+    try {
+        CSR csr;
+        csr.M = M; csr.N = N; csr.nnz = M ? row_ptr[M] : 0;
+        csr.row_ptr.assign(row_ptr, row_ptr + M + 1);
+        csr.col.assign(col, col + csr.nnz);
+        csr.val.assign(val, val + csr.nnz);
+        VCSRMC V = csr_to_vcsr_mc(csr, fp32 != 0, segw);
+        destroy_vcsr_mc_device(nullptr);
+        upload_vcsr_mc_device(V);
+        float ms = 0.f;
+        run_vcsr_mc_spmm_gpu(V, dB, O, tileK, dC, nullptr, ms);
+        destroy_vcsr_mc_device(nullptr);
         return 0;
     } catch (const std::exception& e) {
         if (err && errlen > 0) { std::strncpy(err, e.what(), errlen - 1); err[errlen - 1] = 0; }
