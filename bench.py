@@ -196,7 +196,10 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved_gbs / HBM_PEAK_GBS, 4),
-            "traffic": traffic_from_profiles(f"config{cfg}-{prec}"),
+            # measured for the full workload at its O and tileK 128 (profiles/); other runs: null
+            "traffic": (traffic_from_profiles(f"config{cfg}-{prec}")
+                        if args.size == 0 and O == w["O"] and args.tileK == TILEK
+                        and not args.b_fp32 else None),
             "bytes_alg": int(bytes_alg),
         },
         "mfma": {"padded_tflops": round(mfma_tflops, 2), "peak": MFMA_PEAK_TFLOPS[prec],
