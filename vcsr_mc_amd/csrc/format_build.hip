@@ -585,8 +585,8 @@ static void build_exec_layout(DeviceFormat& F, const int* trow, const int* tcol,
 // ------------------------------------------------------------------------------------------
 template <typename K>
 static void build_groups_k(DeviceFormat& F, const int* d_col, const float* d_val,
-                           const int* row_of, const int* pstart, const int* prow, int P, int S,
-                           float inv_scale, hipStream_t st) {
+                           const int* pstart, const int* prow, int P, int S, float inv_scale,
+                           hipStream_t st) {
     const int segw = F.segw;
     const int kbits = 6 + bits_for((unsigned long long)(S > 0 ? S - 1 : 0));
     DevBuf<K> k1(P), k2(P);
@@ -702,10 +702,10 @@ void build_from_csr(DeviceFormat& F, const int* d_row_ptr, const int* d_col, con
     pidx.release();
 
     if (6 + bits_for((unsigned long long)(S - 1)) <= 32)
-        build_groups_k<uint32_t>(F, d_col, d_val, row_of.p, pstart.p, prow.p, P, S, inv_scale, st);
+        build_groups_k<uint32_t>(F, d_col, d_val, pstart.p, prow.p, P, S, inv_scale, st);
     else
-        build_groups_k<unsigned long long>(F, d_col, d_val, row_of.p, pstart.p, prow.p, P, S,
-                                           inv_scale, st);
+        build_groups_k<unsigned long long>(F, d_col, d_val, pstart.p, prow.p, P, S, inv_scale,
+                                           st);
     pstart.release();
     prow.release();
 
