@@ -59,7 +59,8 @@ int vcsrmc_create(vcsrmc_t *out);
 int vcsrmc_destroy(vcsrmc_t h);
 
 /* FP16 range scale of the values of a device array (src/vcsr_mc.cu:14-22, evaluated as the
- * reference binary does, see DESIGN).  Replaces half_scale (include/vcsr_formats.hpp:11). */
+ * reference binary does: it is built with -ffast-math, CMakeLists.txt:24-27, so amax / 60000
+ * is amax * fl(1/60000)).  Replaces half_scale (include/vcsr_formats.hpp:11). */
 int vcsrmc_half_scale(const float *d_val, long long nnz, float *scale, void *stream);
 
 /* Builds the format on the GPU from a device CSR (row_ptr[M+1], col[nnz] strictly increasing
