@@ -94,7 +94,8 @@ int vcsrmc_download(vcsrmc_t h, int *group_ptr, int *group_depth, int *group_seg
  * binary16, converted once by the caller).  tileK in {16,32,64,128} is the widest
  * output-column tile of one work-group, as in the reference; the launcher takes a narrower one
  * when O needs less, or 64 instead of 128 for formats whose tiles hold few nonzeros (FP32, or B
- * larger than the GPU's L2), where that measured faster; the result does not depend on it.
+ * larger than the GPU's L2) and for FP32 formats of fewer than 2048 16-row panels, where that
+ * measured faster; the result does not depend on it.
  * Rows of C that A does not touch
  * are left as they are.  If ms is non-NULL the launch is bracketed by two hipEvents on
  * `stream`, the call waits for it and *ms is the elapsed time (the reference's protocol);

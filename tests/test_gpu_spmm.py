@@ -211,6 +211,34 @@ def test_mixed_tile_fill(orc, fp32, tileK):
     check(orc, rp, c, v, M, N, B, fp32, tileK=tileK, C0=C0)
 
 
+@pytest.mark.parametrize("keep", [1.0, 0.4])
+@pytest.mark.parametrize("O", [100, 128])
+def test_fp32_full_tiles_many_panels(orc, keep, O):
+    """FP32 formats take O tiles of 128 only with at least 2048 panels and tiles of 48 or more
+    nonzeros on average: a band of 49 diagonals over 2100 panels (keep = 1: dense tile copies;
+    keep = 0.4: entry lists), O = 100 (B and C past the vector width) and 128, C starting
+    non-zero, the whole product against the oracle."""
+    rng = np.random.default_rng(int(O + 10 * keep))
+    M = N = 2100 * 16
+    rp, c, v = band_csr(rng, M, N, 24, 1.0)
+    if keep < 1.0:
+        row = np.repeat(np.arange(M), np.diff(rp))
+        sel = rng.random(c.size) < keep
+        rp = np.zeros(M + 1, np.int32)
+        rp[1:] = np.cumsum(np.bincount(row[sel], minlength=M))
+        c, v = c[sel], v[sel]
+    B = rng.uniform(-1, 1, (N, O)).astype(np.float32)
+    C0 = rng.uniform(-1, 1, (M, O)).astype(np.float32)
+    say("fp32 full tiles, many panels", keep, O, c.size)
+    C, info = run_spmm(rp, c, v, M, N, B, True, C0=C0)
+    assert info["num_panels"] >= 2048 and info["nnz"] >= 48 * info["num_chunks"]
+    R, L1 = orc.spmm_csr(rp, c, v, M, B, mode=0, scale=info["scale"])
+    R = R + C0.astype(np.float64)
+    L1 = L1 + np.abs(C0.astype(np.float64)).sum(axis=1)
+    ok, worst, r = row_l1_parity(C, R, L1, TAU[True])
+    assert ok, f"row {r}: error / bound = {worst:.3g}"
+
+
 @pytest.mark.parametrize("seed", range(4))
 def test_random_sweep(orc, seed):
     """Random shapes, patterns (uniform, Poisson rows with heavy rows, bands), value ranges,

@@ -463,7 +463,7 @@ static void check_err(const int* d_err, hipStream_t st) {
 // wave (measured on gfx950: 6 to 12 tiles are equally good for stencil and R-MAT matrices, 6 is
 // 2% faster than 7 or 8 on the power-law matrix; 4 starves the stencil of waves and slows the
 // power-law one by 6%, 16 leaves R-MAT with long single-wave units).
-static int light_tile_limit(int num_panels) { return num_panels >= 2048 ? 6 : 1; }
+static int light_tile_limit(int num_panels) { return num_panels >= kFewPanels ? 6 : 1; }
 
 template <typename K>
 static void build_exec_layout_k(DeviceFormat& F, const int* trow, const int* tcol,

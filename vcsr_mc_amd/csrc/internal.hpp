@@ -48,6 +48,11 @@ struct XcdSplit {
 //                   512 slots are filled: dense_a16[512 d + 32 row + k] (FP16), or
 //                   dense_a32[512 d + 128 (k & 3) + 8 row + (k >> 2)] (FP32) -- exactly the
 //                   order in which MFMA lanes read their A operand, so a lane loads it directly
+// Below this many 16-row panels a launch cannot fill the GPU's 1024 SIMDs with one wave per
+// panel: every multi-tile panel is then shared by a work-group (format_build.hip), and FP32
+// formats take O tiles of 64 (spmm_kernels.hip).
+constexpr int kFewPanels = 2048;
+
 struct DeviceFormat {
     int M = 0, N = 0, segw = 16, bundle = 16, num_segments = 0;
     int G = 0, nitems = 0;

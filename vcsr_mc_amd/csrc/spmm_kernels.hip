@@ -745,16 +745,21 @@ __global__ void k_b_to_half(const float* __restrict__ B, _Float16* __restrict__ 
 //     format is FP32 (each wave's chain of FP32 matrix-core steps halves: uniform 4096^2 8.1 ->
 //     7.0 us, power-law 36,692^2 33.0 -> 30.2, R-MAT scale 22 5.91 -> 5.70 ms) or B is larger
 //     than the 32 MB of L2 on the 8 XCDs (two O halves on separate XCD groups each fetch half of
-//     every B row, over a union of fewer row ranges: FP16 R-MAT 3.05 -> 2.86 ms).  Fuller tiles
-//     keep 128, since every O tile repeats the A side of each tile (27-point stencil 100^3 and
-//     32 x 32 blocks: 2-24% slower at 64), as do FP16 formats with a cache-resident B
-//     (power-law: 15.4 -> 17.4 us at 64).
+//     every B row, over a union of fewer row ranges: FP16 R-MAT 3.05 -> 2.86 ms);
+//   * 64 for FP32 formats with fewer than kFewPanels panels, where the launch at 128 holds too
+//     few waves and each one a long FP32 chain (27-point stencil 18^3 8.22 -> 7.09 us, 30^3
+//     26.6 -> 24.5; 32 x 32 blocks, 96 block rows 6.59 -> 5.97, 512 block rows 26.6 -> 24.7).
+//   Otherwise fuller tiles keep 128, since every O tile repeats the A side of each tile
+//   (27-point stencil 100^3 and 32 x 32 blocks at 8192 block rows: 2-14% slower at 64), as do
+//   FP16 formats with a cache-resident B (power-law: 15.4 -> 17.4 us at 64).
 static int o_tile_width(const DeviceFormat& F, bool b_f16, int O, int tileK) {
     int tk = tileK;
     while (tk > 16 && tk / 2 >= O) tk /= 2;
-    if (tk == 128 && F.num_chunks > 0 && F.nnz < 48LL * F.num_chunks) {
+    if (tk == 128 && F.num_chunks > 0) {
+        const bool sparse_tiles = F.nnz < 48LL * F.num_chunks;
         const long long b_bytes = (long long)F.N * O * (b_f16 ? 2 : 4);
-        if (F.fp32 || b_bytes > (32LL << 20)) tk = 64;
+        if (F.fp32 && (sparse_tiles || F.num_panels < kFewPanels)) tk = 64;
+        else if (sparse_tiles && b_bytes > (32LL << 20)) tk = 64;
     }
     return tk;
 }
