@@ -95,13 +95,14 @@ int vcsrmc_download(vcsrmc_t h, int *group_ptr, int *group_depth, int *group_seg
  * output-column tile of one work-group, as in the reference; the launcher takes a narrower one
  * when O needs less, or 64 instead of 128 for formats whose tiles hold few nonzeros (FP32, or B
  * larger than the GPU's L2) and for FP32 formats of fewer than 2048 16-row panels, where that
- * measured faster; the result does not depend on it.
- * Rows of C that A does not touch
- * are left as they are.  If ms is non-NULL the launch is bracketed by two hipEvents on
- * `stream`, the call waits for it and *ms is the elapsed time (the reference's protocol);
- * if ms is NULL the launch is asynchronous.  An FP16 format given FP32 B with nnz >= 2 N
- * converts B to binary16 once per call into a buffer the handle keeps (N x O halves, allocated
- * on first use), so calls on one handle from several streams at once must not overlap.  The
+ * measured faster; the result does not depend on it.  Rows of C that A does not touch are left
+ * as they are.  If ms is non-NULL the launch is bracketed by two hipEvents on `stream`, the
+ * call waits for it and *ms is the elapsed time (the reference's protocol); if ms is NULL the
+ * launch is asynchronous.  An FP16 format given FP32 B rounds B to binary16 as the kernel
+ * loads it; where nnz >= 4 N and B exceeds 32 MB with tiles averaging fewer than 48 nonzeros,
+ * or exceeds 256 MB, it converts B once per call instead, into a buffer the handle keeps
+ * (N x O halves, allocated on first use), so calls on one handle from several streams at once
+ * must not overlap.  The
  * launch itself allocates and clears nothing, so it can be captured in a HIP graph (make that
  * first FP32-B call before capturing).
  * Replaces run_vcsr_mc_spmm_gpu (include/vcsr_formats.hpp:24-25, src/vcsr_mc.cu:352-394). */

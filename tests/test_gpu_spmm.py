@@ -73,29 +73,35 @@ def test_split_panels_and_accumulate(orc, fp32):
     assert C[empty].tobytes() == C0[empty].tobytes()
 
 
-@pytest.mark.parametrize("density", [0.004, 0.03])
-def test_fp16_b_matches_fp32_b(orc, density):
+@pytest.mark.parametrize("M,N,kw", [(300, 400, dict(density=0.004)),
+                                     (300, 400, dict(density=0.03)),
+                                     (20000, 70000, dict(nnz_per_row=16))])
+def test_fp16_b_matches_fp32_b(orc, M, N, kw):
     """FP16 B in HBM (converted by the caller) gives the same result as FP32 B, which the
-    library rounds to binary16 either in the kernel (nnz < 2 N, density 0.004) or in one
-    conversion pass before it (nnz >= 2 N, density 0.03); B itself is left untouched."""
+    library rounds to binary16 either in the kernel (the two small cases) or in one conversion
+    pass before it (B of 70,000 x 128 floats > 32 MB, tiles of fewer than 48 nonzeros,
+    nnz >= 4 N); B itself is left untouched."""
     import torch
     rng = np.random.default_rng(12)
-    rp, c, v = random_csr(rng, 300, 400, density=density)
-    assert (len(c) >= 800) == (density > 0.01)
-    B = rng.uniform(-2, 2, (400, 128)).astype(np.float32)
-    say("fp16 B vs fp32 B", density)
-    with vm.DeviceFormat.from_device_csr(dev(rp), dev(c), dev(v), 300, 400, False, 32) as f:
-        assert f.info()["num_units"] == f.info()["num_panels"]  # no split panel: no atomics
+    rp, c, v = random_csr(rng, M, N, **kw)
+    B = rng.uniform(-2, 2, (N, 128)).astype(np.float32)
+    say("fp16 B vs fp32 B", M, N, len(c))
+    with vm.DeviceFormat.from_device_csr(dev(rp), dev(c), dev(v), M, N, False, 32) as f:
+        info = f.info()
+        assert info["num_units"] == info["num_panels"]  # no split panel: no atomics
+        converts = (N * 128 * 4 > 32 << 20 and len(c) >= 4 * N
+                    and len(c) < 48 * info["num_chunks"])
+        assert converts == (M == 20000)
         dB = dev(B)
-        C1 = torch.zeros((300, 128), dtype=torch.float32, device="cuda")
+        C1 = torch.zeros((M, 128), dtype=torch.float32, device="cuda")
         C2 = torch.zeros_like(C1)
         f.spmm(dB, C1, tileK=128)
         f.spmm(dB.half(), C2, tileK=128)
         torch.cuda.synchronize()
         assert np.array_equal(dB.cpu().numpy(), B)
         assert np.array_equal(C1.cpu().numpy(), C2.cpu().numpy())
-    check(orc, rp, c, v, 300, 400, B, False)
-    check(orc, rp, c, v, 300, 400, B, False, b16=True)
+    check(orc, rp, c, v, M, N, B, False)
+    check(orc, rp, c, v, M, N, B, False, b16=True)
 
 
 def test_scaled_values(orc):

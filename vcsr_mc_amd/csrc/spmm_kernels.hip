@@ -773,11 +773,22 @@ void spmm_launch(const DeviceFormat& F, const void* dB, bool b_f16, int O, int t
     if (F.fp32 && b_f16) throw Error(VCSRMC_ERR_ARG, "an FP32 format takes an FP32 B");
     if (F.num_units == 0 || O == 0) return;
     if (!dB || !dC) throw Error(VCSRMC_ERR_ARG, "null B or C");
-    // FP16 format, FP32 B: when B rows are used at least twice on average, converting B once
-    // (6 bytes per element) costs less than gathering FP32 rows, and the FP16-B kernel holds
-    // fewer registers (3 waves per SIMD instead of 2).  Same values: the kernel converts with
-    // the same rounding.
-    if (!F.fp32 && !b_f16 && F.nnz >= 2LL * F.N && ((uintptr_t)dB % 16) == 0) {
+    // FP16 format, FP32 B: the kernel rounds each gathered FP32 B row to binary16 as it loads
+    // it.  Converting B once instead costs 6 bytes per element and saves 2 per element on each
+    // gather from beyond the caches, so it pays only where B rows are used at least 4 times and
+    // either B exceeds the 32 MB of L2 on the 8 XCDs with tiles of few nonzeros (< 48 on
+    // average: about one gathered row per nonzero, little reuse inside a panel), or B exceeds
+    // the 256 MB last-level cache, beyond which every re-read of a B row comes from HBM.
+    // Measured on gfx950, reference protocol, converted: uniform 100,000^2 with 16 per row
+    // 118 -> 82 us, 27-point stencil 100^3 572 -> 534 us; kept direct, where converting
+    // measured slower: uniform 4096^2 8.0 us (11.9 converted), 300,000^2 with 3 per row 114
+    // (130), 27-point stencil 60^3 94 (117), R-MAT scale 15 23 (26), power-law 36,692^2 24.9
+    // (25.7).  Same values either way: both round to nearest even.
+    const long long b32_bytes = (long long)F.N * O * 4;
+    if (!F.fp32 && !b_f16 && ((uintptr_t)dB % 16) == 0 && F.num_chunks > 0 &&
+        F.nnz >= 4LL * F.N &&
+        ((F.nnz < 48LL * F.num_chunks && b32_bytes > (32LL << 20)) ||
+         b32_bytes > (256LL << 20))) {
         const long long n = (long long)F.N * O;
         if ((long long)F.b_half.n < n) F.b_half.alloc((size_t)n);
         hipLaunchKernelGGL(k_b_to_half, dim3(grid_for((n + 3) / 4, 256)), dim3(256), 0, st,
