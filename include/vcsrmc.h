@@ -99,7 +99,7 @@ int vcsrmc_download(vcsrmc_t h, int *group_ptr, int *group_depth, int *group_seg
  * as they are.  If ms is non-NULL the launch is bracketed by two hipEvents on `stream`, the
  * call waits for it and *ms is the elapsed time (the reference's protocol); if ms is NULL the
  * launch is asynchronous.  An FP16 format given FP32 B rounds B to binary16 as the kernel
- * loads it; where nnz >= 4 N and B exceeds 32 MB with tiles averaging fewer than 48 nonzeros,
+ * loads it; where nnz >= 12 N and B exceeds 12 MB with tiles averaging fewer than 48 nonzeros,
  * or exceeds 256 MB, it converts B once per call instead, into a buffer the handle keeps
  * (N x O halves, allocated on first use), so calls on one handle from several streams at once
  * must not overlap.  The

@@ -75,12 +75,12 @@ def test_split_panels_and_accumulate(orc, fp32):
 
 @pytest.mark.parametrize("M,N,kw", [(300, 400, dict(density=0.004)),
                                      (300, 400, dict(density=0.03)),
-                                     (20000, 70000, dict(nnz_per_row=16))])
+                                     (30000, 30000, dict(nnz_per_row=16))])
 def test_fp16_b_matches_fp32_b(orc, M, N, kw):
     """FP16 B in HBM (converted by the caller) gives the same result as FP32 B, which the
     library rounds to binary16 either in the kernel (the two small cases) or in one conversion
-    pass before it (B of 70,000 x 128 floats > 32 MB, tiles of fewer than 48 nonzeros,
-    nnz >= 4 N); B itself is left untouched."""
+    pass before it (B of 30,000 x 128 floats > 12 MB, tiles of fewer than 48 nonzeros,
+    nnz >= 12 N); B itself is left untouched."""
     import torch
     rng = np.random.default_rng(12)
     rp, c, v = random_csr(rng, M, N, **kw)
@@ -89,9 +89,9 @@ def test_fp16_b_matches_fp32_b(orc, M, N, kw):
     with vm.DeviceFormat.from_device_csr(dev(rp), dev(c), dev(v), M, N, False, 32) as f:
         info = f.info()
         assert info["num_units"] == info["num_panels"]  # no split panel: no atomics
-        converts = (N * 128 * 4 > 32 << 20 and len(c) >= 4 * N
-                    and len(c) < 48 * info["num_chunks"])
-        assert converts == (M == 20000)
+        converts = (len(c) >= 12 * N and len(c) < 48 * info["num_chunks"]
+                    and N * 128 * 4 > 12 << 20)
+        assert converts == (M == 30000)
         dB = dev(B)
         C1 = torch.zeros((M, 128), dtype=torch.float32, device="cuda")
         C2 = torch.zeros_like(C1)

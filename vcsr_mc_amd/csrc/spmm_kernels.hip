@@ -774,20 +774,24 @@ void spmm_launch(const DeviceFormat& F, const void* dB, bool b_f16, int O, int t
     if (F.num_units == 0 || O == 0) return;
     if (!dB || !dC) throw Error(VCSRMC_ERR_ARG, "null B or C");
     // FP16 format, FP32 B: the kernel rounds each gathered FP32 B row to binary16 as it loads
-    // it.  Converting B once instead costs 6 bytes per element and saves 2 per element on each
-    // gather from beyond the caches, so it pays only where B rows are used at least 4 times and
-    // either B exceeds the 32 MB of L2 on the 8 XCDs with tiles of few nonzeros (< 48 on
-    // average: about one gathered row per nonzero, little reuse inside a panel), or B exceeds
-    // the 256 MB last-level cache, beyond which every re-read of a B row comes from HBM.
-    // Measured on gfx950, reference protocol, converted: uniform 100,000^2 with 16 per row
-    // 118 -> 82 us, 27-point stencil 100^3 572 -> 534 us; kept direct, where converting
-    // measured slower: uniform 4096^2 8.0 us (11.9 converted), 300,000^2 with 3 per row 114
-    // (130), 27-point stencil 60^3 94 (117), R-MAT scale 15 23 (26), power-law 36,692^2 24.9
-    // (25.7).  Same values either way: both round to nearest even.
+    // it.  Converting B once instead costs 6 bytes per element and a pass before the multiply,
+    // and saves 2 bytes per element on each gather from beyond the caches, so it pays only for
+    // B rows used many times (12 or more on average) that come from beyond the caches: B above
+    // 12 MB (three times one XCD's 4 MB L2, which each XCD fills with its own copies) with
+    // tiles of few nonzeros (< 48 on average: about one gathered row per nonzero), or B above
+    // the 256 MB last-level cache.  Measured on gfx950 (reference protocol, 24 synthetic
+    // matrices and the benchmark workloads), direct -> converted: uniform random 100,000^2 with
+    // 16 per row 118 -> 83 us, 50,000^2 with 32 per row 107 -> 62, power-law 30,000^2 with 20
+    // per row 37 -> 31, 27-point stencil 100^3 572 -> 534; kept direct, where converting measured
+    // slower: 5-point grids 500^2 / 700^2 75 / 171 us (105 / 208 converted), 7-point 60^3 61
+    // (88), 27-point 60^3 94 (117), uniform 300,000^2 with 3 per row 113 (129), uniform 4096^2
+    // 8.0 (11.9), power-law 36,692^2 24.9 (25.7), R-MAT scale 17 51 (55).  Missed by the rule:
+    // R-MAT scale 15 (converted, 23 -> 26 us) and power-law 200,000^2 with 6 per row (direct,
+    // 98 against 92).  Same values either way: both round to nearest even.
     const long long b32_bytes = (long long)F.N * O * 4;
     if (!F.fp32 && !b_f16 && ((uintptr_t)dB % 16) == 0 && F.num_chunks > 0 &&
-        F.nnz >= 4LL * F.N &&
-        ((F.nnz < 48LL * F.num_chunks && b32_bytes > (32LL << 20)) ||
+        F.nnz >= 12LL * F.N &&
+        ((F.nnz < 48LL * F.num_chunks && b32_bytes > (12LL << 20)) ||
          b32_bytes > (256LL << 20))) {
         const long long n = (long long)F.N * O;
         if ((long long)F.b_half.n < n) F.b_half.alloc((size_t)n);
