@@ -388,7 +388,8 @@ __device__ __forceinline__ void tiles_f16(int first, int end, int W, int lane, i
 }
 
 // Register budget: FP16 B with aligned rows fits three waves per SIMD without spilling; the
-// FP32-B and unaligned variants hold more B data and are given two.
+// FP32-B and unaligned variants hold more B data and are given two (at O tiles of 64 or less
+// they still fit three: 139 VGPRs for FP32 B).
 template <typename TB, bool ALIGNED>
 constexpr int f16_min_waves() { return (sizeof(TB) == 2 && ALIGNED) ? 3 : 2; }
 
@@ -710,7 +711,7 @@ static void launch_tk(const DeviceFormat& F, const void* dB, bool b_f16, int O, 
             hipLaunchKernelGGL((k_spmm_f16<TK, _Float16, false>), grid, block, 0, st, F.units.p, NH,
                                xs, F.chunk_eptr.p, F.chunk_cols.p, F.chunk_dense.p, F.entries.p,
                                F.dense_a16.p, B, O, F.scale, c4, dC);
-    } else {
+    } else if constexpr (TK <= 64) {
         const float* B = static_cast<const float*>(dB);
         if (aligned)
             hipLaunchKernelGGL((k_spmm_f16<TK, float, true>), grid, block, 0, st, F.units.p, NH,
@@ -720,6 +721,9 @@ static void launch_tk(const DeviceFormat& F, const void* dB, bool b_f16, int O, 
             hipLaunchKernelGGL((k_spmm_f16<TK, float, false>), grid, block, 0, st, F.units.p, NH,
                                xs, F.chunk_eptr.p, F.chunk_cols.p, F.chunk_dense.p, F.entries.p,
                                F.dense_a16.p, B, O, F.scale, c4, dC);
+    } else {
+        // o_tile_width never gives an FP16 format reading FP32 B an O tile of 128.
+        throw Error(VCSRMC_ERR_STATE, "no O tile of 128 for FP32 B with an FP16 format");
     }
     VCSRMC_HIP(hipGetLastError());
 }
@@ -749,9 +753,13 @@ __global__ void k_b_to_half(const float* __restrict__ B, _Float16* __restrict__ 
 //   * 64 for FP32 formats with fewer than kFewPanels panels, where the launch at 128 holds too
 //     few waves and each one a long FP32 chain (27-point stencil 18^3 8.22 -> 7.09 us, 30^3
 //     26.6 -> 24.5; 32 x 32 blocks, 96 block rows 6.59 -> 5.97, 512 block rows 26.6 -> 24.7).
+//   * 64 for FP16 formats reading FP32 B rows: at 128 that kernel needs 222 VGPRs (two waves
+//     per SIMD; three would spill), at 64 139 (three waves), which outweighs repeating the A
+//     side (uniform 4096^2 7.9 -> 7.4 us, uniform 20,000^2 with 8 per row 17.9 -> 16.2,
+//     power-law 36,692^2 24.5 -> 23.5, 27-point stencil 60^3 90.6 -> 83.1).
 //   Otherwise fuller tiles keep 128, since every O tile repeats the A side of each tile
 //   (27-point stencil 100^3 and 32 x 32 blocks at 8192 block rows: 2-14% slower at 64), as do
-//   FP16 formats with a cache-resident B (power-law: 15.4 -> 17.4 us at 64).
+//   FP16 formats with a cache-resident FP16 B (power-law: 15.4 -> 17.4 us at 64).
 static int o_tile_width(const DeviceFormat& F, bool b_f16, int O, int tileK) {
     int tk = tileK;
     while (tk > 16 && tk / 2 >= O) tk /= 2;
@@ -759,6 +767,7 @@ static int o_tile_width(const DeviceFormat& F, bool b_f16, int O, int tileK) {
         const bool sparse_tiles = F.nnz < 48LL * F.num_chunks;
         const long long b_bytes = (long long)F.N * O * (b_f16 ? 2 : 4);
         if (F.fp32 && (sparse_tiles || F.num_panels < kFewPanels)) tk = 64;
+        else if (!F.fp32 && !b_f16) tk = 64;
         else if (sparse_tiles && b_bytes > (32LL << 20)) tk = 64;
     }
     return tk;
