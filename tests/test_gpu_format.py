@@ -120,6 +120,31 @@ def test_build_errors():
     assert e.value.status == vm.ERR_SEGW
 
 
+def test_python_binding_checks_operands():
+    """The Python binding checks sizes, element types and devices on the host, before any
+    launch: a row_ptr of M elements, int64 columns, a B of N - 1 rows, a C of M - 1 rows and a
+    host B are refused; the valid call then runs."""
+    import torch
+    say("binding operand checks")
+    rp = np.array([0, 2, 3], np.int32)
+    c = np.array([0, 4, 1], np.int32)
+    v = np.ones(3, np.float32)
+    for args in ((dev(rp[:2]), dev(c), dev(v)), (dev(rp), dev(c.astype(np.int64)), dev(v))):
+        with pytest.raises(vm.VCSRMCError) as e:
+            vm.DeviceFormat.from_device_csr(*args, 2, 5)
+        assert e.value.status == vm.ERR_ARG
+    with vm.DeviceFormat.from_device_csr(dev(rp), dev(c), dev(v), 2, 5) as f:
+        C = torch.zeros((2, 8), dtype=torch.float32, device="cuda")
+        ones = lambda n, where="cuda": torch.ones((n, 8), device=where)
+        for B, Cout in ((ones(4), C), (ones(5), C[:1]), (ones(5, "cpu"), C)):
+            with pytest.raises(vm.VCSRMCError) as e:
+                f.spmm(B, Cout)
+            assert e.value.status == vm.ERR_ARG
+        f.spmm(ones(5), C)
+        torch.cuda.synchronize()
+    assert C.cpu().numpy().tolist() == [[2.0] * 8, [1.0] * 8]
+
+
 def test_upload_rejects_inconsistent_arrays(orc, rng):
     rp, c, v = random_csr(rng, 100, 100, density=0.05)
     f = orc.build_format(rp, c, v, 100, 100, 16, False)

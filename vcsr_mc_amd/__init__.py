@@ -184,6 +184,7 @@ class DeviceFormat:
         h = C.c_void_p()
         _check(lib().vcsrmc_create(C.byref(h)), "vcsrmc_create")
         self._h = h
+        self._mn = None  # (M, N) once a format is built or uploaded
 
     @property
     def handle(self):
@@ -211,12 +212,19 @@ class DeviceFormat:
     @classmethod
     def from_device_csr(cls, row_ptr, col, val, M, N, fp32=False, segw=16, stream=None):
         """GPU build from torch device tensors (int32 row_ptr/col, float32 val)."""
-        f = cls()
+        import torch
         nnz = int(col.numel())
+        for t, dt, n, name in ((row_ptr, torch.int32, int(M) + 1, "row_ptr"),
+                               (col, torch.int32, nnz, "col"), (val, torch.float32, nnz, "val")):
+            if t.dtype != dt or not t.is_cuda or not t.is_contiguous() or t.numel() != n:
+                raise VCSRMCError(ERR_ARG, f"{name} must be a contiguous {dt} device tensor "
+                                           f"of {n} elements")
+        f = cls()
         _check(lib().vcsrmc_build_csr(f.handle, _ptr(row_ptr), _ptr(col) if nnz else None,
                                       _ptr(val) if nnz else None, int(M), int(N), nnz,
                                       int(bool(fp32)), int(segw), _stream_ptr(stream)),
                "vcsrmc_build_csr")
+        f._mn = (int(M), int(N))
         return f
 
     @classmethod
@@ -265,6 +273,15 @@ class DeviceFormat:
         if not (B.is_contiguous() and C_out.is_contiguous()):
             raise VCSRMCError(ERR_ARG, "B and C must be contiguous row-major")
         O = int(B.shape[1]) if O is None else int(O)
+        if self._mn is None:
+            i = self.info()
+            self._mn = (i["M"], i["N"])
+        M, N = self._mn
+        if not (B.is_cuda and C_out.is_cuda and B.device == C_out.device):
+            raise VCSRMCError(ERR_ARG, "B and C must be tensors on the same GPU")
+        if O < 0 or B.numel() < N * O or C_out.numel() < M * O:
+            raise VCSRMCError(ERR_ARG, f"B needs N x O = {N} x {O} and C M x O = {M} x {O} "
+                                       f"elements; got {B.numel()} and {C_out.numel()}")
         ms = C.c_float(0.0)
         _check(lib().vcsrmc_spmm(self.handle, _ptr(B), b_dtype, O, int(tileK), _ptr(C_out),
                                  _stream_ptr(stream), C.byref(ms) if timed else None),
