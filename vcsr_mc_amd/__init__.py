@@ -124,6 +124,16 @@ def _ptr(x) -> int | None:
     return int(x.data_ptr())
 
 
+def _need(t, dtype, n: int, name: str, exact: bool = True) -> None:
+    """Host-side check of a device operand: a contiguous CUDA tensor of `dtype` holding n
+    elements (at least n when not exact), so that no kernel is launched on a short buffer."""
+    ok = (t is not None and t.dtype == dtype and t.is_cuda and t.is_contiguous()
+          and (t.numel() == n if exact else t.numel() >= n))
+    if not ok:
+        raise VCSRMCError(ERR_ARG, f"{name} must be a contiguous {dtype} device tensor of "
+                                   f"{'' if exact else 'at least '}{n} elements")
+
+
 def _stream_ptr(stream) -> int | None:
     if stream is None:
         import torch
@@ -214,11 +224,9 @@ class DeviceFormat:
         """GPU build from torch device tensors (int32 row_ptr/col, float32 val)."""
         import torch
         nnz = int(col.numel())
-        for t, dt, n, name in ((row_ptr, torch.int32, int(M) + 1, "row_ptr"),
-                               (col, torch.int32, nnz, "col"), (val, torch.float32, nnz, "val")):
-            if t.dtype != dt or not t.is_cuda or not t.is_contiguous() or t.numel() != n:
-                raise VCSRMCError(ERR_ARG, f"{name} must be a contiguous {dt} device tensor "
-                                           f"of {n} elements")
+        _need(row_ptr, torch.int32, int(M) + 1, "row_ptr")
+        _need(col, torch.int32, nnz, "col")
+        _need(val, torch.float32, nnz, "val")
         f = cls()
         _check(lib().vcsrmc_build_csr(f.handle, _ptr(row_ptr), _ptr(col) if nnz else None,
                                       _ptr(val) if nnz else None, int(M), int(N), nnz,
@@ -340,7 +348,11 @@ def destroy_vcsr_mc_device(stream=None) -> None:
 # ---- column reordering (include/reorder.hpp:17-108), computed on the GPU -------------------
 def rcm_order_device(row_ptr, col, M: int, N: int, position, stream=None) -> None:
     """Device tensors: position[N] (int32) = new position of every old column."""
+    import torch
     nnz = int(col.numel())
+    _need(row_ptr, torch.int32, int(M) + 1, "row_ptr")
+    _need(col, torch.int32, nnz, "col")
+    _need(position, torch.int32, int(N), "position", exact=False)
     _check(lib().vcsrmc_rcm_order(_ptr(row_ptr), _ptr(col) if nnz else None, int(M), int(N), nnz,
                                   _ptr(position) if N else None, _stream_ptr(stream)),
            "rcm_column_order")
@@ -349,7 +361,15 @@ def rcm_order_device(row_ptr, col, M: int, N: int, position, stream=None) -> Non
 def apply_column_permutation_device(row_ptr, col, val, M: int, N: int, position, B=None,
                                     B_out=None, O: int = 0, stream=None) -> None:
     """Device tensors; col and val relabelled in place, B_out[position[r]] = B[r]."""
+    import torch
     nnz = int(col.numel())
+    _need(row_ptr, torch.int32, int(M) + 1, "row_ptr")
+    _need(col, torch.int32, nnz, "col")
+    _need(val, torch.float32, nnz, "val")
+    _need(position, torch.int32, int(N), "position", exact=False)
+    if B is not None:
+        _need(B, torch.float32, int(N) * int(O), "B", exact=False)
+        _need(B_out, torch.float32, int(N) * int(O), "B_out", exact=False)
     _check(lib().vcsrmc_apply_column_permutation(
         _ptr(row_ptr), _ptr(col) if nnz else None, _ptr(val) if nnz else None, int(M), int(N),
         nnz, _ptr(position) if N else None, _ptr(B), int(O), _ptr(B_out), _stream_ptr(stream)),
