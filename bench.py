@@ -160,11 +160,13 @@ def main():
     flops = 2.0 * A.nnz * O
     gflops = flops / (ms_per_step * 1e-3) / 1e9
 
-    # algorithmic bytes
-    s = 4 if fp32 else 2
+    # algorithmic bytes: A values and columns, row pointers, each distinct B row once (in the
+    # element type B is held in), each non-empty C row once
+    s_a = 4 if fp32 else 2
+    s_b = 4 if (fp32 or args.b_fp32) else 2
     U = int(np.unique(A.col).size)
     M_ne = int(np.count_nonzero(np.diff(A.row_ptr)))
-    bytes_alg = A.nnz * (s + 4) + (A.M + 1) * 4 + U * O * s + M_ne * O * 4
+    bytes_alg = A.nnz * (s_a + 4) + (A.M + 1) * 4 + U * O * s_b + M_ne * O * 4
     achieved_gbs = bytes_alg / (kernel_ms * 1e-3) / 1e9
     f_pad = info["num_groups"] * 2.0 * 16 * SEGW * O
     mfma_tflops = f_pad / (kernel_ms * 1e-3) / 1e12
