@@ -109,6 +109,19 @@ int vcsrmc_download(vcsrmc_t h, int *group_ptr, int *group_depth, int *group_seg
 int vcsrmc_spmm(vcsrmc_t h, const void *dB, int b_dtype, int O, int tileK, float *dC,
                 void *stream, float *ms);
 
+/* Flags of vcsrmc_spmm_ex. */
+#define VCSRMC_SPMM_OVERWRITE 1 /* C = A.B on the rows A touches, without reading C */
+
+/* vcsrmc_spmm with flags; flags = 0 is vcsrmc_spmm (C += A.B).  VCSRMC_SPMM_OVERWRITE writes
+ * C = A.B on every row that holds a nonzero of A and leaves the other rows as they are, so it
+ * never reads C: it equals zeroing C and calling vcsrmc_spmm, bit for bit (the reference's
+ * measured protocol, src/main.cpp:242-245), and saves the read of C.  Where a 16-row panel of A
+ * is split across work-groups (panels of very many 32-column tiles), its rows are first set to
+ * zero by a small kernel on `stream`.  No counterpart in the reference, whose kernels always
+ * accumulate into C with atomicAdd (src/vcsr_mc.cu:228-234). */
+int vcsrmc_spmm_ex(vcsrmc_t h, const void *dB, int b_dtype, int O, int tileK, float *dC,
+                   int flags, void *stream, float *ms);
+
 /* Reverse Cuthill-McKee order of the columns of a device CSR (row_ptr[M+1], col[nnz]; any
  * column order inside a row): d_position[N] receives the new position of every old column,
  * equal element for element to the reference's rcm_column_order, tie order included

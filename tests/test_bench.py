@@ -46,3 +46,30 @@ def test_bench_json_line():
     cpu = d["cpu_baseline"]
     assert cpu["kind"] == "port" and cpu["cores"] == 1 and cpu["value"] > 0 and cpu["sample"]
     assert d["parity_row_sample"] is True
+    (p,) = d["per_config"]
+    assert p["config"] == 1 and p["O"] == 128 and p["precision"] == "fp32"
+    for mode in ("accumulate", "overwrite"):
+        m = p[mode]
+        assert m["parity_row_sample"] is True
+        assert m["kernel_ms"] > 0 and m["single_launch_median_ms"] > 0
+        assert abs(m["roofline"]["achieved"] - p["bytes_alg"] / m["kernel_ms"] / 1e6) < \
+            1e-3 * m["roofline"]["achieved"] + 0.1
+        assert m["speedup_vs_rocsparse_fp32"] > 0
+    assert d["value"] == p["accumulate"]["gflops"]
+
+
+def test_traffic_stamp_matches_sources():
+    """The measured HBM traffic in profiles/ is stamped with the hash of the kernel and layout
+    sources it was profiled at; bench.py reports it only while that hash is current."""
+    sys.path.insert(0, ROOT)
+    import bench
+    import json
+    d = json.load(open(os.path.join(ROOT, "profiles", "hbm_traffic.json")))
+    assert set(d) >= {"sources_sha256_16", "launches"}
+    for key, e in d["launches"].items():
+        assert e["bytes"] > 0 and e["fetch_kib"] > 0 and e["write_kib"] >= 0, key
+    got, stamp = bench.measured_traffic("config2-fp16-accumulate")
+    if d["sources_sha256_16"] == bench.traffic_source_hash():
+        assert got == d["launches"]["config2-fp16-accumulate"]["bytes"]
+    else:
+        assert got is None and stamp.startswith("stale")

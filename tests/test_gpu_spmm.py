@@ -400,3 +400,115 @@ def test_graph_replay(fp32, b32):
             got, want = C.cpu().numpy(), ref.cpu().numpy()
             # split panels merge with atomics: only their order may differ
             assert np.allclose(got, want, rtol=1e-6, atol=1e-6), it
+
+
+def _split_rows(rp, c, M, N, light_max=1, heavy_tiles=64):
+    """Rows of the 16-row panels that the format cuts into several heavy units (a panel of
+    more than heavy_tiles 32-column tiles, for formats of fewer than 2048 panels)."""
+    rows = np.repeat(np.arange(M), np.diff(rp))
+    panel = rows // 16
+    keys = np.unique(panel.astype(np.int64) * (N + 1) + c)
+    tiles = (np.bincount(keys // (N + 1), minlength=(M + 15) // 16) + 31) // 32
+    split = np.nonzero((tiles > light_max) & (tiles > heavy_tiles))[0]
+    out = np.zeros(M, bool)
+    for p in split:
+        out[16 * p:16 * p + 16] = True
+    return out
+
+
+@pytest.mark.parametrize("fp32", [False, True])
+@pytest.mark.parametrize("tileK", [32, 128])
+@pytest.mark.parametrize("O", [7, 128])
+def test_overwrite_equals_zero_then_accumulate(orc, fp32, tileK, O):
+    """C = A.B (the overwrite flag, C never read) against C zeroed and C += A.B: bit for bit on
+    every row outside split panels; split panels (several units adding through atomics into
+    rows the launcher clears first) within the parity norm of the oracle.  Rows without
+    nonzeros keep what C held, bit for bit."""
+    import torch
+    rng = np.random.default_rng(31 + tileK + O + fp32)
+    M, N = 900, 5000
+    rp, c, v = random_csr(rng, M, N, density=0.001, heavy_rows=5, heavy_nnz=4000,
+                          empty_frac=0.3)
+    B = rng.uniform(-1, 1, (N, O)).astype(np.float32)
+    split = _split_rows(rp, c, M, N)
+    assert split.any()
+    say("overwrite vs accumulate", fp32, tileK, O)
+    with vm.DeviceFormat.from_device_csr(dev(rp), dev(c), dev(v), M, N, fp32, 32) as f:
+        dB = dev(B) if fp32 else dev(B).half()
+        Ca = torch.zeros((M, O), dtype=torch.float32, device="cuda")
+        f.spmm(dB, Ca, tileK=tileK)
+        C0 = rng.uniform(5, 6, (M, O)).astype(np.float32)
+        Co = dev(C0)
+        f.spmm(dB, Co, tileK=tileK, overwrite=True)
+        Co2 = Co.clone()
+        f.spmm(dB, Co2, tileK=tileK, overwrite=True)  # idempotent
+        torch.cuda.synchronize()
+        scale = f.info()["scale"]
+        Ca, Co, Co2 = Ca.cpu().numpy(), Co.cpu().numpy(), Co2.cpu().numpy()
+    empty = np.diff(rp) == 0
+    keep = ~split & ~empty
+    assert Co[keep].tobytes() == Ca[keep].tobytes()
+    assert Co2[keep].tobytes() == Ca[keep].tobytes()
+    assert Co[empty].tobytes() == C0[empty].tobytes()
+    R, L1 = orc.spmm_csr(rp, c, v, M, B, mode=0 if fp32 else 1, scale=scale)
+    for C in (Co, Co2):
+        ok, worst, row = row_l1_parity(C[~empty], R[~empty], L1[~empty], TAU[fp32])
+        assert ok, f"row {row}: {worst:.3g}"
+
+
+def test_overwrite_unaligned_c(orc):
+    """Overwrite with C not 16-byte aligned (scalar epilogue) and O not a multiple of 4."""
+    import torch
+    rng = np.random.default_rng(33)
+    M, N, O = 400, 300, 13
+    rp, c, v = random_csr(rng, M, N, density=0.02, empty_frac=0.2)
+    B = rng.uniform(-1, 1, (N, O)).astype(np.float32)
+    say("overwrite unaligned")
+    with vm.DeviceFormat.from_device_csr(dev(rp), dev(c), dev(v), M, N, True, 32) as f:
+        buf = torch.full((M * O + 1,), 3.0, dtype=torch.float32, device="cuda")
+        Cv = buf[1:]
+        f.spmm(dev(B), Cv, tileK=16, O=O, overwrite=True)
+        torch.cuda.synchronize()
+        got = Cv.cpu().numpy().reshape(M, O)
+    R, L1 = orc.spmm_csr(rp, c, v, M, B, mode=0)
+    empty = np.diff(rp) == 0
+    assert np.all(got[empty] == 3.0)
+    ok, worst, row = row_l1_parity(got[~empty], R[~empty], L1[~empty], TAU[True])
+    assert ok, f"row {row}: {worst:.3g}"
+
+
+@pytest.mark.parametrize("config", [1, 2, 4, 5])
+def test_workloads_full_size_overwrite(orc, config):
+    """Full benchmark sizes: the overwrite launch equals zero-then-accumulate bit for bit outside
+    split panels (R-MAT has a few), and a seeded sample of 2000 rows meets the parity norm."""
+    import torch
+    w = vm.WORKLOADS[config]
+    fp32 = w["precision"] == "fp32"
+    A = vm.generate(config, 0)
+    O = w["O"]
+    B = vm.dense(A.N, O, seed=vm.SEED_BASE + 100 + config, fp16_exact=not fp32)
+    say("full-size overwrite", config, A.M, A.nnz, O)
+    with vm.DeviceFormat.from_device_csr(dev(A.row_ptr), dev(A.col), dev(A.val), A.M, A.N,
+                                         fp32, 32) as f:
+        info = f.info()
+        dB = dev(B) if fp32 else dev(B).half()
+        Ca = torch.zeros((A.M, O), dtype=torch.float32, device="cuda")
+        f.spmm(dB, Ca, tileK=128)
+        Co = torch.full((A.M, O), 9.0, dtype=torch.float32, device="cuda")
+        f.spmm(dB, Co, tileK=128, overwrite=True)
+        torch.cuda.synchronize()
+        empty = torch.from_numpy(np.diff(A.row_ptr) == 0).cuda()
+        assert bool(torch.all(Co[empty] == 9.0))
+        if info["num_units"] == info["num_panels"]:  # no split panel
+            assert torch.equal(Co[~empty], Ca[~empty])
+        else:
+            assert bool(torch.allclose(Co[~empty], Ca[~empty], rtol=1e-5, atol=1e-5))
+        rows = np.sort(np.random.default_rng(config).choice(A.M, size=min(A.M, 2000),
+                                                            replace=False))
+        Cs = Co[torch.from_numpy(rows).cuda()].cpu().numpy()
+        scale = info["scale"]
+    srp, sc, sv = sub_csr(A.row_ptr, A.col, A.val, rows)
+    R, L1 = orc.spmm_csr(srp, sc, sv, len(rows), B, mode=0 if fp32 else 1, scale=scale)
+    ne = np.diff(srp) > 0
+    ok, worst, row = row_l1_parity(Cs[ne], R[ne], L1[ne], TAU[fp32])
+    assert ok, f"row {row}: {worst:.3g}"

@@ -31,6 +31,7 @@ BENCH_LIB_PATH = os.path.join(HERE, "libvcsrmc_bench.so")
 OK, ERR_ARG, ERR_SEGW, ERR_TILEK, ERR_CSR, ERR_UNSORTED, ERR_FORMAT, ERR_OVERFLOW, ERR_HIP, \
     ERR_STATE = range(10)
 B_F32, B_F16 = 0, 1
+SPMM_OVERWRITE = 1
 
 
 class VCSRMCError(RuntimeError):
@@ -72,6 +73,7 @@ def lib():
         L.vcsrmc_get_info.argtypes = [vp, C.POINTER(_Info)]
         L.vcsrmc_download.argtypes = [vp] + [vp] * 8
         L.vcsrmc_spmm.argtypes = [vp, vp, C.c_int, C.c_int, C.c_int, vp, vp, fp]
+        L.vcsrmc_spmm_ex.argtypes = [vp, vp, C.c_int, C.c_int, C.c_int, vp, C.c_int, vp, fp]
         L.vcsrmc_rcm_order.argtypes = [vp, vp, C.c_int, C.c_int, C.c_int, vp, vp]
         L.vcsrmc_apply_column_permutation.argtypes = [vp, vp, vp, C.c_int, C.c_int, C.c_int, vp,
                                                       vp, C.c_int, vp, vp]
@@ -80,7 +82,7 @@ def lib():
         L.vcsrmc_last_error.restype = C.c_char_p
         for f in ("vcsrmc_create", "vcsrmc_destroy", "vcsrmc_half_scale", "vcsrmc_build_csr",
                   "vcsrmc_upload", "vcsrmc_get_info", "vcsrmc_download", "vcsrmc_spmm",
-                  "vcsrmc_rcm_order", "vcsrmc_apply_column_permutation"):
+                  "vcsrmc_spmm_ex", "vcsrmc_rcm_order", "vcsrmc_apply_column_permutation"):
             getattr(L, f).restype = C.c_int
         _lib_handle = L
     return _lib_handle
@@ -271,9 +273,10 @@ class DeviceFormat:
                       num_segments=i["num_segments"], scale=float(np.float32(i["scale"])),
                       fp32=bool(i["fp32"]), **out)
 
-    def spmm(self, B, C_out, tileK=128, O=None, stream=None, timed=False):
-        """C_out += A . B on the GPU.  B: (N, O) float32 or float16 device tensor; C_out:
-        (M, O) float32.  Returns the event-timed kernel time in ms when timed, else None."""
+    def spmm(self, B, C_out, tileK=128, O=None, stream=None, timed=False, overwrite=False):
+        """C_out += A . B on the GPU (overwrite: C_out = A . B on the rows A touches, C_out
+        not read).  B: (N, O) float32 or float16 device tensor; C_out: (M, O) float32.
+        Returns the event-timed kernel time in ms when timed, else None."""
         import torch
         b_dtype = B_F16 if B.dtype == torch.float16 else B_F32
         if B.dtype not in (torch.float16, torch.float32) or C_out.dtype != torch.float32:
@@ -291,8 +294,9 @@ class DeviceFormat:
             raise VCSRMCError(ERR_ARG, f"B needs N x O = {N} x {O} and C M x O = {M} x {O} "
                                        f"elements; got {B.numel()} and {C_out.numel()}")
         ms = C.c_float(0.0)
-        _check(lib().vcsrmc_spmm(self.handle, _ptr(B), b_dtype, O, int(tileK), _ptr(C_out),
-                                 _stream_ptr(stream), C.byref(ms) if timed else None),
+        _check(lib().vcsrmc_spmm_ex(self.handle, _ptr(B), b_dtype, O, int(tileK), _ptr(C_out),
+                                    SPMM_OVERWRITE if overwrite else 0, _stream_ptr(stream),
+                                    C.byref(ms) if timed else None),
                "vcsrmc_spmm")
         return ms.value if timed else None
 

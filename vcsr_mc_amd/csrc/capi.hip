@@ -186,13 +186,20 @@ int vcsrmc_download(vcsrmc_t h, int* group_ptr, int* group_depth, int* group_seg
 
 int vcsrmc_spmm(vcsrmc_t h, const void* dB, int b_dtype, int O, int tileK, float* dC,
                 void* stream, float* ms) {
+    return vcsrmc_spmm_ex(h, dB, b_dtype, O, tileK, dC, 0, stream, ms);
+}
+
+int vcsrmc_spmm_ex(vcsrmc_t h, const void* dB, int b_dtype, int O, int tileK, float* dC,
+                   int flags, void* stream, float* ms) {
     return guarded([&] {
         need(h != nullptr, "null handle");
         need(b_dtype == VCSRMC_B_F32 || b_dtype == VCSRMC_B_F16, "unknown B dtype");
+        need((flags & ~VCSRMC_SPMM_OVERWRITE) == 0, "unknown flag");
+        const bool accumulate = !(flags & VCSRMC_SPMM_OVERWRITE);
         DeviceScope ds(h->device);
         hipStream_t st = (hipStream_t)stream;
         if (!ms) {
-            vcsrmc::spmm_launch(h->F, dB, b_dtype == VCSRMC_B_F16, O, tileK, dC, st);
+            vcsrmc::spmm_launch(h->F, dB, b_dtype == VCSRMC_B_F16, O, tileK, dC, accumulate, st);
             return;
         }
         hipEvent_t t0, t1;
@@ -200,7 +207,7 @@ int vcsrmc_spmm(vcsrmc_t h, const void* dB, int b_dtype, int O, int tileK, float
         VCSRMC_HIP(hipEventCreate(&t1));
         try {
             VCSRMC_HIP(hipEventRecord(t0, st));
-            vcsrmc::spmm_launch(h->F, dB, b_dtype == VCSRMC_B_F16, O, tileK, dC, st);
+            vcsrmc::spmm_launch(h->F, dB, b_dtype == VCSRMC_B_F16, O, tileK, dC, accumulate, st);
             VCSRMC_HIP(hipEventRecord(t1, st));
             VCSRMC_HIP(hipEventSynchronize(t1));
             VCSRMC_HIP(hipEventElapsedTime(ms, t0, t1));

@@ -12,6 +12,7 @@
 //   6. work items: runs of <= chunk groups of one segment, stable sort by work, descending
 // Part 2 derives the execution layout read by the multiply kernels (16-row panels cut into
 // compacted 32-column tiles; see internal.hpp) from the same nonzeros.
+#include <algorithm>
 #include <climits>
 #include <cmath>
 #include <cstring>
@@ -368,23 +369,28 @@ __global__ void k_dense_fill(const uint32_t* __restrict__ entries,
 }
 
 // Units.  A panel with at most `light_max` tiles is one light unit (one wave); a larger panel
-// is cut into heavy units of at most kHeavyTiles tiles (the waves of a work-group share them).
+// is cut into heavy units of at most `heavy_tiles` tiles (the waves of a work-group share them).
+// nsplit[j] = 1 for a panel cut into several units.
 __global__ void k_units_per_panel(const int* __restrict__ nch, int NP, int light_max,
-                                  int* __restrict__ nu, int* __restrict__ nheavy) {
+                                  int heavy_tiles, int* __restrict__ nu, int* __restrict__ nheavy,
+                                  int* __restrict__ nsplit) {
     const long long j = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     if (j >= NP) return;
     const bool heavy = nch[j] > light_max;
-    const int n = heavy ? (nch[j] + kHeavyTiles - 1) / kHeavyTiles : 1;
+    const int n = heavy ? (nch[j] + heavy_tiles - 1) / heavy_tiles : 1;
     nu[j] = n;
     nheavy[j] = heavy ? n : 0;
+    nsplit[j] = n > 1;
 }
 
 // Writes the units of panel j (in panel order) with their schedule keys: heavy units first,
 // larger first; then light units in panel order (the stable sort keeps it), so that the
 // contiguous range of light units an XCD walks holds neighbouring panels.
+// The first unit of a split panel also carries kUnitSplitFirst (it clears the panel's rows before
+// an overwriting launch, see spmm_launch).
 __global__ void k_make_units(const int* __restrict__ cbase, const int* __restrict__ ubase,
                              const int* __restrict__ ppanel, const int* __restrict__ pmask,
-                             const int* __restrict__ nch, int NP, int light_max,
+                             const int* __restrict__ nch, int NP, int light_max, int heavy_tiles,
                              int4* __restrict__ units, uint32_t* __restrict__ key,
                              uint32_t* __restrict__ pay) {
     const long long j = (long long)blockIdx.x * blockDim.x + threadIdx.x;
@@ -392,12 +398,14 @@ __global__ void k_make_units(const int* __restrict__ cbase, const int* __restric
     const int c0 = cbase[j], c1 = cbase[j + 1];
     const int u0 = ubase[j], nu = ubase[j + 1] - u0;
     const bool heavy = nch[j] > light_max;
-    const int split = nu > 1 ? (1 << 16) : 0;
-    const int step = heavy ? kHeavyTiles : (c1 - c0);
+    const int split = nu > 1 ? kUnitSplit : 0;
+    const int step = heavy ? heavy_tiles : (c1 - c0);
     for (int u = 0; u < nu; ++u) {
         const int cb = c0 + u * step;
         const int ce = min(cb + step, c1);
-        units[u0 + u] = make_int4(ppanel[j] * kPanelRows, cb, ce, (pmask[j] & 0xffff) | split);
+        const int first = (split && u == 0) ? kUnitSplitFirst : 0;
+        units[u0 + u] =
+            make_int4(ppanel[j] * kPanelRows, cb, ce, (pmask[j] & 0xffff) | split | first);
         key[u0 + u] = heavy ? (uint32_t)(0xffff - min(ce - cb, 0xffff)) : (1u << 16);
         pay[u0 + u] = (uint32_t)(u0 + u);
     }
@@ -464,6 +472,16 @@ static void check_err(const int* d_err, hipStream_t st) {
 // 2% faster than 7 or 8 on the power-law matrix; 4 starves the stencil of waves and slows the
 // power-law one by 6%, 16 leaves R-MAT with long single-wave units).
 static int light_tile_limit(int num_panels) { return num_panels >= kFewPanels ? 6 : 1; }
+
+// Largest heavy unit.  Heavy units run first, larger first, each on the four waves of one
+// work-group, while the GPU holds about 3072 waves (1024 SIMDs, three waves each); a unit of
+// up to 1/1024 of all tiles gives each of its waves at most 3/4 of the average wave's share, so
+// it ends before the launch does.  Smaller launches keep units of kHeavyTiles, which split the
+// few large panels of a short launch across work-groups.  Every cut makes the panel's units
+// merge in C through atomics.
+static int heavy_tile_limit(int num_chunks) {
+    return std::max(kHeavyTiles, std::min(num_chunks / 1024, 0xffff));
+}
 
 template <typename K>
 static void build_exec_layout_k(DeviceFormat& F, const int* trow, const int* tcol,
@@ -534,17 +552,20 @@ static void build_exec_layout_k(DeviceFormat& F, const int* trow, const int* tco
     }
 
     const int light_max = light_tile_limit(NP);
-    DevBuf<int> nu(NP), ubase(NP + 1), nheavy(NP), hbase(NP + 1);
-    LAUNCH(k_units_per_panel, NP, nch.p, NP, light_max, nu.p, nheavy.p);
+    const int heavy_tiles = heavy_tile_limit(NC);
+    DevBuf<int> nu(NP), ubase(NP + 1), nheavy(NP), hbase(NP + 1), nsplit(NP), sbase(NP + 1);
+    LAUNCH(k_units_per_panel, NP, nch.p, NP, light_max, heavy_tiles, nu.p, nheavy.p, nsplit.p);
     exclusive_sum<int, int>(nu.p, ubase.p, NP, st);
     exclusive_sum<int, int>(nheavy.p, hbase.p, NP, st);
+    exclusive_sum<int, int>(nsplit.p, sbase.p, NP, st);
     const int NU = read_scalar(ubase.p + NP, st);
     const int NH = read_scalar(hbase.p + NP, st);
+    const int NS = read_scalar(sbase.p + NP, st);
     {
         DevBuf<int4> raw(NU);
         DevBuf<uint32_t> k1(NU), k2(NU), v1(NU), v2(NU);
-        LAUNCH(k_make_units, NP, cbase.p, ubase.p, ppanel.p, pmask.p, nch.p, NP, light_max, raw.p,
-               k1.p, v1.p);
+        LAUNCH(k_make_units, NP, cbase.p, ubase.p, ppanel.p, pmask.p, nch.p, NP, light_max,
+               heavy_tiles, raw.p, k1.p, v1.p);
         uint32_t *kp2 = k1.p, *ka2 = k2.p, *vp2 = v1.p, *va2 = v2.p;
         radix_sort_pairs<uint32_t>(kp2, vp2, ka2, va2, NU, 17, st);
         F.units.alloc(NU);
@@ -566,7 +587,9 @@ static void build_exec_layout_k(DeviceFormat& F, const int* trow, const int* tco
     F.num_chunks = NC;
     F.num_units = NU;
     F.num_heavy = NH;
+    F.num_split_panels = NS;
     F.light_max = light_max;
+    F.heavy_tiles = heavy_tiles;
 }
 
 static void build_exec_layout(DeviceFormat& F, const int* trow, const int* tcol, const float* tval,

@@ -15,8 +15,12 @@ constexpr int kChunkCols = 32;
 constexpr int kPanelRows = 16;
 // A tile holding more nonzeros than this (of 16 x 32) is also stored dense.
 constexpr int kDenseMin = 192;
-// Tiles per heavy unit (shared by the kWaves waves of one work-group).
+// Fewest tiles a heavy unit may be cut to (shared by the kWaves waves of one work-group); large
+// launches use larger units (format_build.hip, heavy_tile_limit).
 constexpr int kHeavyTiles = 64;
+// Flag bits of units[u].w above the 16-bit row mask.
+constexpr int kUnitSplit = 1 << 16;       // the panel has several units (merge through atomics)
+constexpr int kUnitSplitFirst = 1 << 17;  // ... and this is its first unit
 constexpr int kWaves = 4;
 
 // Light-unit ranges per XCD, passed to the multiply kernels by value.
@@ -32,9 +36,10 @@ struct XcdSplit {
 // item_gend.
 //
 // Execution layout (what the multiply kernels read), derived from the same matrix:
-//   units[u]        = {row0, chunk_begin, chunk_end, rowmask | split << 16}
-//                     a run of chunks of one 16-row panel; split = the panel has several
-//                     units, whose partial sums meet in C through atomics.  The first
+//   units[u]        = {row0, chunk_begin, chunk_end, rowmask | flags}
+//                     a run of chunks of one 16-row panel; kUnitSplit = the panel has several
+//                     units, whose partial sums meet in C through atomics, kUnitSplitFirst =
+//                     the first of them.  The first
 //                     num_heavy units are heavy (one work-group each, larger first), the rest
 //                     light (one wave each, four per work-group, in panel order; XCD x runs
 //                     the range starting at xcd_start[x], cut for equal tile counts).
@@ -64,6 +69,8 @@ struct DeviceFormat {
     DevBuf<float> val;
 
     int num_panels = 0, num_chunks = 0, num_units = 0, num_heavy = 0, light_max = 0;
+    int heavy_tiles = 0;       // largest heavy unit, in tiles
+    int num_split_panels = 0;  // panels cut into several units
     // Light units [num_heavy + xcd_start[x], num_heavy + xcd_start[x + 1]) run on XCD x.
     int xcd_start[9] = {0, 0, 0, 0, 0, 0, 0, 0, 0};
     DevBuf<int4> units;
@@ -104,8 +111,9 @@ struct HostArrays {
 void build_from_host(DeviceFormat& F, const HostArrays& H, hipStream_t st);
 
 // C += A.B (src/vcsr_mc.cu:352-394 semantics).  b_f16: B is binary16 in HBM.
+// accumulate: C += A.B; otherwise C = A.B on the rows A touches (other rows untouched).
 void spmm_launch(const DeviceFormat& F, const void* dB, bool b_f16, int O, int tileK, float* dC,
-                 hipStream_t st);
+                 bool accumulate, hipStream_t st);
 
 // Reverse Cuthill-McKee order of the columns of a device CSR (include/reorder.hpp:17-77):
 // position[old column] = new column.  Synchronises `st`.

@@ -121,11 +121,13 @@ struct CAhead {
 
 template <int TK, int W>
 __device__ __forceinline__ void read_c_ahead(CAhead<TK, W>& ca, const int4& U, int k0, int O,
-                                             bool c4, const float* __restrict__ C) {
+                                             bool c4, bool accumulate,
+                                             const float* __restrict__ C) {
     constexpr int VEC = TK / 16;
     constexpr int N = CAhead<TK, W>::N;
     const int lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
-    const bool ok = c4 && !((U.w >> 16) & 1);
+    // Overwrite launches (C = A.B) read zeros instead of C; split panels merge through atomics.
+    const bool ok = c4 && accumulate && !(U.w & kUnitSplit);
     const long long OL = O;
     if constexpr (W == 1) {
         if constexpr (N > 0) {
@@ -162,11 +164,11 @@ __device__ __forceinline__ void read_c_ahead(CAhead<TK, W>& ca, const int4& U, i
 template <int TK, int W>
 __device__ __forceinline__ void merge_into_c(const floatx4 (&acc)[TK / 16], float scale,
                                              const int4& U, int k0, int O, bool c4,
-                                             float* __restrict__ C, float* P,
+                                             bool accumulate, float* __restrict__ C, float* P,
                                              const CAhead<TK, W>& ca) {
     constexpr int VEC = TK / 16;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, n = lane & 15, g = lane >> 4;
-    const bool split = (U.w >> 16) & 1;
+    const bool split = U.w & kUnitSplit;
     const long long OL = O;
     if constexpr (W == 1) {
         const int c0 = k0 + VEC * n;
@@ -190,7 +192,7 @@ __device__ __forceinline__ void merge_into_c(const floatx4 (&acc)[TK / 16], floa
             } else {
 #pragma unroll
                 for (int q = 0; q < VEC; ++q)
-                    if (c0 + q < O) crow[q] += acc[q][i] * scale;
+                    if (c0 + q < O) crow[q] = (accumulate ? crow[q] : 0.0f) + acc[q][i] * scale;
             }
         }
     } else {
@@ -226,7 +228,7 @@ __device__ __forceinline__ void merge_into_c(const floatx4 (&acc)[TK / 16], floa
             } else {
 #pragma unroll
                 for (int jj = 0; jj < 4; ++jj)
-                    if (cc + jj < O) crow[jj] += sum[jj] * scale;
+                    if (cc + jj < O) crow[jj] = (accumulate ? crow[jj] : 0.0f) + sum[jj] * scale;
             }
         }
     }
@@ -399,7 +401,7 @@ __global__ __launch_bounds__(64 * kWaves, (f16_min_waves<TB, ALIGNED>())) void k
     const int* __restrict__ chunk_eptr, const int* __restrict__ chunk_cols,
     const int* __restrict__ chunk_dense, const uint32_t* __restrict__ entries,
     const _Float16* __restrict__ dense_a, const TB* __restrict__ B, int O, float scale, bool c4,
-    float* __restrict__ C) {
+    bool accumulate, float* __restrict__ C) {
     constexpr int VEC = TK / 16;
     __shared__ __attribute__((aligned(16))) _Float16 As[kWaves][16 * kApitch];
     __shared__ __attribute__((aligned(16))) float P[kWaves * 16 * TK];
@@ -420,17 +422,17 @@ __global__ __launch_bounds__(64 * kWaves, (f16_min_waves<TB, ALIGNED>())) void k
     // counting sees one fixed sequence of loads on each.
     if (heavy) {
         CAhead<TK, kWaves> ca;
-        read_c_ahead<TK, kWaves>(ca, U, k0, O, c4, C);
+        read_c_ahead<TK, kWaves>(ca, U, k0, O, c4, accumulate, C);
         tiles_f16<TK, TB, ALIGNED>(U.y + wave, U.z, kWaves, lane, n, g, c0, (long long)O,
                                    chunk_eptr, chunk_cols, chunk_dense, entries, dense_a, B,
                                    As[wave], acc, [] {});
-        merge_into_c<TK, kWaves>(acc, scale, U, k0, O, c4, C, P, ca);
+        merge_into_c<TK, kWaves>(acc, scale, U, k0, O, c4, accumulate, C, P, ca);
     } else {
         CAhead<TK, 1> ca;
         tiles_f16<TK, TB, ALIGNED>(U.y, U.z, 1, lane, n, g, c0, (long long)O, chunk_eptr,
                                    chunk_cols, chunk_dense, entries, dense_a, B, As[wave], acc,
-                                   [&] { read_c_ahead<TK, 1>(ca, U, k0, O, c4, C); });
-        merge_into_c<TK, 1>(acc, scale, U, k0, O, c4, C, P, ca);
+                                   [&] { read_c_ahead<TK, 1>(ca, U, k0, O, c4, accumulate, C); });
+        merge_into_c<TK, 1>(acc, scale, U, k0, O, c4, accumulate, C, P, ca);
     }
 }
 
@@ -638,7 +640,7 @@ __global__ __launch_bounds__(64 * kWaves, 3) void k_spmm_f32(
     const int* __restrict__ chunk_eptr, const int* __restrict__ chunk_cols,
     const int* __restrict__ chunk_dense, const uint32_t* __restrict__ entries,
     const float* __restrict__ dense_a, const float* __restrict__ B, int O, bool c4,
-    float* __restrict__ C) {
+    bool accumulate, float* __restrict__ C) {
     constexpr int VEC = TK / 16;
     __shared__ __attribute__((aligned(16))) float At[kWaves][4 * kAgroup32];
     __shared__ __attribute__((aligned(16))) float P[kWaves * 16 * TK];
@@ -655,22 +657,22 @@ __global__ __launch_bounds__(64 * kWaves, 3) void k_spmm_f32(
     for (int q = 0; q < VEC; ++q) acc[q] = floatx4{0.f, 0.f, 0.f, 0.f};
     if (heavy) {
         CAhead<TK, kWaves> ca;
-        read_c_ahead<TK, kWaves>(ca, U, k0, O, c4, C);
+        read_c_ahead<TK, kWaves>(ca, U, k0, O, c4, accumulate, C);
         tiles_f32<TK, ALIGNED>(U.y + wave, U.z, kWaves, lane, n, g, c0, (long long)O, chunk_eptr,
                                chunk_cols, chunk_dense, entries, dense_a, B, At[wave], acc, [] {});
-        merge_into_c<TK, kWaves>(acc, 1.0f, U, k0, O, c4, C, P, ca);
+        merge_into_c<TK, kWaves>(acc, 1.0f, U, k0, O, c4, accumulate, C, P, ca);
     } else {
         CAhead<TK, 1> ca;
         tiles_f32<TK, ALIGNED>(U.y, U.z, 1, lane, n, g, c0, (long long)O, chunk_eptr, chunk_cols,
                                chunk_dense, entries, dense_a, B, At[wave], acc,
-                               [&] { read_c_ahead<TK, 1>(ca, U, k0, O, c4, C); });
-        merge_into_c<TK, 1>(acc, 1.0f, U, k0, O, c4, C, P, ca);
+                               [&] { read_c_ahead<TK, 1>(ca, U, k0, O, c4, accumulate, C); });
+        merge_into_c<TK, 1>(acc, 1.0f, U, k0, O, c4, accumulate, C, P, ca);
     }
 }
 
 template <int TK>
 static void launch_tk(const DeviceFormat& F, const void* dB, bool b_f16, int O, float* dC,
-                      hipStream_t st) {
+                      bool accumulate, hipStream_t st) {
     constexpr int VEC = TK / 16;
     // Vector loads of B need O % VEC == 0 and a 16-byte aligned base.
     const bool aligned = (O % VEC) == 0 && ((uintptr_t)dB % 16) == 0;
@@ -696,36 +698,54 @@ static void launch_tk(const DeviceFormat& F, const void* dB, bool b_f16, int O, 
         if (aligned)
             hipLaunchKernelGGL((k_spmm_f32<TK, true>), grid, block, 0, st, F.units.p, NH, xs,
                                F.chunk_eptr.p, F.chunk_cols.p, F.chunk_dense.p, F.entries.p,
-                               F.dense_a32.p, B, O, c4, dC);
+                               F.dense_a32.p, B, O, c4, accumulate, dC);
         else
             hipLaunchKernelGGL((k_spmm_f32<TK, false>), grid, block, 0, st, F.units.p, NH, xs,
                                F.chunk_eptr.p, F.chunk_cols.p, F.chunk_dense.p, F.entries.p,
-                               F.dense_a32.p, B, O, c4, dC);
+                               F.dense_a32.p, B, O, c4, accumulate, dC);
     } else if (b_f16) {
         const _Float16* B = static_cast<const _Float16*>(dB);
         if (aligned)
             hipLaunchKernelGGL((k_spmm_f16<TK, _Float16, true>), grid, block, 0, st, F.units.p, NH,
                                xs, F.chunk_eptr.p, F.chunk_cols.p, F.chunk_dense.p, F.entries.p,
-                               F.dense_a16.p, B, O, F.scale, c4, dC);
+                               F.dense_a16.p, B, O, F.scale, c4, accumulate, dC);
         else
             hipLaunchKernelGGL((k_spmm_f16<TK, _Float16, false>), grid, block, 0, st, F.units.p, NH,
                                xs, F.chunk_eptr.p, F.chunk_cols.p, F.chunk_dense.p, F.entries.p,
-                               F.dense_a16.p, B, O, F.scale, c4, dC);
+                               F.dense_a16.p, B, O, F.scale, c4, accumulate, dC);
     } else if constexpr (TK <= 64) {
         const float* B = static_cast<const float*>(dB);
         if (aligned)
             hipLaunchKernelGGL((k_spmm_f16<TK, float, true>), grid, block, 0, st, F.units.p, NH,
                                xs, F.chunk_eptr.p, F.chunk_cols.p, F.chunk_dense.p, F.entries.p,
-                               F.dense_a16.p, B, O, F.scale, c4, dC);
+                               F.dense_a16.p, B, O, F.scale, c4, accumulate, dC);
         else
             hipLaunchKernelGGL((k_spmm_f16<TK, float, false>), grid, block, 0, st, F.units.p, NH,
                                xs, F.chunk_eptr.p, F.chunk_cols.p, F.chunk_dense.p, F.entries.p,
-                               F.dense_a16.p, B, O, F.scale, c4, dC);
+                               F.dense_a16.p, B, O, F.scale, c4, accumulate, dC);
     } else {
         // o_tile_width never gives an FP16 format reading FP32 B an O tile of 128.
         throw Error(VCSRMC_ERR_STATE, "no O tile of 128 for FP32 B with an FP16 format");
     }
     VCSRMC_HIP(hipGetLastError());
+}
+
+// Before an overwriting launch (C = A.B), the rows of every split panel are set to zero: their
+// units add into them through atomics.  One work-group per heavy unit; only a panel's first unit
+// (kUnitSplitFirst) writes, its masked rows over columns [0, O).
+__global__ __launch_bounds__(256) void k_zero_split_rows(const int4* __restrict__ units,
+                                                         int num_heavy, int O,
+                                                         float* __restrict__ C) {
+    const int u = blockIdx.x;
+    if (u >= num_heavy) return;
+    const int4 U = units[u];
+    if (!(U.w & kUnitSplitFirst)) return;
+    const long long OL = O;
+    for (int r = 0; r < kPanelRows; ++r) {
+        if (!((U.w >> r) & 1)) continue;
+        float* row = C + (long long)(U.x + r) * OL;
+        for (int c = threadIdx.x; c < O; c += 256) row[c] = 0.0f;
+    }
 }
 
 // B (n floats) to binary16, round to nearest even -- the conversion the FP16 kernel applies to
@@ -774,7 +794,7 @@ static int o_tile_width(const DeviceFormat& F, bool b_f16, int O, int tileK) {
 }
 
 void spmm_launch(const DeviceFormat& F, const void* dB, bool b_f16, int O, int tileK, float* dC,
-                 hipStream_t st) {
+                 bool accumulate, hipStream_t st) {
     if (tileK != 16 && tileK != 32 && tileK != 64 && tileK != 128)
         throw Error(VCSRMC_ERR_TILEK, "vcsr_mc supports tileK in {16, 32, 64, 128}");
     if (!F.ready) throw Error(VCSRMC_ERR_STATE, "no format in this handle");
@@ -810,11 +830,16 @@ void spmm_launch(const DeviceFormat& F, const void* dB, bool b_f16, int O, int t
         dB = F.b_half.p;
         b_f16 = true;
     }
+    if (!accumulate && F.num_split_panels > 0) {
+        hipLaunchKernelGGL(k_zero_split_rows, dim3((unsigned)F.num_heavy), dim3(256), 0, st,
+                           F.units.p, F.num_heavy, O, dC);
+        VCSRMC_HIP(hipGetLastError());
+    }
     switch (o_tile_width(F, b_f16, O, tileK)) {
-        case 16: launch_tk<16>(F, dB, b_f16, O, dC, st); break;
-        case 32: launch_tk<32>(F, dB, b_f16, O, dC, st); break;
-        case 64: launch_tk<64>(F, dB, b_f16, O, dC, st); break;
-        default: launch_tk<128>(F, dB, b_f16, O, dC, st); break;
+        case 16: launch_tk<16>(F, dB, b_f16, O, dC, accumulate, st); break;
+        case 32: launch_tk<32>(F, dB, b_f16, O, dC, accumulate, st); break;
+        case 64: launch_tk<64>(F, dB, b_f16, O, dC, accumulate, st); break;
+        default: launch_tk<128>(F, dB, b_f16, O, dC, accumulate, st); break;
     }
 }
 
