@@ -57,3 +57,24 @@ def test_no_oracle_in_product():
         assert "oracle" not in deps
         syms = subprocess.run(["nm", "-D", path], capture_output=True, text=True).stdout
         assert "orc_" not in syms and "ref_build" not in syms
+
+
+@pytest.mark.parametrize("field,delta", [("group_ptr", -1), ("group_seg_base", 1),
+                                          ("group_rows", -16), ("lcol", -1), ("item_gend", 1)])
+def test_upload_refuses_short_arrays_without_gpu(field, delta):
+    """from_host_format checks every array length against the sizes the format implies before a
+    handle exists or anything is copied (the C ABI reads those sizes from each pointer)."""
+    import numpy as np
+
+    import vcsr_mc_amd as vm
+    G, nval, ni = 2, 64, 1
+    V = vm.VCSRMC(M=32, N=32, segw=16, num_segments=2,
+                  group_ptr=np.array([0, 32, 64], np.int32), group_depth=np.array([2, 2], np.int32),
+                  group_seg_base=np.zeros(G, np.int32), group_rows=np.zeros(16 * G, np.int32),
+                  lcol=np.zeros(nval, np.int32), val=np.zeros(nval, np.float32),
+                  item_gbeg=np.zeros(ni, np.int32), item_gend=np.ones(ni, np.int32))
+    a = getattr(V, field)
+    setattr(V, field, np.zeros(len(a) + delta, np.int32))
+    with pytest.raises(vm.VCSRMCError) as e:
+        vm.DeviceFormat.from_host_format(V)
+    assert e.value.status == vm.ERR_FORMAT and field in str(e.value)

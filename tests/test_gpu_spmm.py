@@ -512,3 +512,37 @@ def test_workloads_full_size_overwrite(orc, config):
     ne = np.diff(srp) > 0
     ok, worst, row = row_l1_parity(Cs[ne], R[ne], L1[ne], TAU[fp32])
     assert ok, f"row {row}: {worst:.3g}"
+
+
+def test_failed_conversion_allocation_leaves_handle_usable(orc):
+    """An FP16 format given FP32 B converts B into a buffer its handle allocates on first use.
+    When that allocation fails (N x O binary16 values far beyond the GPU's memory; nothing is
+    launched, since the conversion follows the allocation) the call returns the HIP error and
+    the handle stays usable: the next call allocates again and meets the parity norm."""
+    import torch
+    rng = np.random.default_rng(51)
+    M = N = 2000
+    rp, c, v = random_csr(rng, M, N, nnz_per_row=16)
+    assert len(c) >= 12 * N  # with B above 256 MB the launcher converts
+    O_huge = 2**31 - 1
+    total = torch.cuda.get_device_properties(0).total_memory
+    assert N * O_huge * 2 > 10 * total
+    O = 128
+    B = rng.uniform(-1, 1, (N, O)).astype(np.float32)
+    say("failed conversion allocation")
+    with vm.DeviceFormat.from_device_csr(dev(rp), dev(c), dev(v), M, N, False, 32) as f:
+        dB = dev(B)
+        C = torch.zeros((M, O), dtype=torch.float32, device="cuda")
+        stream = int(torch.cuda.current_stream().cuda_stream)
+        rc = vm.lib().vcsrmc_spmm(f.handle, dB.data_ptr(), vm.B_F32, O_huge, 128, C.data_ptr(),
+                                  stream, None)
+        assert rc == vm.ERR_HIP and b"hipMalloc" in vm.lib().vcsrmc_last_error()
+        torch.cuda.synchronize()
+        assert bool(torch.all(C == 0))
+        f.spmm(dB, C, tileK=128)
+        torch.cuda.synchronize()
+        Cn = C.cpu().numpy()
+        scale = f.info()["scale"]
+    R, L1 = orc.spmm_csr(rp, c, v, M, B, mode=1, scale=scale)
+    ok, worst, row = row_l1_parity(Cn, R, L1, TAU[False])
+    assert ok, f"row {row}: {worst:.3g}"

@@ -239,16 +239,26 @@ class DeviceFormat:
 
     @classmethod
     def from_host_format(cls, V: VCSRMC, stream=None):
-        f = cls()
+        """Uploads caller-held format arrays.  Their lengths are checked against the sizes they
+        imply (G = len(group_depth), nval = len(val), items = len(item_gbeg)) before anything
+        is copied: the C ABI reads exactly those sizes from each pointer."""
         arrs = {}
         for name in _FMT_ARRAYS:
             dt = np.float32 if name == "val" else np.int32
             a = np.ascontiguousarray(getattr(V, name), dtype=dt)
             arrs[name] = a
         G = len(arrs["group_depth"])
+        nval, ni = len(arrs["val"]), len(arrs["item_gbeg"])
+        want = {"group_ptr": G + 1, "group_seg_base": G, "group_rows": 16 * G, "lcol": nval,
+                "item_gend": ni}
+        for name, n in want.items():
+            if len(arrs[name]) != n:
+                raise VCSRMCError(ERR_FORMAT, f"{name} holds {len(arrs[name])} entries; the "
+                                              f"format's sizes need {n}")
+        f = cls()
         _check(lib().vcsrmc_upload(
             f.handle, int(V.M), int(V.N), int(V.segw), int(V.bundle), int(V.num_segments), G,
-            len(arrs["val"]), len(arrs["item_gbeg"]),
+            nval, ni,
             *[(arrs[n].ctypes.data if arrs[n].size else None) for n in _FMT_ARRAYS],
             float(V.scale), int(bool(V.fp32)), _stream_ptr(stream)), "vcsrmc_upload")
         return f

@@ -125,20 +125,36 @@ __global__ void k_emit_pairs(const int* __restrict__ head, const int* __restrict
 
 template <typename K>
 __global__ void k_pair_keys(const int* __restrict__ pstart, const int* __restrict__ col, int P,
-                            int segw, K* __restrict__ key, uint32_t* __restrict__ pay,
-                            int* __restrict__ seg_n) {
+                            int segw, K* __restrict__ key, uint32_t* __restrict__ pay) {
     const long long q = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     if (q >= P) return;
     const int cnt = pstart[q + 1] - pstart[q];
     const int seg = col[pstart[q]] / segw;
     key[q] = ((K)seg << 6) | (K)(segw - cnt);
     pay[q] = (uint32_t)q;
-    atomicAdd(&seg_n[seg], 1);
 }
 
-__global__ void k_groups_per_seg(const int* __restrict__ seg_n, int S, int* __restrict__ gnum) {
+// seg_start[s] = first sorted pair of segment s or later (s = 0..S; seg_start[S] = P): a lower
+// bound over the sorted keys, one thread per segment.
+template <typename K>
+__global__ void k_seg_starts(const K* __restrict__ skey, int P, int S,
+                             int* __restrict__ seg_start) {
     const long long s = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (s < S) gnum[s] = (seg_n[s] + 15) / 16;
+    if (s > S) return;
+    const K want = (K)s << 6;
+    int lo = 0, hi = P;
+    while (lo < hi) {
+        const int mid = (int)(((unsigned)lo + (unsigned)hi) >> 1);
+        if (skey[mid] < want) lo = mid + 1;
+        else hi = mid;
+    }
+    seg_start[s] = lo;
+}
+
+__global__ void k_groups_per_seg(const int* __restrict__ seg_start, int S,
+                                 int* __restrict__ gnum) {
+    const long long s = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (s < S) gnum[s] = (seg_start[s + 1] - seg_start[s] + 15) / 16;
 }
 
 template <typename K>
@@ -308,8 +324,7 @@ __global__ void k_panel_entries(const K* __restrict__ skey, const uint32_t* __re
                                 const int* __restrict__ cbase, const int* __restrict__ tcol,
                                 const float* __restrict__ tval, long long n,
                                 uint32_t* __restrict__ entries, int* __restrict__ chunk_cols,
-                                int* __restrict__ chunk_eptr,
-                                int* __restrict__ pmask, int* __restrict__ echunk) {
+                                int* __restrict__ chunk_eptr, int* __restrict__ echunk) {
     const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
     const int j = pin[i] - 1;
@@ -335,7 +350,26 @@ __global__ void k_panel_entries(const K* __restrict__ skey, const uint32_t* __re
         chunk_cols[(long long)c * kChunkCols + slot] = tcol[src];
         if (k == 0) chunk_eptr[c] = (int)i;
     }
-    atomicOr(&pmask[j], 1 << r16);
+}
+
+// rflag[r] = 1 for every row holding a nonzero (plain stores; every writer stores the same 1).
+__global__ void k_row_flags(const int* __restrict__ trow, long long n,
+                            unsigned char* __restrict__ rflag) {
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) rflag[trow[i]] = 1;
+}
+
+// pmask[j] = the non-empty rows of panel j, from its 16 row flags (one 16-byte load).
+__global__ void k_panel_masks(const unsigned char* __restrict__ rflag,
+                              const int* __restrict__ ppanel, int NP, int* __restrict__ pmask) {
+    const long long j = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= NP) return;
+    const uint4 w = *reinterpret_cast<const uint4*>(rflag + (long long)ppanel[j] * kPanelRows);
+    const uint32_t words[4] = {w.x, w.y, w.z, w.w};
+    int m = 0;
+#pragma unroll
+    for (int b = 0; b < 16; ++b) m |= ((words[b >> 2] >> (8 * (b & 3))) & 1u) << b;
+    pmask[j] = m;
 }
 
 __global__ void k_dense_flags(const int* __restrict__ eptr, int NC, int* __restrict__ flag) {
@@ -518,14 +552,19 @@ static void build_exec_layout_k(DeviceFormat& F, const int* trow, const int* tco
     F.entries.alloc(F.fp32 ? 2 * n : n);
     fill<int>(F.chunk_cols.p, (long long)NC * kChunkCols, -1, st);
     fill<int>(F.chunk_eptr.p + NC, 1, (int)n, st);
-    VCSRMC_HIP(hipMemsetAsync(pmask.p, 0, sizeof(int) * (size_t)NP, st));
+    {
+        DevBuf<unsigned char> rflag((size_t)num_panels_all * kPanelRows);
+        fill<unsigned char>(rflag.p, (long long)num_panels_all * kPanelRows, 0, st);
+        LAUNCH(k_row_flags, n, trow, n, rflag.p);
+        LAUNCH(k_panel_masks, NP, rflag.p, ppanel.p, NP, pmask.p);
+    }
     DevBuf<int> echunk(n);
     if (F.fp32)
         LAUNCH((k_panel_entries<K, true>), n, kp, vp, hdist.p, dc.p, pin.p, pstart.p, cbase.p, tcol,
-               tval, n, F.entries.p, F.chunk_cols.p, F.chunk_eptr.p, pmask.p, echunk.p);
+               tval, n, F.entries.p, F.chunk_cols.p, F.chunk_eptr.p, echunk.p);
     else
         LAUNCH((k_panel_entries<K, false>), n, kp, vp, hdist.p, dc.p, pin.p, pstart.p, cbase.p,
-               tcol, tval, n, F.entries.p, F.chunk_cols.p, F.chunk_eptr.p, pmask.p, echunk.p);
+               tcol, tval, n, F.entries.p, F.chunk_cols.p, F.chunk_eptr.p, echunk.p);
 
     // dense copies of well-filled tiles
     {
@@ -614,14 +653,13 @@ static void build_groups_k(DeviceFormat& F, const int* d_col, const float* d_val
     const int kbits = 6 + bits_for((unsigned long long)(S > 0 ? S - 1 : 0));
     DevBuf<K> k1(P), k2(P);
     DevBuf<uint32_t> v1(P), v2(P);
-    DevBuf<int> seg_n(S), seg_start(S + 1), gnum(S), gbase(S + 1);
-    VCSRMC_HIP(hipMemsetAsync(seg_n.p, 0, sizeof(int) * (size_t)S, st));
-    LAUNCH((k_pair_keys<K>), P, pstart, d_col, P, segw, k1.p, v1.p, seg_n.p);
+    DevBuf<int> seg_start(S + 1), gnum(S), gbase(S + 1);
+    LAUNCH((k_pair_keys<K>), P, pstart, d_col, P, segw, k1.p, v1.p);
     K* kp = k1.p; K* ka = k2.p;
     uint32_t* vp = v1.p; uint32_t* va = v2.p;
     radix_sort_pairs<K>(kp, vp, ka, va, P, kbits, st);
-    exclusive_sum<int, int>(seg_n.p, seg_start.p, S, st);
-    LAUNCH(k_groups_per_seg, S, seg_n.p, S, gnum.p);
+    LAUNCH((k_seg_starts<K>), (long long)S + 1, kp, P, S, seg_start.p);
+    LAUNCH(k_groups_per_seg, S, seg_start.p, S, gnum.p);
     exclusive_sum<int, int>(gnum.p, gbase.p, S, st);
     const int G = read_scalar(gbase.p + S, st);
 

@@ -26,10 +26,18 @@ struct DevBuf {
         return *this;
     }
     ~DevBuf() { release(); }
+    // On failure the buffer stays empty (p null, n 0) and the runtime's error is cleared, so
+    // a later launch does not report it.
     void alloc(size_t count) {
         release();
+        if (!count) return;
+        const hipError_t e = hipMalloc((void**)&p, count * sizeof(T));
+        if (e != hipSuccess) {
+            p = nullptr;
+            (void)hipGetLastError();
+            throw_hip(e, "hipMalloc", __FILE__, __LINE__);
+        }
         n = count;
-        if (n) VCSRMC_HIP(hipMalloc((void**)&p, n * sizeof(T)));
     }
     void release() {
         if (p) (void)hipFree(p);

@@ -949,15 +949,20 @@ __global__ void k_relabel_keys(const int* __restrict__ row_of, const int* __rest
     val[p] = (uint32_t)p;
 }
 
+// Two equal sorted (row, new column) keys: a row holds a column twice.  Checked before
+// anything is written, so a rejected call leaves the caller's CSR as it was.
+__global__ void k_relabel_dups(const u64* __restrict__ key, long long nnz,
+                               int* __restrict__ err) {
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i > 0 && i < nnz && key[i - 1] == key[i]) atomicOr(err, kDupCol);
+}
+
 __global__ void k_relabel_write(const u64* __restrict__ key, const uint32_t* __restrict__ src,
                                 const float* __restrict__ vin, long long nnz, int nb,
-                                int* __restrict__ col, float* __restrict__ vout,
-                                int* __restrict__ err) {
+                                int* __restrict__ col, float* __restrict__ vout) {
     const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= nnz) return;
-    const u64 k = key[i];
-    if (i > 0 && key[i - 1] == k) atomicOr(err, kDupCol);
-    col[i] = (int)(k & ((1ull << nb) - 1));
+    col[i] = (int)(key[i] & ((1ull << nb) - 1));
     vout[i] = vin[src[i]];
 }
 
@@ -1200,11 +1205,12 @@ void apply_column_permutation_device(const int* rp, int* col, float* val, int M,
         u64 *ka = k1.p, *kb = k2.p;
         uint32_t *va = v1.p, *vb = v2.p;
         radix_sort_pairs<u64>(ka, va, kb, vb, nnz, nb + mb, st);
+        RLAUNCH(k_relabel_dups, nnz, ka, (long long)nnz, err.p);
+        raise_if(err.p, st);
         DevBuf<float> vcopy(nnz);
         VCSRMC_HIP(hipMemcpyAsync(vcopy.p, val, sizeof(float) * (size_t)nnz,
                                   hipMemcpyDeviceToDevice, st));
-        RLAUNCH(k_relabel_write, nnz, ka, va, vcopy.p, (long long)nnz, nb, col, val, err.p);
-        raise_if(err.p, st);
+        RLAUNCH(k_relabel_write, nnz, ka, va, vcopy.p, (long long)nnz, nb, col, val);
     }
     if (B && N > 0 && O > 0)
         RLAUNCH(k_permute_rows, (long long)N * O, B, position, N, O, B_out);

@@ -823,11 +823,12 @@ void spmm_launch(const DeviceFormat& F, const void* dB, bool b_f16, int O, int t
         ((F.nnz < 48LL * F.num_chunks && b32_bytes > (12LL << 20)) ||
          b32_bytes > (256LL << 20))) {
         const long long n = (long long)F.N * O;
-        if ((long long)F.b_half.n < n) F.b_half.alloc((size_t)n);
+        if (!F.b_half.p || (long long)F.b_half.n < n) F.b_half.alloc((size_t)n);
+        _Float16* half = F.b_half.p;
         hipLaunchKernelGGL(k_b_to_half, dim3(grid_for((n + 3) / 4, 256)), dim3(256), 0, st,
-                           static_cast<const float*>(dB), F.b_half.p, n);
+                           static_cast<const float*>(dB), half, n);
         VCSRMC_HIP(hipGetLastError());
-        dB = F.b_half.p;
+        dB = half;
         b_f16 = true;
     }
     if (!accumulate && F.num_split_panels > 0) {

@@ -98,6 +98,13 @@ VCSRMC csr_to_vcsr_mc(const CSR& csr, bool fp32, int segw) {
 
 void upload_vcsr_mc_device(const VCSRMC& V) {
     if (g_uploaded) return;
+    // The C ABI takes sizes and pointers; the vectors must hold what those sizes say.
+    const size_t G = V.group_depth.size();
+    if (V.group_ptr.size() != G + 1 || V.group_seg_base.size() != G ||
+        V.group_rows.size() != 16 * G || V.lcol.size() != V.val.size() ||
+        V.item_gend.size() != V.item_gbeg.size())
+        throw std::runtime_error(
+            "upload_vcsr_mc_device: format arrays differ in length from the sizes they imply");
     if (!g_handle) check(vcsrmc_create(&g_handle), "upload_vcsr_mc_device");
     check(vcsrmc_upload(g_handle, V.M, V.N, V.segw, V.bundle, V.num_segments,
                         (int)V.group_depth.size(), (long long)V.val.size(),
