@@ -29,6 +29,7 @@ extern "C" {
 #define VCSRMC_ERR_OVERFLOW 7  /* |val| or another size exceeds the int32 of the format   */
 #define VCSRMC_ERR_HIP 8       /* HIP runtime error                                        */
 #define VCSRMC_ERR_STATE 9     /* no format built or uploaded in this handle               */
+#define VCSRMC_ERR_SCRATCH 10  /* input exceeds the static scratch of vcsrmc_spmm_noalloc  */
 
 /* Element type of the dense B operand. */
 #define VCSRMC_B_F32 0
@@ -121,6 +122,23 @@ int vcsrmc_spmm(vcsrmc_t h, const void *dB, int b_dtype, int O, int tileK, float
  * accumulate into C with atomicAdd (src/vcsr_mc.cu:228-234). */
 int vcsrmc_spmm_ex(vcsrmc_t h, const void *dB, int b_dtype, int O, int tileK, float *dC,
                    int flags, void *stream, float *ms);
+
+/* Bytes of the static device scratch of vcsrmc_spmm_noalloc, per GPU. */
+#define VCSRMC_NOALLOC_SCRATCH_BYTES (64u << 20)
+
+/* vcsrmc_spmm_ex that allocates nothing.  No counterpart in the reference: for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  The only device memory vcsrmc_spmm may allocate is the binary16 copy
+ * of an FP32 B that an FP16 format converts once per call (N x O halves); here it lives in a
+ * static device array of VCSRMC_NOALLOC_SCRATCH_BYTES per GPU, reserved when the library's
+ * code is loaded on that GPU and held until the process ends.  A call whose conversion would
+ * need more returns VCSRMC_ERR_SCRATCH before launching anything.  Every call on one GPU shares
+ * that GPU's scratch, so calls that overlap on one GPU (several streams or threads) race; the
+ * scratch keeps the last call's contents, and nothing in it needs to start at zero.  No timing
+ * events: the launch is asynchronous on `stream`.  Same results as vcsrmc_spmm_ex, bit for
+ * bit, under the same arguments. */
+int vcsrmc_spmm_noalloc(vcsrmc_t h, const void *dB, int b_dtype, int O, int tileK, float *dC,
+                        int flags, void *stream);
 
 /* Reverse Cuthill-McKee order of the columns of a device CSR (row_ptr[M+1], col[nnz]; any
  * column order inside a row): d_position[N] receives the new position of every old column,

@@ -29,7 +29,8 @@ LIB_PATH = os.path.join(HERE, "libvcsrmc.so")
 BENCH_LIB_PATH = os.path.join(HERE, "libvcsrmc_bench.so")
 
 OK, ERR_ARG, ERR_SEGW, ERR_TILEK, ERR_CSR, ERR_UNSORTED, ERR_FORMAT, ERR_OVERFLOW, ERR_HIP, \
-    ERR_STATE = range(10)
+    ERR_STATE, ERR_SCRATCH = range(11)
+NOALLOC_SCRATCH_BYTES = 64 << 20
 B_F32, B_F16 = 0, 1
 SPMM_OVERWRITE = 1
 
@@ -74,6 +75,7 @@ def lib():
         L.vcsrmc_download.argtypes = [vp] + [vp] * 8
         L.vcsrmc_spmm.argtypes = [vp, vp, C.c_int, C.c_int, C.c_int, vp, vp, fp]
         L.vcsrmc_spmm_ex.argtypes = [vp, vp, C.c_int, C.c_int, C.c_int, vp, C.c_int, vp, fp]
+        L.vcsrmc_spmm_noalloc.argtypes = [vp, vp, C.c_int, C.c_int, C.c_int, vp, C.c_int, vp]
         L.vcsrmc_rcm_order.argtypes = [vp, vp, C.c_int, C.c_int, C.c_int, vp, vp]
         L.vcsrmc_apply_column_permutation.argtypes = [vp, vp, vp, C.c_int, C.c_int, C.c_int, vp,
                                                       vp, C.c_int, vp, vp]
@@ -82,7 +84,8 @@ def lib():
         L.vcsrmc_last_error.restype = C.c_char_p
         for f in ("vcsrmc_create", "vcsrmc_destroy", "vcsrmc_half_scale", "vcsrmc_build_csr",
                   "vcsrmc_upload", "vcsrmc_get_info", "vcsrmc_download", "vcsrmc_spmm",
-                  "vcsrmc_spmm_ex", "vcsrmc_rcm_order", "vcsrmc_apply_column_permutation"):
+                  "vcsrmc_spmm_ex", "vcsrmc_spmm_noalloc", "vcsrmc_rcm_order",
+                  "vcsrmc_apply_column_permutation"):
             getattr(L, f).restype = C.c_int
         _lib_handle = L
     return _lib_handle

@@ -2,6 +2,7 @@
 // Internal errors are C++ exceptions carrying a status; they stop here and become return
 // codes, with the message kept per thread for vcsrmc_last_error().
 #include <cstdio>
+#include <mutex>
 #include <new>
 #include <string>
 
@@ -23,6 +24,11 @@ namespace vcsrmc {
 }
 
 }  // namespace vcsrmc
+
+// Scratch of vcsrmc_spmm_noalloc: a static device array, one copy per GPU.  In host code the
+// name `scratch` is only a stand-in for the symbol, never a device address: the copy of the
+// current device is reached through the address hipGetSymbolAddress returns for it.
+static __device__ __attribute__((aligned(256))) unsigned char scratch[VCSRMC_NOALLOC_SCRATCH_BYTES];
 
 namespace {
 
@@ -60,6 +66,24 @@ struct DeviceScope {
 
 void need(bool ok, const char* msg) {
     if (!ok) throw vcsrmc::Error(VCSRMC_ERR_ARG, msg);
+}
+
+// The copy of `scratch` (below) on each device, looked up once per device.
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The current device's scratch (the caller has made `dev` current).
+void* scratch_of_device(int dev) {
+    if (dev < 0 || dev >= kMaxDevices) throw vcsrmc::Error(VCSRMC_ERR_ARG, "device index too large");
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (!g_scratch_ptr[dev]) {
+        void* ptr = nullptr;
+        VCSRMC_HIP(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+        if (!ptr) throw vcsrmc::Error(VCSRMC_ERR_HIP, "no device address for the scratch array");
+        g_scratch_ptr[dev] = ptr;
+    }
+    return g_scratch_ptr[dev];
 }
 
 }  // namespace
@@ -221,6 +245,21 @@ int vcsrmc_spmm_ex(vcsrmc_t h, const void* dB, int b_dtype, int O, int tileK, fl
     });
 }
 
+int vcsrmc_spmm_noalloc(vcsrmc_t h, const void* dB, int b_dtype, int O, int tileK, float* dC,
+                        int flags, void* stream) {
+    return guarded([&] {
+        need(h != nullptr, "null handle");
+        need(b_dtype == VCSRMC_B_F32 || b_dtype == VCSRMC_B_F16, "unknown B dtype");
+        need((flags & ~VCSRMC_SPMM_OVERWRITE) == 0, "unknown flag");
+        DeviceScope ds(h->device);
+        vcsrmc::HalfScratch ext;
+        ext.p = static_cast<_Float16*>(scratch_of_device(h->device));
+        ext.halves = VCSRMC_NOALLOC_SCRATCH_BYTES / sizeof(_Float16);
+        vcsrmc::spmm_launch(h->F, dB, b_dtype == VCSRMC_B_F16, O, tileK, dC,
+                            !(flags & VCSRMC_SPMM_OVERWRITE), (hipStream_t)stream, ext);
+    });
+}
+
 const char* vcsrmc_status_string(int status) {
     switch (status) {
         case VCSRMC_OK: return "ok";
@@ -233,6 +272,7 @@ const char* vcsrmc_status_string(int status) {
         case VCSRMC_ERR_OVERFLOW: return "format size exceeds int32";
         case VCSRMC_ERR_HIP: return "HIP runtime error";
         case VCSRMC_ERR_STATE: return "no format";
+        case VCSRMC_ERR_SCRATCH: return "input exceeds the static scratch of vcsrmc_spmm_noalloc";
         default: return "unknown status";
     }
 }

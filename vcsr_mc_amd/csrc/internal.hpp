@@ -111,9 +111,17 @@ struct HostArrays {
 void build_from_host(DeviceFormat& F, const HostArrays& H, hipStream_t st);
 
 // C += A.B (src/vcsr_mc.cu:352-394 semantics).  b_f16: B is binary16 in HBM.
+// Device memory a launch may use for the binary16 copy of an FP32 B (an FP16 format converts
+// B once per call where that pays, see spmm_launch): `p` of `halves` elements, or p = null for
+// the format's own buffer, allocated on first use.
+struct HalfScratch {
+    _Float16* p = nullptr;
+    size_t halves = 0;
+};
+
 // accumulate: C += A.B; otherwise C = A.B on the rows A touches (other rows untouched).
 void spmm_launch(const DeviceFormat& F, const void* dB, bool b_f16, int O, int tileK, float* dC,
-                 bool accumulate, hipStream_t st);
+                 bool accumulate, hipStream_t st, HalfScratch ext = HalfScratch());
 
 // Reverse Cuthill-McKee order of the columns of a device CSR (include/reorder.hpp:17-77):
 // position[old column] = new column.  Synchronises `st`.

@@ -794,7 +794,7 @@ static int o_tile_width(const DeviceFormat& F, bool b_f16, int O, int tileK) {
 }
 
 void spmm_launch(const DeviceFormat& F, const void* dB, bool b_f16, int O, int tileK, float* dC,
-                 bool accumulate, hipStream_t st) {
+                 bool accumulate, hipStream_t st, HalfScratch ext) {
     if (tileK != 16 && tileK != 32 && tileK != 64 && tileK != 128)
         throw Error(VCSRMC_ERR_TILEK, "vcsr_mc supports tileK in {16, 32, 64, 128}");
     if (!F.ready) throw Error(VCSRMC_ERR_STATE, "no format in this handle");
@@ -823,8 +823,17 @@ void spmm_launch(const DeviceFormat& F, const void* dB, bool b_f16, int O, int t
         ((F.nnz < 48LL * F.num_chunks && b32_bytes > (12LL << 20)) ||
          b32_bytes > (256LL << 20))) {
         const long long n = (long long)F.N * O;
-        if (!F.b_half.p || (long long)F.b_half.n < n) F.b_half.alloc((size_t)n);
-        _Float16* half = F.b_half.p;
+        _Float16* half = ext.p;
+        if (half) {
+            if ((unsigned long long)n > ext.halves)
+                throw Error(VCSRMC_ERR_SCRATCH,
+                            "B of N x O = " + std::to_string(n) +
+                                " values exceeds the static scratch of " +
+                                std::to_string(ext.halves) + " binary16 values");
+        } else {
+            if (!F.b_half.p || (long long)F.b_half.n < n) F.b_half.alloc((size_t)n);
+            half = F.b_half.p;
+        }
         hipLaunchKernelGGL(k_b_to_half, dim3(grid_for((n + 3) / 4, 256)), dim3(256), 0, st,
                            static_cast<const float*>(dB), half, n);
         VCSRMC_HIP(hipGetLastError());
