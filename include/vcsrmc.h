@@ -94,18 +94,24 @@ int vcsrmc_download(vcsrmc_t h, int *group_ptr, int *group_depth, int *group_seg
  * b_dtype = VCSRMC_B_F32 (the reference's `const float* dB`) or VCSRMC_B_F16 (B already in
  * binary16, converted once by the caller).  tileK in {16,32,64,128} is the widest
  * output-column tile of one work-group, as in the reference; the launcher takes a narrower one
- * when O needs less, or 64 instead of 128 for formats whose tiles hold few nonzeros (FP32, or B
- * larger than the GPU's L2) and for FP32 formats of fewer than 2048 16-row panels, where that
- * measured faster; the result does not depend on it.  Rows of C that A does not touch are left
- * as they are.  If ms is non-NULL the launch is bracketed by two hipEvents on `stream`, the
- * call waits for it and *ms is the elapsed time (the reference's protocol); if ms is NULL the
- * launch is asynchronous.  An FP16 format given FP32 B rounds B to binary16 as the kernel
- * loads it; where nnz >= 12 N and B exceeds 12 MB with tiles averaging fewer than 48 nonzeros,
- * or exceeds 256 MB, it converts B once per call instead, into a buffer the handle keeps
- * (N x O halves, allocated on first use), so calls on one handle from several streams at once
- * must not overlap.  The
- * launch itself allocates and clears nothing, so it can be captured in a HIP graph (make that
- * first FP32-B call before capturing).
+ * where that measured faster, and the result does not depend on it:
+ *   - never wider than O needs;
+ *   - 64 instead of 128 for formats whose tiles hold few nonzeros (fewer than 48 on average)
+ *     that are FP32 or whose B exceeds the GPU's 32 MB of L2;
+ *   - 64 for FP32 formats of fewer than 2048 16-row panels;
+ *   - 64 for an FP16 format reading FP32 B directly (at 128 that kernel holds too many
+ *     registers for three waves per SIMD).
+ * Rows of C that A does not touch are left as they are.  If ms is non-NULL the launch is
+ * bracketed by two hipEvents on `stream`, the call waits for it and *ms is the elapsed time (the
+ * reference's protocol); if ms is NULL the launch is asynchronous.  An FP16 format given FP32 B
+ * rounds B to binary16 as the kernel loads it; where nnz >= 12 N and B exceeds 12 MB with tiles
+ * averaging fewer than 48 nonzeros, or exceeds 256 MB, it converts B once per call instead,
+ * into a buffer the handle keeps (N x O halves, allocated on first use and reallocated when a
+ * later call needs more), so calls on one handle from several streams at once must not overlap.
+ * Otherwise the launch allocates and clears nothing, so it can be captured in a HIP graph: make
+ * the first FP32-B call, with the largest O, before capturing; a call with a larger O frees
+ * that buffer, and graphs captured earlier must not be replayed after it
+ * (vcsrmc_spmm_noalloc below never allocates).
  * Replaces run_vcsr_mc_spmm_gpu (include/vcsr_formats.hpp:24-25, src/vcsr_mc.cu:352-394). */
 int vcsrmc_spmm(vcsrmc_t h, const void *dB, int b_dtype, int O, int tileK, float *dC,
                 void *stream, float *ms);
@@ -146,6 +152,13 @@ int vcsrmc_spmm_noalloc(vcsrmc_t h, const void *dB, int b_dtype, int O, int tile
  * (include/reorder.hpp:17-77).  Computed on the GPU; synchronises `stream`. */
 int vcsrmc_rcm_order(const int *d_row_ptr, const int *d_col, int M, int N, int nnz,
                      int *d_position, void *stream);
+
+/* Iteration limits of vcsrmc_rcm_order's loops: levels of the breadth-first walk and rounds of
+ * the connected-component search.  0 (the default) keeps the proven maxima, N + 1 levels and
+ * N (ceil(lg N) + 2) + 1 rounds, which a correct walk never reaches; a walk that would pass a
+ * limit stops, with every kernel ended, and vcsrmc_rcm_order returns VCSRMC_ERR_STATE.  Lower
+ * limits exist to test that path.  Process-wide; no counterpart in the reference. */
+int vcsrmc_set_rcm_limits(long long max_levels, long long max_rounds);
 
 /* Relabels the columns of a device CSR in place, col[p] = position[col[p]], with every row
  * re-sorted by its new columns (values follow), and, when d_B is non-NULL, writes

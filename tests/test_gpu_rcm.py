@@ -197,3 +197,40 @@ def test_rcm_then_spmm_gpu(orc):
     R, L1 = orc.spmm_csr(A.row_ptr, A.col, A.val, A.M, B, mode=0)
     ok, worst, row = row_l1_parity(Cd.cpu().numpy(), R, L1, 1e-5)
     assert ok, (worst, row)
+
+
+def test_rcm_limits_give_up_cleanly():
+    """The ordering's loops run to proven maxima (N + 1 levels, N (ceil(lg N) + 2) + 1
+    component rounds) that a correct walk never reaches.  Lowered from the host, they make the
+    walk stop -- inside the work-group kernel, which then ends normally, or between the
+    host-driven levels -- and the call returns ERR_STATE; restored, the same call succeeds."""
+    rp, col = banded(2000, 1)  # a path: 1999 levels
+    L = vm.lib()
+    try:
+        for levels, rounds, what in ((50, 0, b"levels"), (0, 1, b"rounds")):
+            assert L.vcsrmc_set_rcm_limits(levels, rounds) == vm.OK
+            say("rcm limits", levels, rounds)
+            with pytest.raises(vm.VCSRMCError) as e:
+                gpu_rcm(rp, col, 2000, 2000)
+            assert e.value.status == vm.ERR_STATE and what.decode() in str(e.value)
+        A = vm.generate(2, 30000)  # frontiers beyond one work-group: host-driven levels
+        assert L.vcsrmc_set_rcm_limits(2, 0) == vm.OK
+        say("rcm limits host levels", A.N)
+        with pytest.raises(vm.VCSRMCError) as e:
+            gpu_rcm(A.row_ptr, A.col, A.M, A.N)
+        assert e.value.status == vm.ERR_STATE
+    finally:
+        assert L.vcsrmc_set_rcm_limits(0, 0) == vm.OK
+    assert np.array_equal(gpu_rcm(rp, col, 2000, 2000), 1999 - np.arange(2000))
+
+
+def test_apply_duplicate_leaves_csr_unchanged():
+    """A row holding one column twice is refused before anything is written."""
+    rp = np.array([0, 1, 3], np.int32)
+    col, val = np.array([2, 0, 0], np.int32), np.array([1.5, 2.5, 3.5], np.float32)
+    dc, dv = dev(col), dev(val)
+    with pytest.raises(vm.VCSRMCError) as e:
+        vm.apply_column_permutation_device(dev(rp), dc, dv, 2, 3,
+                                           dev(np.array([2, 1, 0], np.int32)))
+    assert e.value.status == vm.ERR_UNSORTED
+    assert np.array_equal(dc.cpu().numpy(), col) and np.array_equal(dv.cpu().numpy(), val)

@@ -55,12 +55,21 @@ _lib_handle = None
 _bench_handle = None
 
 
+def _one_hip_runtime():
+    """Loads torch's HIP runtime before either library.  torch ships its own libamdhip64
+    (soname libamdhip64.so.7, needed by torch as libamdhip64.so); loaded first, it also serves
+    the libraries' libamdhip64.so.7.  Loaded the other way round, the process would hold two
+    HIP runtimes, and the second to open the GPU finds no device."""
+    import torch  # noqa: F401
+
+
 def lib():
     """The product library; raises if it has not been built."""
     global _lib_handle
     if _lib_handle is None:
         if not os.path.exists(LIB_PATH):
             raise ImportError(f"{LIB_PATH} is not built (run __graft_entry__.build())")
+        _one_hip_runtime()
         L = C.CDLL(LIB_PATH)
         vp, ip, fp = C.c_void_p, C.POINTER(C.c_int), C.POINTER(C.c_float)
         L.vcsrmc_create.argtypes = [C.POINTER(vp)]
@@ -77,6 +86,7 @@ def lib():
         L.vcsrmc_spmm_ex.argtypes = [vp, vp, C.c_int, C.c_int, C.c_int, vp, C.c_int, vp, fp]
         L.vcsrmc_spmm_noalloc.argtypes = [vp, vp, C.c_int, C.c_int, C.c_int, vp, C.c_int, vp]
         L.vcsrmc_rcm_order.argtypes = [vp, vp, C.c_int, C.c_int, C.c_int, vp, vp]
+        L.vcsrmc_set_rcm_limits.argtypes = [C.c_longlong, C.c_longlong]
         L.vcsrmc_apply_column_permutation.argtypes = [vp, vp, vp, C.c_int, C.c_int, C.c_int, vp,
                                                       vp, C.c_int, vp, vp]
         L.vcsrmc_status_string.restype = C.c_char_p
@@ -85,7 +95,7 @@ def lib():
         for f in ("vcsrmc_create", "vcsrmc_destroy", "vcsrmc_half_scale", "vcsrmc_build_csr",
                   "vcsrmc_upload", "vcsrmc_get_info", "vcsrmc_download", "vcsrmc_spmm",
                   "vcsrmc_spmm_ex", "vcsrmc_spmm_noalloc", "vcsrmc_rcm_order",
-                  "vcsrmc_apply_column_permutation"):
+                  "vcsrmc_set_rcm_limits", "vcsrmc_apply_column_permutation"):
             getattr(L, f).restype = C.c_int
         _lib_handle = L
     return _lib_handle
@@ -96,6 +106,7 @@ def bench_lib():
     if _bench_handle is None:
         if not os.path.exists(BENCH_LIB_PATH):
             raise ImportError(f"{BENCH_LIB_PATH} is not built (run __graft_entry__.build())")
+        _one_hip_runtime()
         L = C.CDLL(BENCH_LIB_PATH)
         vp = C.c_void_p
         L.vcsrmc_gen.argtypes = [C.c_int, C.c_int, C.c_ulonglong, C.POINTER(vp)]

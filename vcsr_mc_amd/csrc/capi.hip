@@ -129,6 +129,13 @@ int vcsrmc_rcm_order(const int* d_row_ptr, const int* d_col, int M, int N, int n
     });
 }
 
+int vcsrmc_set_rcm_limits(long long max_levels, long long max_rounds) {
+    return guarded([&] {
+        need(max_levels >= 0 && max_rounds >= 0, "negative limit");
+        vcsrmc::set_rcm_limits(max_levels, max_rounds);
+    });
+}
+
 int vcsrmc_apply_column_permutation(const int* d_row_ptr, int* d_col, float* d_val, int M, int N,
                                     int nnz, const int* d_position, const float* d_B, int O,
                                     float* d_B_out, void* stream) {

@@ -127,6 +127,9 @@ void spmm_launch(const DeviceFormat& F, const void* dB, bool b_f16, int O, int t
 // position[old column] = new column.  Synchronises `st`.
 void rcm_order_device(const int* rp, const int* col, int M, int N, int nnz, int* position,
                       hipStream_t st);
+// Iteration limits of rcm_order_device's loops (BFS levels, component rounds); 0 restores the
+// proven maxima.  Lowered only to test that an exhausted loop returns an error.
+void set_rcm_limits(long long max_level, long long max_rounds);
 // Column relabelling (include/reorder.hpp:82-108): col and val in place, rows re-sorted by new
 // column; B_out[position[r], :] = B[r, :] when B is given.  Synchronises `st`.
 void apply_column_permutation_device(const int* rp, int* col, float* val, int M, int N, int nnz,

@@ -28,6 +28,7 @@
 #include <algorithm>
 #include <climits>
 #include <cstdint>
+#include <string>
 
 #include "../../include/vcsrmc.h"
 #include "internal.hpp"
@@ -341,10 +342,12 @@ __device__ void ls_median_to_first(u64* a, long long dst, long long x, long long
     }
 }
 
+// Every pass moves lo up and hi down by at least one, so at most (hi - lo) / 2 + 1 passes run;
+// the loop states that bound.
 __device__ long long ls_partition(u64* a, long long lo, long long hi, long long piv) {
     const uint32_t kp = skey(a[piv]);
     const long long end = hi;
-    for (;;) {
+    for (long long pass = (hi - lo) / 2 + 1; pass >= 0; --pass) {
         while (lo < end && skey(a[lo]) < kp) ++lo;
         --hi;
         while (hi > piv && kp < skey(a[hi])) --hi;
@@ -352,6 +355,7 @@ __device__ long long ls_partition(u64* a, long long lo, long long hi, long long 
         ls_swap(a, lo, hi);
         ++lo;
     }
+    return lo;
 }
 
 struct SortRange {
@@ -742,9 +746,14 @@ __device__ int block_partition_lds(u64* a, int lo, int hi, int* lpos, int* rpos,
     return cut;
 }
 
+// A walk of N vertices has at most N levels after the roots; the loop runs to `max_level` at
+// most (N + 1, or lower when a test asks) and otherwise reports state.w = kBfsOverrun.
+constexpr int kBfsOverrun = 2;
+
 __global__ __launch_bounds__(kBfsThreads) void k_bfs_levels(
     int* __restrict__ front, const long long* __restrict__ head, const int* __restrict__ adj,
-    int* __restrict__ lev, int* __restrict__ seq, int* claim, int N, int4* __restrict__ state) {
+    int* __restrict__ lev, int* __restrict__ seq, int* claim, int N, long long max_level,
+    int4* __restrict__ state) {
     constexpr int NW = kBfsThreads / 64;
     __shared__ int s_ofs[kBfsCap + 1];    // edge offset of each frontier vertex
     __shared__ int s_fx[kBfsCap + 1];     // the frontier; then children before each edge
@@ -758,12 +767,17 @@ __global__ __launch_bounds__(kBfsThreads) void k_bfs_levels(
     const int t = threadIdx.x;
     const int4 s0 = *state;
     int f = s0.x, base = s0.y, level = s0.z;
-    bool finished = false, moved = false;
+    bool finished = false, moved = false, overrun = false;
     for (int i = t; i < f; i += kBfsThreads) s_front[i] = front[i];
+    // `level` is the same in every thread: the bound ends the loop for all of them at once.
     for (;;) {
         __syncthreads();
         if (f == 0 || base >= N) {
             finished = true;
+            break;
+        }
+        if (level > max_level) {
+            overrun = true;
             break;
         }
         // edge offsets of the frontier vertices [v0, v1) of this thread
@@ -893,7 +907,7 @@ __global__ __launch_bounds__(kBfsThreads) void k_bfs_levels(
                 const int m = s_mark[i];
                 if (m <= kMarkHeap) {
                     int e = i + 1;
-                    while (s_mark[e] == kMarkNone) ++e;
+                    while (e < n && s_mark[e] == kMarkNone) ++e;  // the group's end is marked
                     if (m == kMarkHeap) ls_heapsort(s_packed, i, e);  // depth exhausted
                     else if (e - i > 1) ls_sort_range(s_packed, i, e, m);
                 }
@@ -913,7 +927,7 @@ __global__ __launch_bounds__(kBfsThreads) void k_bfs_levels(
     }
     if (moved)
         for (int i = t; i < f; i += kBfsThreads) front[i] = s_front[i];
-    if (t == 0) *state = make_int4(f, base, level, finished ? 1 : 0);
+    if (t == 0) *state = make_int4(f, base, level, overrun ? kBfsOverrun : finished ? 1 : 0);
 }
 
 // ---- 5. order ----------------------------------------------------------------------------
@@ -1033,7 +1047,15 @@ void sort_groups(const int* gstart, int ngroups, int n, u64* packed, SortJobs& J
     }
 }
 
+// Iteration limits of the ordering's loops; 0 selects the proven maxima (see rcm_order_device).
+long long g_max_level = 0, g_max_rounds = 0;
+
 }  // namespace
+
+void set_rcm_limits(long long max_level, long long max_rounds) {
+    g_max_level = max_level;
+    g_max_rounds = max_rounds;
+}
 
 void rcm_order_device(const int* rp, const int* col, int M, int N, int nnz, int* position,
                       hipStream_t st) {
@@ -1089,12 +1111,25 @@ void rcm_order_device(const int* rp, const int* col, int M, int N, int nnz, int*
         RLAUNCH(k_scatter_rank, N, order.p, N, rank.p);
     }
 
+    // Proven maxima of the loops below.  Levels: every level but the last places at least one
+    // vertex, so level <= N.  Component rounds: a round changes something or ends the loop;
+    // between two rounds with a hook (each hook removes a tree, so at most N - 1 of them),
+    // pointer jumping alone halves every depth, so after ceil(lg N) + 1 rounds all trees are
+    // stars and the next round either hooks or changes nothing: at most
+    // N (ceil(lg N) + 2) + 1 rounds.
+    const long long max_level = g_max_level > 0 ? g_max_level : (long long)N + 1;
+    const long long max_rounds =
+        g_max_rounds > 0 ? g_max_rounds : (long long)N * (bits_for((u64)N) + 2) + 1;
+
     // 3. components
     DevBuf<int> comp(N);
     {
         DevBuf<int> changed(1);
         RLAUNCH(k_cc_init, N, comp.p, N);
-        for (;;) {
+        for (long long round = 0;; ++round) {
+            if (round >= max_rounds)
+                throw Error(VCSRMC_ERR_STATE, "rcm ordering: connected components did not settle "
+                                              "within " + std::to_string(max_rounds) + " rounds");
             fill<int>(changed.p, 1, 0, st);
             RLAUNCH(k_cc_hook, E, adj_u.p, adj.p, E, rank.p, comp.p, changed.p);
             RLAUNCH(k_cc_jump, N, comp.p, N, changed.p);
@@ -1129,14 +1164,15 @@ void rcm_order_device(const int* rp, const int* col, int M, int N, int nnz, int*
             const int4 s0 = make_int4(f, base, level, 0);
             VCSRMC_HIP(hipMemcpyAsync(bfs_state.p, &s0, sizeof(s0), hipMemcpyHostToDevice, st));
             hipLaunchKernelGGL(k_bfs_levels, dim3(1), dim3(kBfsThreads), 0, st, front.p, head.p,
-                               adj.p, lev.p, seq.p, claim.p, N, bfs_state.p);
+                               adj.p, lev.p, seq.p, claim.p, N, max_level, bfs_state.p);
             VCSRMC_HIP(hipGetLastError());
             const int4 s1 = read_scalar(bfs_state.p, st);
             f = s1.x;
             base = s1.y;
             level = s1.z;
-            if (s1.w || f == 0 || base >= N) break;
+            if (s1.w || f == 0 || base >= N) break;  // finished, or overran max_level
         }
+        if (level > max_level) break;
         // a level whose frontier or edge count exceeds one work-group
         RLAUNCH(k_front_degree, f, front.p, f, head.p, fdeg.p);
         exclusive_sum<long long, long long>(fdeg.p, fofs.p, f, st);
@@ -1163,6 +1199,9 @@ void rcm_order_device(const int* rp, const int* col, int M, int N, int nnz, int*
         f = n;
         ++level;
     }
+    if (level > max_level)
+        throw Error(VCSRMC_ERR_STATE, "rcm ordering: the breadth-first walk passed " +
+                                          std::to_string(max_level) + " levels");
     if (base != N) throw Error(VCSRMC_ERR_STATE, "rcm ordering left vertices unvisited");
 
     // 5. order

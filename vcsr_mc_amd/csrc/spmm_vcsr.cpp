@@ -1,473 +1,534 @@
-// spmm_vcsr.cpp -- benchmark driver with the reference's command line and CSV.
+// spmm_vcsr.cpp -- benchmark driver with the reference's command line, messages and CSV
+// (MuuSeoTia/VCSR_MC src/main.cpp:33-372), over libvcsrmc.so and libvcsrmc_bench.so.
 //
-// Mirrors MuuSeoTia/VCSR_MC src/main.cpp (CLI :33-43, B fill :161-179, oracle :199-218,
-// measure :239-308, VCSR loop :345-362, CSV :220) on top of libvcsrmc.so and libvcsrmc_bench.so:
-//   vcsr_mc / vcsr_mc_fp32     through the drop-in C++ surface (include/vcsr_formats.hpp),
-//                              with the reference's call sequence convert -> upload -> run
+//   vcsr_mc / vcsr_mc_fp32     the drop-in C++ surface (include/vcsr_formats.hpp), called in the
+//                              reference's sequence convert -> upload -> run -> destroy
 //   rocsparse / rocsparse_fp16 hipSPARSE SpMM (libvcsrmc_bench.so)
-// --reorder rcm (main.cpp:182-183) runs the GPU column reordering through the drop-in
-// include/reorder.hpp.  Additive: --gen K[:size] reads a seeded synthetic workload instead of
-// --mtx (configs of include/vcsrmc_bench.h).
+// Input: a Matrix Market file through the drop-in reader (include/mmio.hpp, include/csr.hpp),
+// or, additive, a seeded synthetic workload (--gen K[:size]).  --reorder rcm runs the GPU column
+// reordering of include/reorder.hpp.  --dump-csr PATH (additive) writes the CSR as read and
+// stops before any GPU call.
+//
+// The driver is organised as: options -> input matrix -> dense B -> device operands -> reference
+// result -> for each selected kernel, the timing protocol, the validation and one report row.
 #include <getopt.h>
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
-#include <chrono>
 #include <cerrno>
+#include <chrono>
 #include <climits>
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
-#include <fstream>
-#include <functional>
-#include <limits>
-#include <numeric>
+#include <memory>
 #include <random>
-#include <sstream>
 #include <stdexcept>
 #include <string>
 #include <vector>
 
 #include "csr.hpp"
+#include "cuda_check.hpp"
+#include "mmio.hpp"
 #include "reorder.hpp"
 #include "vcsr_formats.hpp"
 #include "vcsrmc_bench.h"
 
 namespace {
 
-void hip_ok(hipError_t e, const char* what) {
-    if (e != hipSuccess) {
-        std::fprintf(stderr, "HIP error in %s: %s\n", what, hipGetErrorString(e));
-        std::exit(EXIT_FAILURE);
-    }
+using Clock = std::chrono::steady_clock;
+
+double ms_since(Clock::time_point t0) {
+    return std::chrono::duration<double, std::milli>(Clock::now() - t0).count();
 }
 
-// ---- Matrix Market coordinate files (semantics of include/mmio.hpp:19-75) ----------------
-struct Triples {
-    int M = 0, N = 0;
-    std::vector<int> r, c;
-    std::vector<float> v;
+// ---- options ------------------------------------------------------------------------------
+struct Options {
+    std::string mtx, gen, dump_csr;
+    std::string algo = "all", check = "rocsparse", reorder = "none", bdist = "pattern";
+    std::string stat = "mean";
+    int O = 128, segw = 16, tileK = 64, repeat = 10, warmup = 3;
+    bool csv = false, lenient = false, help = false;
+    std::vector<std::string> kernels;  // the --algo list, validated
 };
 
-Triples read_mtx(const std::string& path) {
-    std::ifstream in(path);
-    if (!in) throw std::runtime_error("Failed to open MTX: " + path);
-    std::string line;
-    if (!std::getline(in, line)) throw std::runtime_error("Empty MTX file");
-    std::istringstream banner(line);
-    std::string magic, object, layout, field, sym;
-    banner >> magic >> object >> layout >> field >> sym;
-    if (magic != "%%MatrixMarket" || object != "matrix" || layout != "coordinate")
-        throw std::runtime_error("Expected a Matrix Market coordinate matrix");
-    if (field != "real" && field != "integer" && field != "pattern")
-        throw std::runtime_error("Unsupported MTX field: " + field);
-    if (sym != "general" && sym != "symmetric" && sym != "skew-symmetric")
-        throw std::runtime_error("Unsupported MTX symmetry: " + sym);
-    auto data_line = [&](std::string& out) {
-        while (std::getline(in, out)) {
-            const size_t k = out.find_first_not_of(" \t\r");
-            if (k != std::string::npos && out[k] != '%') return true;
-        }
-        return false;
-    };
-    if (!data_line(line)) throw std::runtime_error("Missing MTX dimensions");
-    long long m = 0, n = 0, cnt = 0;
-    {
-        std::istringstream d(line);
-        if (!(d >> m >> n >> cnt) || m <= 0 || n <= 0 || m >= INT_MAX || n >= INT_MAX ||
-            cnt < 0 || cnt > INT_MAX)
-            throw std::runtime_error("Invalid or unsupported MTX dimensions/nnz");
-    }
-    if (sym != "general" && m != n) throw std::runtime_error("Symmetric MTX must be square");
-    Triples t;
-    t.M = (int)m;
-    t.N = (int)n;
-    auto push = [&](long long r, long long c, float v) {
-        if (t.v.size() >= (size_t)INT_MAX)
-            throw std::runtime_error("Expanded MTX exceeds 32-bit nnz limit");
-        t.r.push_back((int)r);
-        t.c.push_back((int)c);
-        t.v.push_back(v);
-    };
-    for (long long i = 0; i < cnt; ++i) {
-        if (!data_line(line)) throw std::runtime_error("Truncated MTX data");
-        std::istringstream e(line);
-        long long r, c;
-        double val = 1.0;
-        if (!(e >> r >> c) || (field != "pattern" && !(e >> val)))
-            throw std::runtime_error("Bad MTX entry at index " + std::to_string(i));
-        std::string extra;
-        if (e >> extra) throw std::runtime_error("Extra fields in MTX entry");
-        if (r < 1 || r > m || c < 1 || c > n)
-            throw std::runtime_error("MTX row/column index out of range (expected one-based indices)");
-        if (!std::isfinite(val) || std::fabs(val) > std::numeric_limits<float>::max())
-            throw std::runtime_error("MTX value is not finite FP32");
-        if (sym == "skew-symmetric" && r == c && val != 0)
-            throw std::runtime_error("Skew-symmetric MTX diagonal must be zero");
-        push(r - 1, c - 1, (float)val);
-        if (sym != "general" && r != c) push(c - 1, r - 1, (float)(sym == "symmetric" ? val : -val));
-    }
-    if (data_line(line)) throw std::runtime_error("Extra entries after declared MTX nnz");
-    return t;
-}
-
-// COO -> CSR with sorted columns; duplicates are rejected (include/csr.hpp:16-42).
-CSR to_csr(const Triples& t) {
-    CSR a;
-    a.M = t.M;
-    a.N = t.N;
-    a.nnz = (int)t.v.size();
-    a.row_ptr.assign((size_t)a.M + 1, 0);
-    for (int r : t.r) a.row_ptr[(size_t)r + 1]++;
-    for (int i = 0; i < a.M; ++i) a.row_ptr[i + 1] += a.row_ptr[i];
-    std::vector<int> fill(a.row_ptr.begin(), a.row_ptr.end() - 1);
-    std::vector<std::pair<int, float>> tmp(a.nnz);
-    for (size_t i = 0; i < t.v.size(); ++i) tmp[fill[t.r[i]]++] = {t.c[i], t.v[i]};
-    a.col.resize(a.nnz);
-    a.val.resize(a.nnz);
-    for (int r = 0; r < a.M; ++r) {
-        auto b = tmp.begin() + a.row_ptr[r], e = tmp.begin() + a.row_ptr[r + 1];
-        std::stable_sort(b, e, [](const auto& x, const auto& y) { return x.first < y.first; });
-        for (auto it = b; it != e; ++it) {
-            if (it != b && it->first == (it - 1)->first)
-                throw std::runtime_error(
-                    "Duplicate MTX coordinates are unsupported; coalesce them before benchmarking");
-            a.col[it - tmp.begin()] = it->first;
-            a.val[it - tmp.begin()] = it->second;
-        }
-    }
-    return a;
-}
-
-CSR generated(const std::string& spec) {
-    const size_t colon = spec.find(':');
-    const int cfg = std::stoi(spec.substr(0, colon));
-    const int size = colon == std::string::npos ? 0 : std::stoi(spec.substr(colon + 1));
-    vcsrmc_matrix_t h = nullptr;
-    if (vcsrmc_gen(cfg, size, 20260923ULL + (unsigned)cfg, &h) != 0)
-        throw std::runtime_error("Unknown or failed --gen workload: " + spec);
-    CSR a;
-    long long nnz = 0;
-    vcsrmc_gen_info(h, &a.M, &a.N, &nnz);
-    a.nnz = (int)nnz;
-    a.row_ptr.resize((size_t)a.M + 1);
-    a.col.resize(a.nnz);
-    a.val.resize(a.nnz);
-    vcsrmc_gen_copy(h, a.row_ptr.data(), a.col.data(), a.val.data());
-    vcsrmc_gen_free(h);
-    return a;
-}
-
-int int_at_least(const char* s, long lo) {
-    char* end = nullptr;
+// Decimal integer >= lo that fits an int, or the reference's error text.
+int parse_int(const char* text, long lo) {
     errno = 0;
-    const long v = std::strtol(s, &end, 10);
-    if (errno || end == s || *end || v < lo || v > INT_MAX)
-        throw std::runtime_error(std::string("Expected integer >= ") + std::to_string(lo) +
-                                 ", got: " + s);
+    char* end = nullptr;
+    const long long v = std::strtoll(text, &end, 10);
+    const bool whole = end != text && *end == '\0' && errno == 0;
+    if (!whole || v < lo || v > INT_MAX)
+        throw std::runtime_error("Expected integer >= " + std::to_string(lo) + ", got: " + text);
     return (int)v;
 }
 
-std::string quote(const std::string& s) {
-    std::string o = "\"";
-    for (char ch : s) { if (ch == '"') o += '"'; o += ch; }
-    return o + '"';
+const char* const kKernelNames[] = {"all", "rocsparse", "rocsparse_fp16", "vcsr_mc",
+                                    "vcsr_mc_fp32"};
+
+std::vector<std::string> split_algorithms(const std::string& list) {
+    std::vector<std::string> out;
+    size_t b = 0;
+    while (true) {
+        size_t e = list.find(',', b);
+        const std::string one = list.substr(b, e == std::string::npos ? std::string::npos : e - b);
+        bool known = false;
+        for (const char* k : kKernelNames) known |= one == k;
+        if (!known) throw std::runtime_error("Unknown algorithm: " + one);
+        out.push_back(one);
+        if (e == std::string::npos) return out;
+        b = e + 1;
+    }
 }
 
-void usage() {
+void print_usage() {
     std::printf(
         "Usage: spmm_vcsr (--mtx file.mtx | --gen K[:size]) --O 128 [options]\n"
-        "Algorithms: rocsparse, rocsparse_fp16, vcsr_mc (FP16 inputs, MFMA), vcsr_mc_fp32\n"
+        "Algorithms: rocsparse, rocsparse_fp16 (FP16 A and B, FP32 compute and C),\n"
+        "            vcsr_mc (FP16 inputs, MFMA), vcsr_mc_fp32 (FP32 operands, FP32 MFMA)\n"
         "Options: --segw 16 --tileK 64 --repeat 10 --warmup 3 --stat mean|median\n"
         "         --reorder none|rcm --check cpu|rocsparse|none --csv --help\n"
         "         --bdist pattern|normal|uniform|wide   (B fill; random ones use a fixed seed)\n"
         "         --lenient   record a failed correctness check as FAIL instead of aborting\n"
         "         --gen K[:size]  seeded synthetic workload K = 1..5 instead of --mtx\n"
+        "         --dump-csr PATH  write the CSR as read (PATH - = stdout) and stop\n"
         "tileK must be one of 16, 32, 64, 128.\n");
 }
 
-int run(int argc, char** argv) {
-    std::string mtx, gen, algo = "all", check = "rocsparse", reorder = "none", bdist = "pattern",
-                                stat = "mean";
-    int O = 128, segw = 16, tileK = 64, repeat = 10, warmup = 3;
-    constexpr int bundle = 16;
-    bool csv = false, lenient = false;
-    static option opts[] = {
-        {"mtx", required_argument, nullptr, 'm'},    {"gen", required_argument, nullptr, 'g'},
-        {"O", required_argument, nullptr, 'o'},      {"segw", required_argument, nullptr, 's'},
-        {"tileK", required_argument, nullptr, 't'},  {"repeat", required_argument, nullptr, 'r'},
-        {"warmup", required_argument, nullptr, 'w'}, {"reorder", required_argument, nullptr, 'R'},
-        {"algo", required_argument, nullptr, 'a'},   {"check", required_argument, nullptr, 'c'},
-        {"csv", no_argument, nullptr, 'j'},          {"help", no_argument, nullptr, 'h'},
-        {"bdist", required_argument, nullptr, 'D'},  {"lenient", no_argument, nullptr, 'L'},
-        {"stat", required_argument, nullptr, 'S'},   {nullptr, 0, nullptr, 0}};
-    int opt;
-    while ((opt = getopt_long(argc, argv, "", opts, nullptr)) != -1) {
-        switch (opt) {
-            case 'm': mtx = optarg; break;
-            case 'g': gen = optarg; break;
-            case 'o': O = int_at_least(optarg, 1); break;
-            case 's': segw = int_at_least(optarg, 1); break;
-            case 't': tileK = int_at_least(optarg, 1); break;
-            case 'r': repeat = int_at_least(optarg, 1); break;
-            case 'w': warmup = int_at_least(optarg, 0); break;
-            case 'R': reorder = optarg; break;
-            case 'a': algo = optarg; break;
-            case 'c': check = optarg; break;
-            case 'D': bdist = optarg; break;
-            case 'L': lenient = true; break;
-            case 'S': stat = optarg; break;
-            case 'j': csv = true; break;
-            case 'h': usage(); return 0;
-            default: usage(); return 2;
+// Returns false when the command line asks for usage with exit status 2.
+bool parse_options(int argc, char** argv, Options& o) {
+    enum { kMtx = 256, kGen, kO, kSegw, kTileK, kRepeat, kWarmup, kReorder, kAlgo, kCheck, kCsv,
+           kHelp, kBdist, kLenient, kStat, kDump };
+    static const option table[] = {
+        {"mtx", required_argument, nullptr, kMtx},        {"gen", required_argument, nullptr, kGen},
+        {"O", required_argument, nullptr, kO},            {"segw", required_argument, nullptr, kSegw},
+        {"tileK", required_argument, nullptr, kTileK},    {"repeat", required_argument, nullptr, kRepeat},
+        {"warmup", required_argument, nullptr, kWarmup},  {"reorder", required_argument, nullptr, kReorder},
+        {"algo", required_argument, nullptr, kAlgo},      {"check", required_argument, nullptr, kCheck},
+        {"csv", no_argument, nullptr, kCsv},              {"help", no_argument, nullptr, kHelp},
+        {"bdist", required_argument, nullptr, kBdist},    {"lenient", no_argument, nullptr, kLenient},
+        {"stat", required_argument, nullptr, kStat},      {"dump-csr", required_argument, nullptr, kDump},
+        {nullptr, 0, nullptr, 0}};
+    for (int c; (c = getopt_long(argc, argv, "", table, nullptr)) != -1;) {
+        switch (c) {
+            case kMtx: o.mtx = optarg; break;
+            case kGen: o.gen = optarg; break;
+            case kO: o.O = parse_int(optarg, 1); break;
+            case kSegw: o.segw = parse_int(optarg, 1); break;
+            case kTileK: o.tileK = parse_int(optarg, 1); break;
+            case kRepeat: o.repeat = parse_int(optarg, 1); break;
+            case kWarmup: o.warmup = parse_int(optarg, 0); break;
+            case kReorder: o.reorder = optarg; break;
+            case kAlgo: o.algo = optarg; break;
+            case kCheck: o.check = optarg; break;
+            case kCsv: o.csv = true; break;
+            case kHelp: o.help = true; return true;
+            case kBdist: o.bdist = optarg; break;
+            case kLenient: o.lenient = true; break;
+            case kStat: o.stat = optarg; break;
+            case kDump: o.dump_csr = optarg; break;
+            default: return false;
         }
     }
-    const std::vector<std::string> known = {"all", "rocsparse", "rocsparse_fp16", "vcsr_mc",
-                                            "vcsr_mc_fp32"};
-    std::vector<std::string> want;
-    for (size_t pos = 0;;) {
-        const size_t comma = algo.find(',', pos);
-        const std::string one = algo.substr(pos, comma == std::string::npos ? std::string::npos
-                                                                              : comma - pos);
-        if (one.empty() || std::find(known.begin(), known.end(), one) == known.end())
-            throw std::runtime_error("Unknown algorithm: " + one);
-        want.push_back(one);
-        if (comma == std::string::npos) break;
-        pos = comma + 1;
-    }
-    const bool all = std::find(want.begin(), want.end(), "all") != want.end();
-    auto selected = [&](const char* n) {
-        return all || std::find(want.begin(), want.end(), n) != want.end();
-    };
-    if (check != "cpu" && check != "rocsparse" && check != "none")
-        throw std::runtime_error("Unknown reference: " + check);
-    if ((mtx.empty() == gen.empty()) || optind != argc) { usage(); return 2; }
-    if (reorder != "none" && reorder != "rcm")
-        throw std::runtime_error("Unknown reordering: " + reorder);
-    if (stat != "mean" && stat != "median")
-        throw std::runtime_error("Unknown --stat: " + stat + " (mean|median)");
-    if (tileK != 16 && tileK != 32 && tileK != 64 && tileK != 128)
+    o.kernels = split_algorithms(o.algo);
+    if (o.check != "cpu" && o.check != "rocsparse" && o.check != "none")
+        throw std::runtime_error("Unknown reference: " + o.check);
+    if (o.mtx.empty() == o.gen.empty() || optind != argc) return false;
+    if (o.reorder != "none" && o.reorder != "rcm")
+        throw std::runtime_error("Unknown reordering: " + o.reorder);
+    if (o.stat != "mean" && o.stat != "median")
+        throw std::runtime_error("Unknown --stat: " + o.stat + " (mean|median)");
+    if (o.tileK != 16 && o.tileK != 32 && o.tileK != 64 && o.tileK != 128)
         throw std::runtime_error("tileK must be one of 16, 32, 64, 128");
+    return true;
+}
 
-    CSR csr = mtx.empty() ? generated(gen) : to_csr(read_mtx(mtx));
-    const std::string name = mtx.empty() ? "gen:" + gen : mtx;
-    if ((size_t)csr.N * O > INT_MAX || (size_t)csr.M * O > INT_MAX || segw > INT_MAX - csr.N + 1 ||
-        tileK > INT_MAX - O + 1)
-        throw std::runtime_error("Dimensions exceed the kernels' 32-bit indexing limit");
-    hipDeviceProp_t prop{};
-    int dev = 0;
-    hip_ok(hipGetDevice(&dev), "hipGetDevice");
-    hip_ok(hipGetDeviceProperties(&prop, dev), "hipGetDeviceProperties");
-    const size_t nB = (size_t)csr.N * O, nC = (size_t)csr.M * O;
+bool wants(const Options& o, const char* name) {
+    for (const std::string& k : o.kernels)
+        if (k == "all" || k == name) return true;
+    return false;
+}
 
-    // B fill (src/main.cpp:161-179): the same generator and distributions, seed 20260923.
-    std::vector<float> hB(nB);
-    if (bdist == "pattern") {
-        for (size_t i = 0; i < nB; ++i) hB[i] = float(int(i % 13) - 6) / 7.f;
+// ---- input ---------------------------------------------------------------------------------
+CSR synthetic_csr(const std::string& spec) {
+    const size_t colon = spec.find(':');
+    const int config = parse_int(spec.substr(0, colon).c_str(), 1);
+    const int size = colon == std::string::npos ? 0 : parse_int(spec.c_str() + colon + 1, 0);
+    vcsrmc_matrix_t m = nullptr;
+    if (vcsrmc_gen(config, size, 20260923ULL + (unsigned)config, &m) != 0)
+        throw std::runtime_error("Unknown or failed --gen workload: " + spec);
+    std::unique_ptr<vcsrmc_matrix_s, int (*)(vcsrmc_matrix_t)> guard(m, vcsrmc_gen_free);
+    CSR a;
+    long long nnz = 0;
+    vcsrmc_gen_info(m, &a.M, &a.N, &nnz);
+    a.nnz = (int)nnz;
+    a.row_ptr.resize((size_t)a.M + 1);
+    a.col.resize((size_t)a.nnz);
+    a.val.resize((size_t)a.nnz);
+    vcsrmc_gen_copy(m, a.row_ptr.data(), a.col.data(), a.val.data());
+    return a;
+}
+
+// The CSR as text: "OK M N nnz", then row_ptr, col, and the values' bit patterns, one line each.
+void dump_csr(const CSR& a, const std::string& path) {
+    std::FILE* f = path == "-" ? stdout : std::fopen(path.c_str(), "w");
+    if (!f) throw std::runtime_error("Cannot write " + path);
+    std::fprintf(f, "OK %d %d %d\n", a.M, a.N, a.nnz);
+    for (int x : a.row_ptr) std::fprintf(f, "%d ", x);
+    std::fprintf(f, "\n");
+    for (int x : a.col) std::fprintf(f, "%d ", x);
+    std::fprintf(f, "\n");
+    for (float v : a.val) {
+        uint32_t u;
+        std::memcpy(&u, &v, sizeof u);
+        std::fprintf(f, "%08x ", u);
+    }
+    std::fprintf(f, "\n");
+    if (f != stdout) std::fclose(f);
+}
+
+// Dense B, row-major N x O (src/main.cpp:161-179): "pattern" cycles 13 values in [-6/7, 6/7];
+// the random fills draw from one std::mt19937_64 seeded 20260923 in element order.
+std::vector<float> make_b(size_t n, const std::string& dist) {
+    std::vector<float> b(n);
+    if (dist == "pattern") {
+        for (size_t i = 0; i < n; ++i) b[i] = (float)((int)(i % 13) - 6) / 7.0f;
+        return b;
+    }
+    std::mt19937_64 gen(20260923);
+    if (dist == "normal") {
+        std::normal_distribution<float> d(0.0f, 1.0f);
+        std::generate(b.begin(), b.end(), [&] { return d(gen); });
+    } else if (dist == "uniform") {
+        std::uniform_real_distribution<float> d(-1.0f, 1.0f);
+        std::generate(b.begin(), b.end(), [&] { return d(gen); });
+    } else if (dist == "wide") {
+        std::uniform_real_distribution<float> exponent(-3.0f, 3.0f);
+        std::bernoulli_distribution negative(0.5);
+        std::generate(b.begin(), b.end(), [&] {
+            const float s = negative(gen) ? -1.0f : 1.0f;  // sign drawn before the magnitude
+            return s * std::pow(10.0f, exponent(gen));
+        });
     } else {
-        std::mt19937_64 rng(20260923);
-        if (bdist == "normal") {
-            std::normal_distribution<float> d(0.f, 1.f);
-            for (float& x : hB) x = d(rng);
-        } else if (bdist == "uniform") {
-            std::uniform_real_distribution<float> d(-1.f, 1.f);
-            for (float& x : hB) x = d(rng);
-        } else if (bdist == "wide") {
-            std::uniform_real_distribution<float> e(-3.f, 3.f);
-            std::bernoulli_distribution sgn(0.5);
-            for (float& x : hB) x = (sgn(rng) ? -1.f : 1.f) * std::pow(10.f, e(rng));
-        } else {
-            throw std::runtime_error("Unknown --bdist: " + bdist + " (pattern|normal|uniform|wide)");
-        }
+        throw std::runtime_error("Unknown --bdist: " + dist + " (pattern|normal|uniform|wide)");
+    }
+    return b;
+}
+
+// ---- device operands ------------------------------------------------------------------------
+template <typename T>
+class DeviceArray {
+public:
+    explicit DeviceArray(size_t n) : n_(n) { CUDA_CHECK(hipMalloc(&p_, std::max<size_t>(n, 1) * sizeof(T))); }
+    DeviceArray(const DeviceArray&) = delete;
+    DeviceArray& operator=(const DeviceArray&) = delete;
+    ~DeviceArray() { (void)hipFree(p_); }
+    T* get() const { return p_; }
+    size_t size() const { return n_; }
+    void upload(const T* h, size_t n) {
+        if (n) CUDA_CHECK(hipMemcpy(p_, h, n * sizeof(T), hipMemcpyHostToDevice));
+    }
+    std::vector<T> download() const {
+        std::vector<T> h(n_);
+        if (n_) CUDA_CHECK(hipMemcpy(h.data(), p_, n_ * sizeof(T), hipMemcpyDeviceToHost));
+        return h;
     }
 
-    // Relabelling A's columns and permuting B's rows to match leaves C = A B unchanged; done
-    // once, before every algorithm and the reference result (src/main.cpp:180-183).
-    if (reorder == "rcm" && csr.nnz) {
-        const auto t0 = std::chrono::steady_clock::now();
-        apply_column_permutation(csr, hB, O, rcm_column_order(csr));
-        const double ms =
-            std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
-        std::fprintf(stderr, "reorder rcm: %.1f ms (GPU ordering and relabelling, with copies)\n",
-                     ms);
-    }
+private:
+    T* p_ = nullptr;
+    size_t n_;
+};
 
-    float *dB = nullptr, *dC = nullptr, *dval = nullptr;
-    int *drp = nullptr, *dcol = nullptr;
-    hip_ok(hipMalloc(&dB, std::max<size_t>(nB, 1) * 4), "hipMalloc");
-    hip_ok(hipMalloc(&dC, std::max<size_t>(nC, 1) * 4), "hipMalloc");
-    hip_ok(hipMalloc(&drp, ((size_t)csr.M + 1) * 4), "hipMalloc");
-    hip_ok(hipMalloc(&dcol, std::max(csr.nnz, 1) * 4), "hipMalloc");
-    hip_ok(hipMalloc(&dval, std::max(csr.nnz, 1) * 4), "hipMalloc");
-    hip_ok(hipMemcpy(drp, csr.row_ptr.data(), ((size_t)csr.M + 1) * 4, hipMemcpyHostToDevice), "H2D");
-    if (csr.nnz) {
-        hip_ok(hipMemcpy(dcol, csr.col.data(), (size_t)csr.nnz * 4, hipMemcpyHostToDevice), "H2D");
-        hip_ok(hipMemcpy(dval, csr.val.data(), (size_t)csr.nnz * 4, hipMemcpyHostToDevice), "H2D");
+struct Operands {
+    const CSR& a;
+    int O;
+    hipStream_t stream = nullptr;
+    DeviceArray<int> row_ptr, col;
+    DeviceArray<float> val, B, C;
+    Operands(const CSR& csr, const std::vector<float>& hB, int O_)
+        : a(csr), O(O_), row_ptr((size_t)csr.M + 1), col((size_t)csr.nnz), val((size_t)csr.nnz),
+          B(hB.size()), C((size_t)csr.M * O_) {
+        row_ptr.upload(csr.row_ptr.data(), row_ptr.size());
+        col.upload(csr.col.data(), col.size());
+        val.upload(csr.val.data(), val.size());
+        B.upload(hB.data(), hB.size());
+        CUDA_CHECK(hipStreamCreate(&stream));
     }
-    hip_ok(hipMemcpy(dB, hB.data(), nB * 4, hipMemcpyHostToDevice), "H2D");
-    hipStream_t st;
-    hip_ok(hipStreamCreate(&st), "hipStreamCreate");
+    ~Operands() { (void)hipStreamDestroy(stream); }
+};
 
-    // Reference result (src/main.cpp:199-218).
-    std::vector<double> ref;
-    if (check != "none") ref.assign(nC, 0.0);
-    if (check == "cpu") {
-        for (int r = 0; r < csr.M; ++r)
-            for (int p = csr.row_ptr[r]; p < csr.row_ptr[r + 1]; ++p)
-                for (int k = 0; k < O; ++k)
-                    ref[(size_t)r * O + k] += (double)csr.val[p] * hB[(size_t)csr.col[p] * O + k];
-    } else if (check == "rocsparse" && csr.nnz) {
-        hip_ok(hipMemset(dC, 0, nC * 4), "hipMemset");
+// ---- kernels ---------------------------------------------------------------------------------
+// One algorithm of the driver: launch() runs one SpMM into C (C zeroed before) and returns its
+// event-timed milliseconds; setup / convert / upload are reported beside the timing.
+struct Kernel {
+    const char* name;
+    bool half_inputs;  // FP16 operands: the looser validation bound
+    double setup_ms = 0, convert_ms = 0, upload_ms = 0;
+    Kernel(const char* n, bool h) : name(n), half_inputs(h) {}
+    virtual ~Kernel() = default;
+    virtual float launch(Operands& d) = 0;
+};
+
+struct RocsparseKernel : Kernel {
+    RocsparseKernel() : Kernel("rocsparse", false) {}
+    float launch(Operands& d) override {
         float ms = 0, setup = 0;
-        if (vcsrmc_rocsparse_spmm(csr.M, csr.N, csr.nnz, drp, dcol, dval, 0, dB, 0, O, dC, 1.f, 0,
-                                  st, &ms, &setup) != 0)
-            throw std::runtime_error("hipSPARSE reference failed");
-        std::vector<float> res(nC);
-        hip_ok(hipMemcpy(res.data(), dC, nC * 4, hipMemcpyDeviceToHost), "D2H");
-        ref.assign(res.begin(), res.end());
+        if (vcsrmc_rocsparse_spmm(d.a.M, d.a.N, d.a.nnz, d.row_ptr.get(), d.col.get(),
+                                  d.val.get(), 0, d.B.get(), 0, d.O, d.C.get(), 1.0f, 0, d.stream,
+                                  &ms, &setup) != 0)
+            throw std::runtime_error("hipSPARSE SpMM failed");
+        setup_ms = setup;
+        return ms;
     }
-    for (double v : ref)
-        if (!std::isfinite(v)) throw std::runtime_error("Reference contains non-finite values");
+};
 
-    if (csv)
-        std::printf("gpu,sm,mtx,O,segw,bundle,tileK,repeat,algo,ms,gflops,validation,rel_l2,"
-                    "setup_ms,ms_mean,ms_median,convert_ms,upload_ms\n");
-    else
+// FP16 A (divided by half_scale, undone through alpha) and FP16 B, FP32 compute and C; the
+// copies are made once, outside the timing (src/main.cpp:314-340).
+struct RocsparseFp16Kernel : Kernel {
+    std::unique_ptr<DeviceArray<_Float16>> val16, b16;
+    float scale = 1.0f;
+    double lib_setup = 0;
+    RocsparseFp16Kernel(const CSR& a, const std::vector<float>& hB) : Kernel("rocsparse_fp16", true) {
+        scale = half_scale(a);
+        const float inv = 1.0f / scale;
+        std::vector<_Float16> v16, h16;
+        auto t0 = Clock::now();
+        v16.resize(a.val.size());
+        h16.resize(hB.size());
+        std::transform(a.val.begin(), a.val.end(), v16.begin(),
+                       [inv](float v) { return (_Float16)(v * inv); });
+        std::transform(hB.begin(), hB.end(), h16.begin(), [](float v) { return (_Float16)v; });
+        convert_ms = ms_since(t0);
+        t0 = Clock::now();
+        val16 = std::make_unique<DeviceArray<_Float16>>(v16.size());
+        b16 = std::make_unique<DeviceArray<_Float16>>(h16.size());
+        val16->upload(v16.data(), v16.size());
+        b16->upload(h16.data(), h16.size());
+        upload_ms = ms_since(t0);
+    }
+    float launch(Operands& d) override {
+        float ms = 0, setup = 0;
+        if (vcsrmc_rocsparse_spmm(d.a.M, d.a.N, d.a.nnz, d.row_ptr.get(), d.col.get(),
+                                  val16->get(), 1, b16->get(), 1, d.O, d.C.get(), scale, 0,
+                                  d.stream, &ms, &setup) != 0)
+            throw std::runtime_error("hipSPARSE FP16 SpMM failed");
+        lib_setup = setup;
+        setup_ms = convert_ms + upload_ms + lib_setup;
+        return ms;
+    }
+};
+
+// The drop-in surface, as the reference's driver calls it (src/main.cpp:356-361).
+struct VcsrKernel : Kernel {
+    VCSRMC V;
+    int tileK;
+    VcsrKernel(const CSR& a, bool fp32, int segw, int tileK_)
+        : Kernel(fp32 ? "vcsr_mc_fp32" : "vcsr_mc", !fp32), tileK(tileK_) {
+        auto t0 = Clock::now();
+        V = csr_to_vcsr_mc(a, fp32, segw);
+        convert_ms = ms_since(t0);
+        t0 = Clock::now();
+        upload_vcsr_mc_device(V);
+        upload_ms = ms_since(t0);
+        setup_ms = convert_ms + upload_ms;
+    }
+    ~VcsrKernel() override { destroy_vcsr_mc_device(nullptr); }
+    float launch(Operands& d) override {
+        float ms = 0;
+        run_vcsr_mc_spmm_gpu(V, d.B.get(), d.O, tileK, d.C.get(), d.stream, ms);
+        return ms;
+    }
+};
+
+// ---- protocol, validation, report -----------------------------------------------------------
+// `warmup` discarded launches, then `repeat` timed ones; C is zeroed and the stream drained
+// before each (src/main.cpp:241-256).
+std::vector<double> time_launches(Kernel& k, Operands& d, int warmup, int repeat) {
+    std::vector<double> t;
+    for (int i = 0; i < warmup + repeat; ++i) {
+        CUDA_CHECK(hipMemsetAsync(d.C.get(), 0, d.C.size() * sizeof(float), d.stream));
+        CUDA_CHECK(hipStreamSynchronize(d.stream));
+        const float ms = d.a.nnz ? k.launch(d) : 0.0f;
+        CUDA_CHECK(hipGetLastError());
+        CUDA_CHECK(hipStreamSynchronize(d.stream));
+        if (!(ms >= 0.0f) || std::isinf(ms)) throw std::runtime_error("Invalid kernel timing");
+        if (i >= warmup) t.push_back(ms);
+    }
+    return t;
+}
+
+struct Verdict {
+    double rel_l2 = 0;
+    bool failed = false;
+};
+
+// Relative L2 error of C against the reference, and the reference's two-sided bound
+// (src/main.cpp:257-291): error <= tol_rel * ||ref|| + 1e-5 sqrt(|C|) and rel_l2 <= cap, with
+// (tol_rel, cap) = (3e-3, 1e-1) for FP16 inputs, (1e-4, 1e-2) otherwise.  A non-finite output,
+// or a result outside the bound, aborts unless lenient (then FAIL).
+Verdict validate(const Kernel& k, const std::vector<float>& got, const std::vector<double>& ref,
+                 bool lenient) {
+    Verdict v;
+    double err2 = 0, ref2 = 0;
+    for (size_t i = 0; i < got.size(); ++i) {
+        if (!std::isfinite(got[i])) {
+            if (!lenient) throw std::runtime_error(std::string(k.name) + ": non-finite output");
+            v.rel_l2 = INFINITY;
+            v.failed = true;
+            return v;
+        }
+        const double e = (double)got[i] - ref[i];
+        err2 += e * e;
+        ref2 += ref[i] * ref[i];
+    }
+    const double err = std::sqrt(err2), norm = std::sqrt(ref2);
+    v.rel_l2 = norm > 0 ? err / norm : err;
+    const double tol_rel = k.half_inputs ? 3e-3 : 1e-4, cap = k.half_inputs ? 1e-1 : 1e-2;
+    const double bound = tol_rel * norm + 1e-5 * std::sqrt((double)got.size());
+    if (err > bound || v.rel_l2 > cap) {
+        if (!lenient)
+            throw std::runtime_error(std::string(k.name) + ": correctness check failed, rel_l2=" +
+                                     std::to_string(v.rel_l2));
+        v.failed = true;
+    }
+    return v;
+}
+
+std::string csv_field(const std::string& s) {
+    std::string q = "\"";
+    for (char ch : s) q += ch == '"' ? std::string("\"\"") : std::string(1, ch);
+    return q + "\"";
+}
+
+struct Report {
+    const Options& o;
+    const CSR& a;
+    std::string source, device;
+    int sm = 0;
+
+    void header() const {
+        if (o.csv) {
+            std::printf("gpu,sm,mtx,O,segw,bundle,tileK,repeat,algo,ms,gflops,validation,rel_l2,"
+                        "setup_ms,ms_mean,ms_median,convert_ms,upload_ms\n");
+            return;
+        }
         std::printf("Matrix: %d x %d, nnz=%d; O=%d segw=%d bundle=%d tileK=%d repeat=%d warmup=%d "
-                    "reorder=%s; reference=%s\nKernel                Time (ms)      GFLOP/s   "
-                    "Validation\n",
-                    csr.M, csr.N, csr.nnz, O, segw, bundle, tileK, repeat, warmup, reorder.c_str(),
-                    check.c_str());
-    auto wall_ms = [](auto&& f) {
-        const auto t0 = std::chrono::steady_clock::now();
-        f();
-        return std::chrono::duration<float, std::milli>(std::chrono::steady_clock::now() - t0)
-            .count();
-    };
+                    "reorder=%s; reference=%s\n",
+                    a.M, a.N, a.nnz, o.O, o.segw, 16, o.tileK, o.repeat, o.warmup,
+                    o.reorder.c_str(), o.check.c_str());
+        std::printf("Kernel                Time (ms)      GFLOP/s   Validation\n");
+    }
 
-    // measure (src/main.cpp:239-308)
-    auto measure = [&](const char* kname, const std::function<void(float&)>& launch,
-                       const float& setup_ms, float convert_ms = 0.f, float upload_ms = 0.f) {
-        auto iterate = [&]() {
-            hip_ok(hipMemsetAsync(dC, 0, nC * 4, st), "hipMemsetAsync");
-            hip_ok(hipStreamSynchronize(st), "sync");
-            float ms = 0;
-            if (csr.nnz) launch(ms);
-            hip_ok(hipGetLastError(), "launch");
-            hip_ok(hipStreamSynchronize(st), "sync");
-            if (!std::isfinite(ms) || ms < 0) throw std::runtime_error("Invalid kernel timing");
-            return (double)ms;
-        };
-        for (int i = 0; i < warmup; ++i) iterate();
-        std::vector<double> t(repeat);
-        for (double& x : t) x = iterate();
-        double rel = 0;
-        bool failed = false;
-        if (check != "none") {
-            std::vector<float> res(nC);
-            hip_ok(hipMemcpy(res.data(), dC, nC * 4, hipMemcpyDeviceToHost), "D2H");
-            double e2 = 0, r2 = 0;
-            bool nonfinite = false;
-            for (size_t i = 0; i < nC; ++i) {
-                if (!std::isfinite(res[i])) {
-                    if (!lenient) throw std::runtime_error(std::string(kname) + ": non-finite output");
-                    nonfinite = true;
-                    break;
-                }
-                const double d = (double)res[i] - ref[i];
-                e2 += d * d;
-                r2 += ref[i] * ref[i];
-            }
-            const double err = std::sqrt(e2), norm = std::sqrt(r2);
-            rel = norm > 0 ? err / norm : err;
-            if (nonfinite) { rel = INFINITY; failed = true; }
-            const std::string kn(kname);
-            const bool half = kn == "vcsr_mc" || kn == "rocsparse_fp16";
-            const double tol = (half ? 3e-3 : 1e-4) * norm + 1e-5 * std::sqrt((double)nC);
-            if (!nonfinite && (err > tol || rel > (half ? 1e-1 : 1e-2))) {
-                if (!lenient)
-                    throw std::runtime_error(std::string(kname) +
-                                             ": correctness check failed, rel_l2=" +
-                                             std::to_string(rel));
-                failed = true;
+    void row(const Kernel& k, std::vector<double> t, const Verdict& v) const {
+        double sum = 0;
+        for (double x : t) sum += x;
+        const double mean = sum / (double)t.size();
+        std::sort(t.begin(), t.end());
+        const size_t h = t.size() / 2;
+        const double median = t.size() % 2 ? t[h] : 0.5 * (t[h - 1] + t[h]);
+        const double ms = o.stat == "median" ? median : mean;
+        const double gflops = ms > 0 ? 2.0 * (double)a.nnz * o.O / (ms * 1e6) : 0.0;
+        const char* verdict = o.check == "none" ? "unchecked" : v.failed ? "FAIL" : "pass";
+        if (o.csv)
+            std::printf("%s,%d,%s,%d,%d,%d,%d,%d,%s,%.9g,%.9g,%s,%.9g,%.6g,%.9g,%.9g,%.6g,%.6g\n",
+                        csv_field(device).c_str(), sm, csv_field(source).c_str(), o.O, o.segw, 16,
+                        o.tileK, o.repeat, k.name, ms, gflops, verdict, v.rel_l2, k.setup_ms, mean,
+                        median, k.convert_ms, k.upload_ms);
+        else
+            std::printf("%-20s %10.6f %12.2f   %s (rel_l2=%.3g, setup %.3f ms)\n", k.name, ms,
+                        gflops, verdict, v.rel_l2, k.setup_ms);
+        std::fflush(stdout);
+    }
+};
+
+// ---- the run --------------------------------------------------------------------------------
+int run(int argc, char** argv) {
+    Options o;
+    if (!parse_options(argc, argv, o)) {
+        print_usage();
+        return 2;
+    }
+    if (o.help) {
+        print_usage();
+        return 0;
+    }
+    CSR a = o.mtx.empty() ? synthetic_csr(o.gen) : coo_to_csr(read_matrix_market_coo(o.mtx));
+    if (!o.dump_csr.empty()) {
+        dump_csr(a, o.dump_csr);
+        return 0;
+    }
+    // The kernels index B and C with 32-bit offsets.
+    if ((size_t)a.N * o.O > INT_MAX || (size_t)a.M * o.O > INT_MAX ||
+        o.segw > INT_MAX - a.N + 1 || o.tileK > INT_MAX - o.O + 1)
+        throw std::runtime_error("Dimensions exceed the kernels' 32-bit indexing limit");
+    std::vector<float> hB = make_b((size_t)a.N * o.O, o.bdist);
+    int dev = 0;
+    hipDeviceProp_t prop{};
+    CUDA_CHECK(hipGetDevice(&dev));
+    CUDA_CHECK(hipGetDeviceProperties(&prop, dev));
+
+    // Relabelling A's columns and permuting B's rows to match leaves A.B unchanged; done once,
+    // before every kernel and the reference result (src/main.cpp:180-183).
+    if (o.reorder == "rcm" && a.nnz) {
+        const auto t0 = Clock::now();
+        apply_column_permutation(a, hB, o.O, rcm_column_order(a));
+        std::fprintf(stderr, "reorder rcm: %.1f ms (GPU ordering and relabelling, with copies)\n",
+                     ms_since(t0));
+    }
+    Operands d(a, hB, o.O);
+
+    // Reference result, outside every timing (src/main.cpp:199-218).
+    std::vector<double> ref;
+    if (o.check == "cpu") {
+        ref.assign((size_t)a.M * o.O, 0.0);
+        for (int r = 0; r < a.M; ++r) {
+            double* out = &ref[(size_t)r * o.O];
+            for (int p = a.row_ptr[r]; p < a.row_ptr[r + 1]; ++p) {
+                const double v = a.val[p];
+                const float* brow = &hB[(size_t)a.col[p] * o.O];
+                for (int k = 0; k < o.O; ++k) out[k] += v * brow[k];
             }
         }
-        const double mean = std::accumulate(t.begin(), t.end(), 0.0) / repeat;
-        std::sort(t.begin(), t.end());
-        const double median = repeat % 2 ? t[repeat / 2] : 0.5 * (t[repeat / 2 - 1] + t[repeat / 2]);
-        const double ms = stat == "median" ? median : mean;
-        const double gflops = ms > 0 ? 2.0 * csr.nnz * O / (ms * 1e6) : 0;
-        const char* val = check == "none" ? "unchecked" : failed ? "FAIL" : "pass";
-        if (csv)
-            std::printf("%s,%d,%s,%d,%d,%d,%d,%d,%s,%.9g,%.9g,%s,%.9g,%.6g,%.9g,%.9g,%.6g,%.6g\n",
-                        quote(prop.name).c_str(), prop.major * 10 + prop.minor, quote(name).c_str(),
-                        O, segw, bundle, tileK, repeat, kname, ms, gflops, val, rel, setup_ms,
-                        mean, median, convert_ms, upload_ms);
-        else
-            std::printf("%-20s %10.6f %12.2f   %s (rel_l2=%.3g, setup %.3f ms)\n", kname, ms, gflops,
-                        val, rel, setup_ms);
-        std::fflush(stdout);
-    };
+    } else if (o.check == "rocsparse") {
+        ref.assign((size_t)a.M * o.O, 0.0);
+        if (a.nnz) {
+            CUDA_CHECK(hipMemset(d.C.get(), 0, d.C.size() * sizeof(float)));
+            RocsparseKernel().launch(d);
+            CUDA_CHECK(hipStreamSynchronize(d.stream));
+            const std::vector<float> c = d.C.download();
+            std::copy(c.begin(), c.end(), ref.begin());
+        }
+    }
+    if (std::any_of(ref.begin(), ref.end(), [](double x) { return !std::isfinite(x); }))
+        throw std::runtime_error("Reference contains non-finite values");
 
-    if (selected("rocsparse")) {
-        float setup = 0.f;
-        measure("rocsparse", [&](float& ms) {
-            if (vcsrmc_rocsparse_spmm(csr.M, csr.N, csr.nnz, drp, dcol, dval, 0, dB, 0, O, dC, 1.f,
-                                      0, st, &ms, &setup) != 0)
-                throw std::runtime_error("hipSPARSE SpMM failed");
-        }, setup);
+    Report rep{o, a, o.mtx.empty() ? "gen:" + o.gen : o.mtx, prop.name, prop.major * 10 + prop.minor};
+    rep.header();
+    auto measure = [&](Kernel& k) {
+        const std::vector<double> t = time_launches(k, d, o.warmup, o.repeat);
+        const Verdict v = o.check == "none" ? Verdict{} : validate(k, d.C.download(), ref, o.lenient);
+        rep.row(k, t, v);
+    };
+    if (wants(o, "rocsparse")) {
+        RocsparseKernel k;
+        measure(k);
     }
-    if (selected("rocsparse_fp16")) {
-        // FP16 A (range-scaled) and B, FP32 compute and C; copies made outside the timing
-        // (src/main.cpp:314-340).
-        const float scale = half_scale(csr), inv = 1.f / scale;
-        std::vector<_Float16> v16, b16;
-        const float convert = wall_ms([&] {
-            v16.resize(csr.nnz);
-            b16.resize(nB);
-            for (int i = 0; i < csr.nnz; ++i) v16[i] = (_Float16)(csr.val[i] * inv);
-            for (size_t i = 0; i < nB; ++i) b16[i] = (_Float16)hB[i];
-        });
-        void *dv16 = nullptr, *db16 = nullptr;
-        const float upload = wall_ms([&] {
-            hip_ok(hipMalloc(&dv16, std::max(csr.nnz, 1) * 2), "hipMalloc");
-            hip_ok(hipMalloc(&db16, std::max<size_t>(nB, 1) * 2), "hipMalloc");
-            if (csr.nnz) hip_ok(hipMemcpy(dv16, v16.data(), (size_t)csr.nnz * 2, hipMemcpyHostToDevice), "H2D");
-            hip_ok(hipMemcpy(db16, b16.data(), nB * 2, hipMemcpyHostToDevice), "H2D");
-        });
-        float lib = 0.f, setup = 0.f;
-        measure("rocsparse_fp16", [&](float& ms) {
-            if (vcsrmc_rocsparse_spmm(csr.M, csr.N, csr.nnz, drp, dcol, dv16, 1, db16, 1, O, dC,
-                                      scale, 0, st, &ms, &lib) != 0)
-                throw std::runtime_error("hipSPARSE FP16 SpMM failed");
-            setup = convert + upload + lib;
-        }, setup, convert, upload);
-        hip_ok(hipFree(dv16), "hipFree");
-        hip_ok(hipFree(db16), "hipFree");
+    if (wants(o, "rocsparse_fp16")) {
+        RocsparseFp16Kernel k(a, hB);
+        measure(k);
     }
-    // VCSR-MC through the drop-in surface (src/main.cpp:345-362).
     for (const bool fp32 : {false, true}) {
-        const char* kname = fp32 ? "vcsr_mc_fp32" : "vcsr_mc";
-        if (!selected(kname)) continue;
-        if (segw != 16 && segw != 32 && segw != 48 && segw != 64) {
-            std::fprintf(stderr, "Skipping %s: needs segw in {16,32,48,64}\n", kname);
+        const char* name = fp32 ? "vcsr_mc_fp32" : "vcsr_mc";
+        if (!wants(o, name)) continue;
+        if (o.segw != 16 && o.segw != 32 && o.segw != 48 && o.segw != 64) {
+            std::fprintf(stderr, "Skipping %s: needs segw in {16,32,48,64}\n", name);
             continue;
         }
-        VCSRMC V;
-        const float convert = wall_ms([&] { V = csr_to_vcsr_mc(csr, fp32, segw); });
-        const float upload = wall_ms([&] { upload_vcsr_mc_device(V); });
-        measure(kname, [&](float& ms) { run_vcsr_mc_spmm_gpu(V, dB, O, tileK, dC, st, ms); },
-                convert + upload, convert, upload);
-        destroy_vcsr_mc_device(st);
+        VcsrKernel k(a, fp32, o.segw, o.tileK);
+        measure(k);
     }
     vcsrmc_rocsparse_release();
-    hip_ok(hipStreamDestroy(st), "hipStreamDestroy");
-    hip_ok(hipFree(dB), "hipFree");
-    hip_ok(hipFree(dC), "hipFree");
-    hip_ok(hipFree(drp), "hipFree");
-    hip_ok(hipFree(dcol), "hipFree");
-    hip_ok(hipFree(dval), "hipFree");
     return 0;
 }
 
