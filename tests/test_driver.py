@@ -205,3 +205,14 @@ def test_lenient_records_nonfinite(tmp_path):
         assert rows[k]["validation"] == "FAIL" and rows[k]["rel_l2"] == "inf", rows[k]
     r = run(base + ["--algo", "vcsr_mc_fp32"])
     assert r.returncode == 2 and "Error: vcsr_mc_fp32: non-finite output" in r.stderr
+
+
+def test_write_mtx_round_trip(tmp_path):
+    """--write-mtx writes the input as a Matrix Market file whose CSR, read back, is the same
+    bit for bit (the timing comparison with the reference's driver reads these files)."""
+    p = tmp_path / "w.mtx"
+    for spec in ("2:3000", "4:40", "5:9"):
+        assert run(["--gen", spec, "--write-mtx", str(p)], timeout=120).returncode == 0
+        a = run(["--mtx", str(p), "--dump-csr", "-"], timeout=120)
+        b = run(["--gen", spec, "--dump-csr", "-"], timeout=120)
+        assert a.returncode == 0 and a.stdout == b.stdout, spec

@@ -336,6 +336,33 @@ def test_workloads_row_sample(orc, config):
     assert ok, f"row {rows[row]}: {worst:.3g}"
 
 
+@pytest.mark.parametrize("config", [1, 2, 3, 4, 5])
+def test_workloads_second_precision_row_sample(orc, config):
+    """The reference's driver runs both kernels on every matrix (src/main.cpp:345): each
+    workload at full size in the precision it is not configured for -- vcsr_mc_fp32 for the
+    FP16 workloads, vcsr_mc for the FP32 ones, fed FP32 B as the reference's
+    run_vcsr_mc_spmm_gpu is -- on a seeded sample of 2000 rows against the oracle."""
+    import torch
+    w = vm.WORKLOADS[config]
+    fp32 = w["precision"] != "fp32"
+    A = vm.generate(config, 0)
+    O = w["O"]
+    B = vm.dense(A.N, O, seed=vm.SEED_BASE + 200 + config)
+    say("workload second precision", config, A.M, A.nnz, O, "fp32" if fp32 else "fp16")
+    with vm.DeviceFormat.from_device_csr(dev(A.row_ptr), dev(A.col), dev(A.val), A.M, A.N,
+                                         fp32, 32) as f:
+        C = torch.zeros((A.M, O), dtype=torch.float32, device="cuda")
+        f.spmm(dev(B), C, tileK=128)
+        rows = np.sort(np.random.default_rng(100 + config).choice(A.M, size=min(A.M, 2000),
+                                                                  replace=False))
+        Cs = C[torch.from_numpy(rows).cuda()].cpu().numpy()
+        scale = f.info()["scale"]
+    srp, sc, sv = sub_csr(A.row_ptr, A.col, A.val, rows)
+    R, L1 = orc.spmm_csr(srp, sc, sv, len(rows), B, mode=0 if fp32 else 1, scale=scale)
+    ok, worst, row = row_l1_parity(Cs, R, L1, TAU[fp32])
+    assert ok, f"row {rows[row]}: {worst:.3g}"
+
+
 @pytest.mark.parametrize("config,tileK", [(1, 128), (2, 128), (3, 128), (4, 128), (4, 64),
                                            (2, 32)])
 def test_workloads_full_size_accumulate_twice(config, tileK):

@@ -45,7 +45,7 @@ double ms_since(Clock::time_point t0) {
 
 // ---- options ------------------------------------------------------------------------------
 struct Options {
-    std::string mtx, gen, dump_csr;
+    std::string mtx, gen, dump_csr, write_mtx;
     std::string algo = "all", check = "rocsparse", reorder = "none", bdist = "pattern";
     std::string stat = "mean";
     int O = 128, segw = 16, tileK = 64, repeat = 10, warmup = 3;
@@ -93,13 +93,14 @@ void print_usage() {
         "         --lenient   record a failed correctness check as FAIL instead of aborting\n"
         "         --gen K[:size]  seeded synthetic workload K = 1..5 instead of --mtx\n"
         "         --dump-csr PATH  write the CSR as read (PATH - = stdout) and stop\n"
+        "         --write-mtx PATH write the input as a Matrix Market file and stop\n"
         "tileK must be one of 16, 32, 64, 128.\n");
 }
 
 // Returns false when the command line asks for usage with exit status 2.
 bool parse_options(int argc, char** argv, Options& o) {
     enum { kMtx = 256, kGen, kO, kSegw, kTileK, kRepeat, kWarmup, kReorder, kAlgo, kCheck, kCsv,
-           kHelp, kBdist, kLenient, kStat, kDump };
+           kHelp, kBdist, kLenient, kStat, kDump, kWriteMtx };
     static const option table[] = {
         {"mtx", required_argument, nullptr, kMtx},        {"gen", required_argument, nullptr, kGen},
         {"O", required_argument, nullptr, kO},            {"segw", required_argument, nullptr, kSegw},
@@ -109,7 +110,7 @@ bool parse_options(int argc, char** argv, Options& o) {
         {"csv", no_argument, nullptr, kCsv},              {"help", no_argument, nullptr, kHelp},
         {"bdist", required_argument, nullptr, kBdist},    {"lenient", no_argument, nullptr, kLenient},
         {"stat", required_argument, nullptr, kStat},      {"dump-csr", required_argument, nullptr, kDump},
-        {nullptr, 0, nullptr, 0}};
+        {"write-mtx", required_argument, nullptr, kWriteMtx}, {nullptr, 0, nullptr, 0}};
     for (int c; (c = getopt_long(argc, argv, "", table, nullptr)) != -1;) {
         switch (c) {
             case kMtx: o.mtx = optarg; break;
@@ -128,6 +129,7 @@ bool parse_options(int argc, char** argv, Options& o) {
             case kLenient: o.lenient = true; break;
             case kStat: o.stat = optarg; break;
             case kDump: o.dump_csr = optarg; break;
+            case kWriteMtx: o.write_mtx = optarg; break;
             default: return false;
         }
     }
@@ -186,6 +188,19 @@ void dump_csr(const CSR& a, const std::string& path) {
     }
     std::fprintf(f, "\n");
     if (f != stdout) std::fclose(f);
+}
+
+// The CSR as a general real Matrix Market file; 9 significant digits give back every float.
+void write_mtx(const CSR& a, const std::string& path) {
+    std::FILE* f = std::fopen(path.c_str(), "w");
+    if (!f) throw std::runtime_error("Cannot write " + path);
+    std::vector<char> buf(1 << 22);
+    std::setvbuf(f, buf.data(), _IOFBF, buf.size());
+    std::fprintf(f, "%%%%MatrixMarket matrix coordinate real general\n%d %d %d\n", a.M, a.N, a.nnz);
+    for (int r = 0; r < a.M; ++r)
+        for (int p = a.row_ptr[r]; p < a.row_ptr[r + 1]; ++p)
+            std::fprintf(f, "%d %d %.9g\n", r + 1, a.col[p] + 1, (double)a.val[p]);
+    if (std::fclose(f) != 0) throw std::runtime_error("Cannot write " + path);
 }
 
 // Dense B, row-major N x O (src/main.cpp:161-179): "pattern" cycles 13 values in [-6/7, 6/7];
@@ -456,6 +471,10 @@ int run(int argc, char** argv) {
     CSR a = o.mtx.empty() ? synthetic_csr(o.gen) : coo_to_csr(read_matrix_market_coo(o.mtx));
     if (!o.dump_csr.empty()) {
         dump_csr(a, o.dump_csr);
+        return 0;
+    }
+    if (!o.write_mtx.empty()) {
+        write_mtx(a, o.write_mtx);
         return 0;
     }
     // The kernels index B and C with 32-bit offsets.
