@@ -160,8 +160,11 @@ __device__ __forceinline__ void read_c_ahead(CAhead<TK, W>& ca, const int4& U, i
 // overwrite: power-law 36,692^2 14.4 -> 13.2 us, 32 x 32 blocks 174 -> 150 us, R-MAT scale 22
 // 2.46 -> 2.39 ms, 27-point stencil within 1%).  An accumulating launch has just read the line,
 // and keeps ordinary stores (non-temporal measured 0-2% slower there).
-__device__ __forceinline__ void store_c4(float* p, const floatx4& v, bool accumulate) {
-    if (accumulate) *reinterpret_cast<floatx4*>(p) = v;
+// (ACC is a template parameter of the kernels: with a run-time flag the compiler merged the two
+// stores into one ordinary store.)
+template <bool ACC>
+__device__ __forceinline__ void store_c4(float* p, const floatx4& v) {
+    if constexpr (ACC) *reinterpret_cast<floatx4*>(p) = v;
     else __builtin_nontemporal_store(v, reinterpret_cast<floatx4*>(p));
 }
 
@@ -171,16 +174,41 @@ __device__ __forceinline__ void store_c4(float* p, const floatx4& v, bool accumu
 // threads on consecutive columns.  Split panels merge through atomics; other rows are a
 // read-modify-write (C += A.B) whose read, on the vector path, came from read_c_ahead.  Rows
 // outside the panel's row mask are never touched.
-template <int TK, int W>
+template <int TK, int W, bool ACC>
 __device__ __forceinline__ void merge_into_c(const floatx4 (&acc)[TK / 16], float scale,
                                              const int4& U, int k0, int O, bool c4,
-                                             bool accumulate, float* __restrict__ C, float* P,
+                                             float* __restrict__ C, float* P,
                                              const CAhead<TK, W>& ca) {
     constexpr int VEC = TK / 16;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, n = lane & 15, g = lane >> 4;
     const bool split = U.w & kUnitSplit;
     const long long OL = O;
     if constexpr (W == 1) {
+        if constexpr (!ACC) {
+            // Overwrite: non-temporal stores are not combined in L2, so each store instruction
+            // must cover whole lines.  The wave parks its tile in its slice of P and writes it
+            // back with consecutive lanes on consecutive 16-byte pieces (a 1 KB run per
+            // instruction), instead of from the accumulators, where one instruction covers
+            // every other 16 bytes of a row at O tiles of 128 (measured: written bytes 1.5x C).
+            if (!split && c4 && k0 + TK <= O) {
+                float* Pw = P + wave * 16 * TK;
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (int q = 0; q < VEC; ++q)
+                        Pw[(4 * g + i) * TK + VEC * n + q] = acc[q][i] * scale;
+                wave_lds_sync();
+#pragma unroll
+                for (int j = 0; j < 16 * TK / 256; ++j) {
+                    const int e = lane * 4 + 256 * j;
+                    const int row = e / TK, col = e % TK;
+                    if ((U.w >> row) & 1)
+                        store_c4<ACC>(C + (long long)(U.x + row) * OL + k0 + col,
+                                      *reinterpret_cast<const floatx4*>(Pw + e));
+                }
+                return;
+            }
+        }
         const int c0 = k0 + VEC * n;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -197,12 +225,12 @@ __device__ __forceinline__ void merge_into_c(const floatx4 (&acc)[TK / 16], floa
                     floatx4 v = ca.v[(i * (VEC / 4) + h / 4) % CAhead<TK, W>::N];
 #pragma unroll
                     for (int q = 0; q < 4; ++q) v[q] += acc[(h + q) % VEC][i] * scale;
-                    store_c4(crow + h, v, accumulate);
+                    store_c4<ACC>(crow + h, v);
                 }
             } else {
 #pragma unroll
                 for (int q = 0; q < VEC; ++q)
-                    if (c0 + q < O) crow[q] = (accumulate ? crow[q] : 0.0f) + acc[q][i] * scale;
+                    if (c0 + q < O) crow[q] = (ACC ? crow[q] : 0.0f) + acc[q][i] * scale;
             }
         }
     } else {
@@ -234,11 +262,11 @@ __device__ __forceinline__ void merge_into_c(const floatx4 (&acc)[TK / 16], floa
             } else if (c4 && cc + 4 <= O) {
                 floatx4 v = ca.v[j];
                 v += sum * scale;
-                store_c4(crow, v, accumulate);
+                store_c4<ACC>(crow, v);
             } else {
 #pragma unroll
                 for (int jj = 0; jj < 4; ++jj)
-                    if (cc + jj < O) crow[jj] = (accumulate ? crow[jj] : 0.0f) + sum[jj] * scale;
+                    if (cc + jj < O) crow[jj] = (ACC ? crow[jj] : 0.0f) + sum[jj] * scale;
             }
         }
     }
@@ -405,13 +433,13 @@ __device__ __forceinline__ void tiles_f16(int first, int end, int W, int lane, i
 template <typename TB, bool ALIGNED>
 constexpr int f16_min_waves() { return (sizeof(TB) == 2 && ALIGNED) ? 3 : 2; }
 
-template <int TK, typename TB, bool ALIGNED>
+template <int TK, typename TB, bool ALIGNED, bool ACC>
 __global__ __launch_bounds__(64 * kWaves, (f16_min_waves<TB, ALIGNED>())) void k_spmm_f16(
     const int4* __restrict__ units, int num_heavy, XcdSplit xs,
     const int* __restrict__ chunk_eptr, const int* __restrict__ chunk_cols,
     const int* __restrict__ chunk_dense, const uint32_t* __restrict__ entries,
     const _Float16* __restrict__ dense_a, const TB* __restrict__ B, int O, float scale, bool c4,
-    bool accumulate, float* __restrict__ C) {
+    float* __restrict__ C) {
     constexpr int VEC = TK / 16;
     __shared__ __attribute__((aligned(16))) _Float16 As[kWaves][16 * kApitch];
     __shared__ __attribute__((aligned(16))) float P[kWaves * 16 * TK];
@@ -432,17 +460,17 @@ __global__ __launch_bounds__(64 * kWaves, (f16_min_waves<TB, ALIGNED>())) void k
     // counting sees one fixed sequence of loads on each.
     if (heavy) {
         CAhead<TK, kWaves> ca;
-        read_c_ahead<TK, kWaves>(ca, U, k0, O, c4, accumulate, C);
+        read_c_ahead<TK, kWaves>(ca, U, k0, O, c4, ACC, C);
         tiles_f16<TK, TB, ALIGNED>(U.y + wave, U.z, kWaves, lane, n, g, c0, (long long)O,
                                    chunk_eptr, chunk_cols, chunk_dense, entries, dense_a, B,
                                    As[wave], acc, [] {});
-        merge_into_c<TK, kWaves>(acc, scale, U, k0, O, c4, accumulate, C, P, ca);
+        merge_into_c<TK, kWaves, ACC>(acc, scale, U, k0, O, c4, C, P, ca);
     } else {
         CAhead<TK, 1> ca;
         tiles_f16<TK, TB, ALIGNED>(U.y, U.z, 1, lane, n, g, c0, (long long)O, chunk_eptr,
                                    chunk_cols, chunk_dense, entries, dense_a, B, As[wave], acc,
-                                   [&] { read_c_ahead<TK, 1>(ca, U, k0, O, c4, accumulate, C); });
-        merge_into_c<TK, 1>(acc, scale, U, k0, O, c4, accumulate, C, P, ca);
+                                   [&] { read_c_ahead<TK, 1>(ca, U, k0, O, c4, ACC, C); });
+        merge_into_c<TK, 1, ACC>(acc, scale, U, k0, O, c4, C, P, ca);
     }
 }
 
@@ -644,13 +672,13 @@ __device__ __forceinline__ void tiles_f32(int first, int end, int W, int lane, i
     }
 }
 
-template <int TK, bool ALIGNED>
+template <int TK, bool ALIGNED, bool ACC>
 __global__ __launch_bounds__(64 * kWaves, 3) void k_spmm_f32(
     const int4* __restrict__ units, int num_heavy, XcdSplit xs,
     const int* __restrict__ chunk_eptr, const int* __restrict__ chunk_cols,
     const int* __restrict__ chunk_dense, const uint32_t* __restrict__ entries,
     const float* __restrict__ dense_a, const float* __restrict__ B, int O, bool c4,
-    bool accumulate, float* __restrict__ C) {
+    float* __restrict__ C) {
     constexpr int VEC = TK / 16;
     __shared__ __attribute__((aligned(16))) float At[kWaves][4 * kAgroup32];
     __shared__ __attribute__((aligned(16))) float P[kWaves * 16 * TK];
@@ -667,22 +695,22 @@ __global__ __launch_bounds__(64 * kWaves, 3) void k_spmm_f32(
     for (int q = 0; q < VEC; ++q) acc[q] = floatx4{0.f, 0.f, 0.f, 0.f};
     if (heavy) {
         CAhead<TK, kWaves> ca;
-        read_c_ahead<TK, kWaves>(ca, U, k0, O, c4, accumulate, C);
+        read_c_ahead<TK, kWaves>(ca, U, k0, O, c4, ACC, C);
         tiles_f32<TK, ALIGNED>(U.y + wave, U.z, kWaves, lane, n, g, c0, (long long)O, chunk_eptr,
                                chunk_cols, chunk_dense, entries, dense_a, B, At[wave], acc, [] {});
-        merge_into_c<TK, kWaves>(acc, 1.0f, U, k0, O, c4, accumulate, C, P, ca);
+        merge_into_c<TK, kWaves, ACC>(acc, 1.0f, U, k0, O, c4, C, P, ca);
     } else {
         CAhead<TK, 1> ca;
         tiles_f32<TK, ALIGNED>(U.y, U.z, 1, lane, n, g, c0, (long long)O, chunk_eptr, chunk_cols,
                                chunk_dense, entries, dense_a, B, At[wave], acc,
-                               [&] { read_c_ahead<TK, 1>(ca, U, k0, O, c4, accumulate, C); });
-        merge_into_c<TK, 1>(acc, 1.0f, U, k0, O, c4, accumulate, C, P, ca);
+                               [&] { read_c_ahead<TK, 1>(ca, U, k0, O, c4, ACC, C); });
+        merge_into_c<TK, 1, ACC>(acc, 1.0f, U, k0, O, c4, C, P, ca);
     }
 }
 
-template <int TK>
-static void launch_tk(const DeviceFormat& F, const void* dB, bool b_f16, int O, float* dC,
-                      bool accumulate, hipStream_t st) {
+template <int TK, bool ACC>
+static void launch_tk_mode(const DeviceFormat& F, const void* dB, bool b_f16, int O, float* dC,
+                           hipStream_t st) {
     constexpr int VEC = TK / 16;
     // Vector loads of B need O % VEC == 0 and a 16-byte aligned base.
     const bool aligned = (O % VEC) == 0 && ((uintptr_t)dB % 16) == 0;
@@ -706,38 +734,45 @@ static void launch_tk(const DeviceFormat& F, const void* dB, bool b_f16, int O, 
     if (F.fp32) {
         const float* B = static_cast<const float*>(dB);
         if (aligned)
-            hipLaunchKernelGGL((k_spmm_f32<TK, true>), grid, block, 0, st, F.units.p, NH, xs,
+            hipLaunchKernelGGL((k_spmm_f32<TK, true, ACC>), grid, block, 0, st, F.units.p, NH, xs,
                                F.chunk_eptr.p, F.chunk_cols.p, F.chunk_dense.p, F.entries.p,
-                               F.dense_a32.p, B, O, c4, accumulate, dC);
+                               F.dense_a32.p, B, O, c4, dC);
         else
-            hipLaunchKernelGGL((k_spmm_f32<TK, false>), grid, block, 0, st, F.units.p, NH, xs,
+            hipLaunchKernelGGL((k_spmm_f32<TK, false, ACC>), grid, block, 0, st, F.units.p, NH, xs,
                                F.chunk_eptr.p, F.chunk_cols.p, F.chunk_dense.p, F.entries.p,
-                               F.dense_a32.p, B, O, c4, accumulate, dC);
+                               F.dense_a32.p, B, O, c4, dC);
     } else if (b_f16) {
         const _Float16* B = static_cast<const _Float16*>(dB);
         if (aligned)
-            hipLaunchKernelGGL((k_spmm_f16<TK, _Float16, true>), grid, block, 0, st, F.units.p, NH,
+            hipLaunchKernelGGL((k_spmm_f16<TK, _Float16, true, ACC>), grid, block, 0, st, F.units.p, NH,
                                xs, F.chunk_eptr.p, F.chunk_cols.p, F.chunk_dense.p, F.entries.p,
-                               F.dense_a16.p, B, O, F.scale, c4, accumulate, dC);
+                               F.dense_a16.p, B, O, F.scale, c4, dC);
         else
-            hipLaunchKernelGGL((k_spmm_f16<TK, _Float16, false>), grid, block, 0, st, F.units.p, NH,
+            hipLaunchKernelGGL((k_spmm_f16<TK, _Float16, false, ACC>), grid, block, 0, st, F.units.p, NH,
                                xs, F.chunk_eptr.p, F.chunk_cols.p, F.chunk_dense.p, F.entries.p,
-                               F.dense_a16.p, B, O, F.scale, c4, accumulate, dC);
+                               F.dense_a16.p, B, O, F.scale, c4, dC);
     } else if constexpr (TK <= 64) {
         const float* B = static_cast<const float*>(dB);
         if (aligned)
-            hipLaunchKernelGGL((k_spmm_f16<TK, float, true>), grid, block, 0, st, F.units.p, NH,
+            hipLaunchKernelGGL((k_spmm_f16<TK, float, true, ACC>), grid, block, 0, st, F.units.p, NH,
                                xs, F.chunk_eptr.p, F.chunk_cols.p, F.chunk_dense.p, F.entries.p,
-                               F.dense_a16.p, B, O, F.scale, c4, accumulate, dC);
+                               F.dense_a16.p, B, O, F.scale, c4, dC);
         else
-            hipLaunchKernelGGL((k_spmm_f16<TK, float, false>), grid, block, 0, st, F.units.p, NH,
+            hipLaunchKernelGGL((k_spmm_f16<TK, float, false, ACC>), grid, block, 0, st, F.units.p, NH,
                                xs, F.chunk_eptr.p, F.chunk_cols.p, F.chunk_dense.p, F.entries.p,
-                               F.dense_a16.p, B, O, F.scale, c4, accumulate, dC);
+                               F.dense_a16.p, B, O, F.scale, c4, dC);
     } else {
         // o_tile_width never gives an FP16 format reading FP32 B an O tile of 128.
         throw Error(VCSRMC_ERR_STATE, "no O tile of 128 for FP32 B with an FP16 format");
     }
     VCSRMC_HIP(hipGetLastError());
+}
+
+template <int TK>
+static void launch_tk(const DeviceFormat& F, const void* dB, bool b_f16, int O, float* dC,
+                      bool accumulate, hipStream_t st) {
+    if (accumulate) launch_tk_mode<TK, true>(F, dB, b_f16, O, dC, st);
+    else launch_tk_mode<TK, false>(F, dB, b_f16, O, dC, st);
 }
 
 // Before an overwriting launch (C = A.B), the rows of every split panel are set to zero: their
