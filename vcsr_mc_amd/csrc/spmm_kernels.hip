@@ -106,16 +106,17 @@ __device__ __forceinline__ void wave_lds_sync() {
 }
 
 // C of a unit's output tile, read ahead of the merge (C += A.B needs it) so that its latency
-// overlaps the tile loop.  W == 1 (light): lane (n, g) reads rows 4g..4g+3 at columns
-// k0 + VEC n .. + VEC - 1 (VEC / 4 float4 per row), just before the wave's last tile is multiplied.
-// W > 1 (heavy): thread t reads the float4 at t*4 + 256 W j of the 16 x TK tile (the layout of
-// the merge) when the unit starts.  The loads are always issued -- rows outside the mask, split
-// panels, unaligned C and columns past O read kZeroRow instead -- so their number is fixed and a
-// wait for an older load never has to cover them.
+// overlaps the tile loop.  W == 1 (light): just before the wave's last tile is multiplied; for a
+// whole, aligned, unsplit tile (the staged merge below) lane l reads the float4s at l*4 + 256 j of
+// the 16 x TK tile, row-major; otherwise lane (n, g) reads rows 4g..4g+3 at columns
+// k0 + VEC n .. + VEC - 1 (VEC / 4 float4 per row).  W > 1 (heavy): thread t reads the float4 at
+// t*4 + 256 W j of the tile when the unit starts.  The loads are always issued -- rows outside
+// the mask, split panels, unaligned C, columns past O and overwriting launches read kZeroRow
+// instead -- so their number is fixed and a wait for an older load never has to cover them.
 template <int TK, int W>
 struct CAhead {
     static constexpr int VEC = TK / 16;
-    static constexpr int N = W == 1 ? (VEC >= 4 ? VEC : 0) : (16 * TK + 256 * W - 1) / (256 * W);
+    static constexpr int N = W == 1 ? TK / 16 : (16 * TK + 256 * W - 1) / (256 * W);
     floatx4 v[N > 0 ? N : 1];
 };
 
@@ -130,7 +131,17 @@ __device__ __forceinline__ void read_c_ahead(CAhead<TK, W>& ca, const int4& U, i
     const bool ok = c4 && accumulate && !(U.w & kUnitSplit);
     const long long OL = O;
     if constexpr (W == 1) {
-        if constexpr (N > 0) {
+        if (c4 && !(U.w & kUnitSplit) && k0 + TK <= O) {
+            // staged merge: lane-contiguous 16-byte pieces, as merge_into_c writes them back
+#pragma unroll
+            for (int j = 0; j < N; ++j) {
+                const int e = lane * 4 + 256 * j;
+                const int row = e / TK, col = e % TK;
+                const bool in = accumulate && ((U.w >> row) & 1);
+                const float* src = in ? C + (long long)(U.x + row) * OL + k0 + col : kZeroRow;
+                ca.v[j] = *reinterpret_cast<const floatx4*>(src);
+            }
+        } else if constexpr (VEC >= 4) {
             const int c0 = k0 + VEC * n;
             const bool lane_ok = ok && c0 + VEC <= O;
 #pragma unroll
@@ -155,11 +166,9 @@ __device__ __forceinline__ void read_c_ahead(CAhead<TK, W>& ca, const int4& U, i
     }
 }
 
-// Four floats of C.  An overwriting launch never reads C, so its stores bypass the caches
-// (non-temporal): they would only evict the B rows that other panels reuse (measured on gfx950,
-// overwrite: power-law 36,692^2 14.4 -> 13.2 us, 32 x 32 blocks 174 -> 150 us, R-MAT scale 22
-// 2.46 -> 2.39 ms, 27-point stencil within 1%).  An accumulating launch has just read the line,
-// and keeps ordinary stores (non-temporal measured 0-2% slower there).
+// Four floats of C: an ordinary store (ACC) or one that bypasses the caches (non-temporal), so
+// that C does not evict the B rows other panels reuse.  Non-temporal stores are not combined in
+// L2, so they are used where each store instruction covers whole lines (the staged merge).
 // (ACC is a template parameter of the kernels: with a run-time flag the compiler merged the two
 // stores into one ordinary store.)
 template <bool ACC>
@@ -168,12 +177,20 @@ __device__ __forceinline__ void store_c4(float* p, const floatx4& v) {
     else __builtin_nontemporal_store(v, reinterpret_cast<floatx4*>(p));
 }
 
-// Adds the unit's 16 x TK result into C.  W == 1: straight from the accumulators (lane (n, g)
-// owns rows 4g..4g+3, columns k0 + VEC n .. + VEC - 1).  W > 1: every wave parks its partial
-// tile in LDS, then the work-group sums the W partials and writes each row with consecutive
-// threads on consecutive columns.  Split panels merge through atomics; other rows are a
-// read-modify-write (C += A.B) whose read, on the vector path, came from read_c_ahead.  Rows
-// outside the panel's row mask are never touched.
+// Adds the unit's 16 x TK result into C (ACC) or writes it (overwrite).  W == 1, staged merge
+// (a whole, aligned tile of an unsplit panel): the wave parks its tile in its slice of P (lane
+// (n, g) owns rows 4g..4g+3, columns k0 + VEC n .. + VEC - 1), reads it back with consecutive
+// lanes on consecutive 16-byte pieces, adds the C read ahead in that order, and stores each run of
+// 1 KB non-temporally.  From the accumulators, one store instruction covered every other 16
+// bytes of a row at O tiles of 128, which non-temporal stores turned into 1.5x the C bytes.
+// Measured on gfx950 against the register epilogue with ordinary stores: overwrite power-law
+// 36,692^2 14.4 -> 12.8 us, 32 x 32 blocks 174 -> 140 us, 27-point stencil 543 -> 508 us, R-MAT
+// scale 22 2.46 -> 2.38 ms; accumulate blocks 189 -> 178 us, stencil 584 -> 565 us, the others
+// within 1%.  Other W == 1 tiles: straight from the accumulators.  W > 1: every wave parks its
+// partial tile in LDS, then the work-group sums the W partials and writes each row with
+// consecutive threads on consecutive columns.  Split panels merge through atomics; other rows
+// are a read-modify-write (C += A.B) whose read came from read_c_ahead.  Rows outside the
+// panel's row mask are never touched.
 template <int TK, int W, bool ACC>
 __device__ __forceinline__ void merge_into_c(const floatx4 (&acc)[TK / 16], float scale,
                                              const int4& U, int k0, int O, bool c4,
@@ -184,30 +201,24 @@ __device__ __forceinline__ void merge_into_c(const floatx4 (&acc)[TK / 16], floa
     const bool split = U.w & kUnitSplit;
     const long long OL = O;
     if constexpr (W == 1) {
-        if constexpr (!ACC) {
-            // Overwrite: non-temporal stores are not combined in L2, so each store instruction
-            // must cover whole lines.  The wave parks its tile in its slice of P and writes it
-            // back with consecutive lanes on consecutive 16-byte pieces (a 1 KB run per
-            // instruction), instead of from the accumulators, where one instruction covers
-            // every other 16 bytes of a row at O tiles of 128 (measured: written bytes 1.5x C).
-            if (!split && c4 && k0 + TK <= O) {
-                float* Pw = P + wave * 16 * TK;
+        if (!split && c4 && k0 + TK <= O) {  // staged merge
+            float* Pw = P + wave * 16 * TK;
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < 4; ++i)
 #pragma unroll
-                    for (int q = 0; q < VEC; ++q)
-                        Pw[(4 * g + i) * TK + VEC * n + q] = acc[q][i] * scale;
-                wave_lds_sync();
+                for (int q = 0; q < VEC; ++q)
+                    Pw[(4 * g + i) * TK + VEC * n + q] = acc[q][i] * scale;
+            wave_lds_sync();
 #pragma unroll
-                for (int j = 0; j < 16 * TK / 256; ++j) {
-                    const int e = lane * 4 + 256 * j;
-                    const int row = e / TK, col = e % TK;
-                    if ((U.w >> row) & 1)
-                        store_c4<ACC>(C + (long long)(U.x + row) * OL + k0 + col,
-                                      *reinterpret_cast<const floatx4*>(Pw + e));
-                }
-                return;
+            for (int j = 0; j < 16 * TK / 256; ++j) {
+                const int e = lane * 4 + 256 * j;
+                const int row = e / TK, col = e % TK;
+                floatx4 v = *reinterpret_cast<const floatx4*>(Pw + e);
+                if constexpr (ACC) v += ca.v[j];
+                if ((U.w >> row) & 1)
+                    store_c4<false>(C + (long long)(U.x + row) * OL + k0 + col, v);
             }
+            return;
         }
         const int c0 = k0 + VEC * n;
 #pragma unroll
