@@ -7,6 +7,7 @@ configured precision and O (segw = 32, tileK = 128):
   1 uniform 4096^2 FP32, O = 128      2 power-law 36,692^2 FP16, O = 128
   3 27-point stencil 100^3 FP32       4 32x32 blocks 262,144^2 FP16, O = 256
   5 R-MAT scale 22 FP16, O = 128
+The block workload also runs in FP32 (the case bound by the FP32 matrix cores), as an extra line.
 `value` is the power-law workload (the headline configuration) with the reference's C += A.B
 semantics; `per_config` holds every workload, in both launch modes (C += A.B, and the additive
 C = A.B that never reads C), with its HBM roofline, matrix-core fraction, hipSPARSE FP32/FP16 on
@@ -51,8 +52,10 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=20)
-    p.add_argument("--configs", default="1,2,3,4,5",
-                   help="workloads to run (comma-separated); the headline value needs 2")
+    p.add_argument("--configs", default="1,2,3,4,5,4:fp32",
+                   help="workloads to run, comma-separated, each K or K:precision (K:fp32 / "
+                        "K:fp16 runs workload K in the other precision); the headline value "
+                        "needs 2")
     p.add_argument("--config", type=int, default=None, help="run one workload only")
     p.add_argument("--size", type=int, default=0, help="workload size parameter (0 = full)")
     p.add_argument("--precision", choices=["fp16", "fp32"], default=None)
@@ -173,14 +176,14 @@ def row_sample_parity(A, Bh, Cgpu, fp32, scale, oracle, np, torch):
     return bool(np.all(err <= tau * L1 + 1e-30))
 
 
-def run_config(cfg, args, stream, want_cpu, cpu_seconds):
+def run_config(cfg, args, stream, want_cpu, cpu_seconds, prec_override=None):
     import numpy as np
     import torch
 
     import vcsr_mc_amd as vm
 
     w = vm.WORKLOADS[cfg]
-    prec = args.precision or w["precision"]
+    prec = prec_override or args.precision or w["precision"]
     fp32 = prec == "fp32"
     O = args.O or w["O"]
     dev = torch.device("cuda:0")
@@ -317,6 +320,11 @@ def run_config(cfg, args, stream, want_cpu, cpu_seconds):
     return out
 
 
+def vm_precision(cfg):
+    import vcsr_mc_amd as vm
+    return vm.WORKLOADS[cfg]["precision"]
+
+
 def geomean(xs):
     return math.exp(sum(math.log(x) for x in xs) / len(xs)) if xs else None
 
@@ -331,7 +339,14 @@ def main():
 
     import torch
 
-    configs = [args.config] if args.config else [int(c) for c in args.configs.split(",") if c]
+    spec = [str(args.config)] if args.config else [c for c in args.configs.split(",") if c]
+    configs = []
+    for c in spec:
+        k, _, pr = c.partition(":")
+        if pr not in ("", "fp16", "fp32"):
+            print(f"--configs: unknown precision in {c}", file=sys.stderr)
+            sys.exit(2)
+        configs.append((int(k), pr or None))
     modes = [m for m in args.modes.split(",") if m]
     if any(m not in ("accumulate", "overwrite") for m in modes) or not modes:
         print("--modes takes accumulate and/or overwrite", file=sys.stderr)
@@ -342,10 +357,12 @@ def main():
     want_cpu = not args.no_cpu
 
     per = []
-    for cfg in configs:
-        per.append(run_config(cfg, args, stream, want_cpu, args.cpu_seconds / len(configs)))
+    for cfg, pr in configs:
+        per.append(run_config(cfg, args, stream, want_cpu, args.cpu_seconds / len(configs), pr))
 
-    head = next((p for p in per if p["config"] == HEADLINE), per[0])
+    # each workload at its configured precision; the others are extra lines of per_config
+    configured = [p for p in per if p["precision"] == vm_precision(p["config"])]
+    head = next((p for p in configured if p["config"] == HEADLINE), per[0])
     hm = "accumulate" if "accumulate" in modes else modes[0]
     h = head[hm]
     out = {
@@ -386,7 +403,8 @@ def main():
     # configured precision, reference protocol (median single launch)
     if not args.no_rocsparse:
         for mode in modes:
-            sp = [p[mode]["speedup_vs_rocsparse_fp32"] for p in per if p["config"] in (1, 2, 3, 4)]
+            sp = [p[mode]["speedup_vs_rocsparse_fp32"] for p in configured
+                  if p["config"] in (1, 2, 3, 4)]
             if len(sp) == 4:
                 out[f"speedup_vs_rocsparse_fp32_geomean_1_4_{mode}"] = round(geomean(sp), 3)
     out["per_config"] = per
