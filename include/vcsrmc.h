@@ -49,6 +49,7 @@ typedef struct vcsrmc_info {
     int num_chunks;        /* 32-column compacted tiles                 */
     int num_units;         /* kernel work units                         */
     int device;            /* HIP device the format lives on            */
+    int num_dense;         /* tiles stored as dense 16 x 32 copies      */
 } vcsrmc_info;
 
 /* Handle holding one device-resident format (the reference keeps one format in

@@ -217,6 +217,41 @@ def test_mixed_tile_fill(orc, fp32, tileK):
     check(orc, rp, c, v, M, N, B, fp32, tileK=tileK, C0=C0)
 
 
+@pytest.mark.parametrize("tileK", [16, 32, 64, 128])
+def test_fp32_entry_tiles(orc, tileK):
+    """FP32 formats of more than 256 panels keep their sparse tiles as entry lists, scattered
+    into the matrix-core operand through LDS: that path over 4,200-6,000-row matrices with empty
+    rows, two heavy rows (split panels) and sparse rows, O from 1 to 257, C starting non-zero."""
+    rng = np.random.default_rng(900 + tileK)
+    for O in (1, 7, 100, 128, 257):
+        M, N = int(rng.integers(4200, 6000)), int(rng.integers(300, 9000))
+        rp, c, v = random_csr(rng, M, N, density=float(rng.choice([0.0005, 0.003])),
+                              empty_frac=0.2, heavy_rows=2, heavy_nnz=3000)
+        B = rng.uniform(-1, 1, (N, O)).astype(np.float32)
+        C0 = rng.uniform(-1, 1, (M, O)).astype(np.float32)
+        say("fp32 entry tiles", tileK, O, M, N, c.size)
+        C, info = run_spmm(rp, c, v, M, N, B, True, tileK=tileK, C0=C0)
+        assert info["num_panels"] > 256 and info["num_dense"] < info["num_chunks"], info
+        R, L1 = orc.spmm_csr(rp, c, v, M, B, mode=0, scale=info["scale"])
+        R = R + C0.astype(np.float64)
+        L1 = L1 + np.abs(C0.astype(np.float64)).sum(axis=1)
+        ok, worst, r = row_l1_parity(C, R, L1, TAU[True])
+        assert ok, f"row {r}: error / bound = {worst:.3g}"
+
+
+def test_small_fp32_formats_all_dense():
+    """An FP32 format of at most 256 panels and 4096 tiles stores every tile dense; the same
+    matrix as an FP16 format, or one panel more, stores only tiles of more than 192 nonzeros."""
+    rng = np.random.default_rng(77)
+    for M, fp32, all_dense in ((4096, True, True), (4096, False, False), (4112, True, False)):
+        rp, c, v = random_csr(rng, M, 4096, nnz_per_row=16)
+        B = rng.uniform(-1, 1, (4096, 8)).astype(np.float32)
+        _, info = run_spmm(rp, c, v, M, 4096, B, fp32)
+        say("small fp32 all dense", M, fp32, info["num_panels"], info["num_chunks"],
+            info["num_dense"])
+        assert (info["num_dense"] == info["num_chunks"]) == all_dense, info
+
+
 @pytest.mark.parametrize("keep", [1.0, 0.4])
 @pytest.mark.parametrize("O", [100, 128])
 def test_fp32_full_tiles_many_panels(orc, keep, O):

@@ -191,6 +191,7 @@ int vcsrmc_get_info(vcsrmc_t h, vcsrmc_info* out) {
         out->num_items = F.nitems; out->scale = F.scale; out->fp32 = F.fp32; out->nnz = F.nnz;
         out->num_panels = F.num_panels; out->num_chunks = F.num_chunks;
         out->num_units = F.num_units; out->device = h->device;
+        out->num_dense = F.num_dense;
     });
 }
 

@@ -372,9 +372,21 @@ __global__ void k_panel_masks(const unsigned char* __restrict__ rflag,
     pmask[j] = m;
 }
 
-__global__ void k_dense_flags(const int* __restrict__ eptr, int NC, int* __restrict__ flag) {
+__global__ void k_dense_flags(const int* __restrict__ eptr, int NC, int dmin,
+                              int* __restrict__ flag) {
     const long long c = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (c < NC) flag[c] = (eptr[c + 1] - eptr[c]) > kDenseMin;
+    if (c < NC) flag[c] = (eptr[c + 1] - eptr[c]) > dmin;
+}
+
+// Tiles holding more than this many nonzeros get a dense copy.  Every tile of a small FP32
+// format does (each tile holds at least one nonzero): measured on gfx950 at O = 128, FP32
+// formats of at most 256 panels ran 2-9% faster with all tiles dense (uniform 2048^2 / 4096^2,
+// power-law 4000^2, 27-point stencil 16^3, R-MAT scale 12), while larger uniform and stencil
+// formats ran 2-13% slower (uniform 8192^2 to 30,000^2, stencil 20^3 to 30^3: the copies' bytes
+// outweigh the LDS round trip once the GPU holds more waves than it runs at once), and FP16
+// formats gained or lost a few percent either way.
+static int dense_min(bool fp32, int num_panels, int num_chunks) {
+    return (fp32 && num_panels <= kSmallPanels && num_chunks <= kSmallTiles) ? 0 : kDenseMin;
 }
 
 __global__ void k_dense_index(const int* __restrict__ flag, const int* __restrict__ idx, int NC,
@@ -569,7 +581,7 @@ static void build_exec_layout_k(DeviceFormat& F, const int* trow, const int* tco
     // dense copies of well-filled tiles
     {
         DevBuf<int> dflag(NC), didx(NC + 1);
-        LAUNCH(k_dense_flags, NC, F.chunk_eptr.p, NC, dflag.p);
+        LAUNCH(k_dense_flags, NC, F.chunk_eptr.p, NC, dense_min(F.fp32, NP, NC), dflag.p);
         exclusive_sum<int, int>(dflag.p, didx.p, NC, st);
         const int ND = read_scalar(didx.p + NC, st);
         F.chunk_dense.alloc(NC);
@@ -633,7 +645,7 @@ static void build_exec_layout_k(DeviceFormat& F, const int* trow, const int* tco
 
 static void build_exec_layout(DeviceFormat& F, const int* trow, const int* tcol, const float* tval,
                               long long n, hipStream_t st) {
-    F.num_panels = F.num_chunks = F.num_units = 0;
+    F.num_panels = F.num_chunks = F.num_units = F.num_dense = 0;
     if (n == 0) return;
     const int num_panels_all = (F.M + kPanelRows - 1) / kPanelRows;
     const int cbits = bits_for(F.N > 0 ? (unsigned long long)(F.N - 1) : 0ull);

@@ -15,6 +15,12 @@ constexpr int kChunkCols = 32;
 constexpr int kPanelRows = 16;
 // A tile holding more nonzeros than this (of 16 x 32) is also stored dense.
 constexpr int kDenseMin = 192;
+// An FP32 format of at most kSmallPanels non-empty panels and kSmallTiles tiles stores every tile
+// dense (at most 8 MB of copies): such a launch is one short chain of dependent loads per wave,
+// and a dense tile reaches the matrix cores without the round trip through LDS that scattering
+// a tile's entries takes (format_build.hip, dense_min).
+constexpr int kSmallPanels = 256;
+constexpr int kSmallTiles = 4096;
 // Fewest tiles a heavy unit may be cut to (shared by the kWaves waves of one work-group); large
 // launches use larger units (format_build.hip, heavy_tile_limit).
 constexpr int kHeavyTiles = 64;
@@ -50,7 +56,8 @@ struct XcdSplit {
 //                   FP32 format: two words per entry, entries[2e] = row-in-panel | k << 4 and
 //                   entries[2e+1] = the value's bits
 //   chunk_dense[c]  -1, or the index of the tile's dense copy when more than kDenseMin of its
-//                   512 slots are filled: dense_a16[512 d + 32 row + k] (FP16), or
+//                   512 slots are filled (every tile of a small FP32 format, kSmallPanels):
+//                   dense_a16[512 d + 32 row + k] (FP16), or
 //                   dense_a32[512 d + 128 (k & 3) + 8 row + (k >> 2)] (FP32) -- exactly the
 //                   order in which MFMA lanes read their A operand, so a lane loads it directly
 // Below this many 16-row panels a launch cannot fill the GPU's 1024 SIMDs with one wave per
