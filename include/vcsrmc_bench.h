@@ -41,8 +41,11 @@ int vcsrmc_gen_dense(int dist, unsigned long long seed, int fp16_exact, float *o
 /* hipSPARSE SpMM (CSR, ALG_DEFAULT unless alg = 1..3 picks CSR_ALG1..3), C = alpha A.B with
  * beta = 0, row-major dense B (N x O) and C (M x O).  val_f16 / b_f16 select binary16 A values
  * and B (FP32 compute and C, as the reference's rocsparse_fp16, src/kernels.cu:139-206).
- * Descriptors, buffer and preprocess are rebuilt only when an argument changes and are timed
- * into *setup_ms; *ms is the event-timed hipsparseSpMM call on `stream`. */
+ * Descriptors, workspace and preprocess are built once per argument set (the four most recent
+ * sets are kept) and timed into *setup_ms; *ms is the event-timed hipsparseSpMM call on
+ * `stream`.  Sets are keyed by device addresses: call vcsrmc_rocsparse_release before reusing
+ * freed addresses for other operands of the same sizes.  Returns 0, 2 (HIP error) or
+ * 10 + a hipSPARSE status. */
 int vcsrmc_rocsparse_spmm(int M, int N, int nnz, const int *d_row_ptr, const int *d_col,
                           const void *d_val, int val_f16, const void *d_B, int b_f16, int O,
                           float *d_C, float alpha, int alg, void *stream, float *ms,
