@@ -50,6 +50,7 @@ typedef struct vcsrmc_info {
     int num_units;         /* kernel work units                         */
     int device;            /* HIP device the format lives on            */
     int num_dense;         /* tiles stored as dense 16 x 32 copies      */
+    int row_grouped;       /* 1: panels of rows grouped by shared columns */
 } vcsrmc_info;
 
 /* Handle holding one device-resident format (the reference keeps one format in
@@ -160,6 +161,15 @@ int vcsrmc_rcm_order(const int *d_row_ptr, const int *d_col, int M, int N, int n
  * limit stops, with every kernel ended, and vcsrmc_rcm_order returns VCSRMC_ERR_STATE.  Lower
  * limits exist to test that path.  Process-wide; no counterpart in the reference. */
 int vcsrmc_set_rcm_limits(long long max_levels, long long max_rounds);
+
+/* Row order of the execution layout that later builds and uploads use (process-wide): 0 natural
+ * order; 1 (the default) rows grouped by shared columns into 16-row panels where the natural
+ * layout's tiles hold 48-256 nonzeros on average over at least 2048 panels and grouping saves
+ * at least a tenth of the tiles; 2 always grouped.  Only the execution layout changes: the
+ * format arrays, C's rows and the product are the same (up to rounding: the sums of a row are
+ * formed in another order).  vcsrmc_info.row_grouped tells which a handle holds.  No
+ * counterpart in the reference. */
+int vcsrmc_set_row_grouping(int mode);
 
 /* Relabels the columns of a device CSR in place, col[p] = position[col[p]], with every row
  * re-sorted by its new columns (values follow), and, when d_B is non-NULL, writes

@@ -1,0 +1,165 @@
+"""Execution layouts with rows grouped by shared columns (a row map from panel positions to C
+rows) against the oracle, with the parity gate of test_gpu_spmm.py: random shapes and
+patterns in both precisions, every O tile width, C += A.B and C = A.B, split panels; the
+automatic choice on a 27-point stencil grid (grouped: far fewer tiles) and on uniform random
+rows (kept in natural order); the format arrays are the same either way."""
+import numpy as np
+import pytest
+
+import vcsr_mc_amd as vm
+from conftest import random_csr
+from gpu_util import dev, row_l1_parity, say
+
+pytestmark = pytest.mark.gpu
+
+TAU = {True: 1e-5, False: 2e-3}
+
+
+@pytest.fixture
+def grouping():
+    """Sets the process-wide row grouping mode for one test and restores the default."""
+    yield vm.set_row_grouping
+    vm.set_row_grouping(vm.ROW_GROUPING_AUTO)
+
+
+def band_rows(rng, M, N, bw):
+    rows = [np.arange(max(0, min(r, N - 1) - bw), min(N, min(r, N - 1) + bw + 1))
+            for r in range(M)]
+    rp = np.zeros(M + 1, np.int32)
+    rp[1:] = np.cumsum([len(x) for x in rows])
+    c = np.concatenate(rows).astype(np.int32)
+    return rp, c, rng.uniform(-1, 1, c.size).astype(np.float32)
+
+
+def run(orc, rp, c, v, M, N, B, fp32, tileK, O, C0, overwrite, segw=32, b16=False):
+    import torch
+    with vm.DeviceFormat.from_device_csr(dev(rp), dev(c), dev(v), M, N, fp32, segw) as f:
+        info = f.info()
+        V = f.download()
+        got = {k: getattr(V, k) for k in ("M", "N", "segw", "bundle", "num_segments", "fp32",
+                                           *vm._FMT_ARRAYS)}
+        got["scale"] = np.float32(V.scale)
+        assert orc.formats_equal(orc.Format(got), orc.build_format(rp, c, v, M, N, segw,
+                                                                   fp32)) == []
+        dB = dev(B)
+        if b16:
+            dB = dB.half()
+        dC = dev(C0)
+        f.spmm(dB, dC, tileK=tileK, O=O, overwrite=overwrite)
+        torch.cuda.synchronize()
+        Cg = dC.cpu().numpy()
+    R, L1 = orc.spmm_csr(rp, c, v, M, B, mode=0 if fp32 else 1, scale=info["scale"])
+    touched = np.diff(rp) > 0
+    base = C0.astype(np.float64).copy()
+    if overwrite:
+        base[touched] = 0.0
+    R = R + base
+    L1 = L1 + np.abs(base).sum(axis=1)
+    ok, worst, row = row_l1_parity(Cg, R, L1, TAU[fp32])
+    assert ok, f"row {row}: error / bound = {worst:.3g}"
+    # rows A does not touch are left alone in both launch modes
+    assert np.array_equal(Cg[~touched], C0[~touched])
+    return info
+
+
+@pytest.mark.parametrize("seed", range(3))
+def test_grouped_random_sweep(orc, grouping, seed):
+    """Always-grouped layouts: random, Poisson-with-heavy-rows (split panels) and banded
+    patterns, empty rows, FP16 / FP32 formats and B, every tileK, O from 1 to 257, C starting
+    non-zero, both launch modes."""
+    grouping(vm.ROW_GROUPING_ALWAYS)
+    Os = [1, 3, 8, 31, 64, 100, 128, 129, 200, 257]
+    grouped = 0
+    for t in range(10):
+        rng = np.random.default_rng(9100 + 100 * seed + t)
+        M, N = int(rng.integers(40, 3000)), int(rng.integers(16, 3000))
+        kind = int(rng.integers(0, 3))
+        if kind == 0:
+            rp, c, v = random_csr(rng, M, N, density=float(rng.choice([0.002, 0.01, 0.05])),
+                                  empty_frac=float(rng.uniform(0, 0.4)))
+        elif kind == 1:
+            rp, c, v = random_csr(rng, M, N, nnz_per_row=float(rng.uniform(1, 20)),
+                                  heavy_rows=int(rng.integers(0, 4)),
+                                  heavy_nnz=int(rng.integers(1, N + 1)))
+        else:
+            rp, c, v = band_rows(rng, M, N, int(rng.integers(1, 30)))
+        fp32 = bool(rng.integers(0, 2))
+        tileK = int(rng.choice([16, 32, 64, 128]))
+        O = int(rng.choice(Os))
+        b16 = (not fp32) and bool(rng.integers(0, 2))
+        overwrite = bool(rng.integers(0, 2))
+        B = rng.uniform(-1, 1, (N, O)).astype(np.float32)
+        if not fp32:
+            B = B.astype(np.float16).astype(np.float32)
+        C0 = rng.uniform(-1, 1, (M, O)).astype(np.float32)
+        say("grouped sweep", seed, t, M, N, c.size, kind, fp32, tileK, O, b16, overwrite)
+        info = run(orc, rp, c, v, M, N, B, fp32, tileK, O, C0, overwrite, b16=b16)
+        grouped += info["row_grouped"]
+    assert grouped >= 8, grouped
+
+
+def stencil27(g):
+    """27-point stencil on a g^3 grid in natural order (x fastest)."""
+    idx = np.arange(g ** 3)
+    x, y, z = idx % g, (idx // g) % g, idx // (g * g)
+    rows = []
+    for dz in (-1, 0, 1):
+        for dy in (-1, 0, 1):
+            for dx in (-1, 0, 1):
+                xx, yy, zz = x + dx, y + dy, z + dz
+                ok = (xx >= 0) & (xx < g) & (yy >= 0) & (yy < g) & (zz >= 0) & (zz < g)
+                rows.append(np.where(ok, xx + g * yy + g * g * zz, -1))
+    cols = np.stack(rows, axis=1)  # (g^3, 27), ascending per row, -1 outside the grid
+    keep = cols >= 0
+    rp = np.zeros(g ** 3 + 1, np.int32)
+    rp[1:] = np.cumsum(keep.sum(axis=1))
+    return rp, cols[keep].astype(np.int32)
+
+
+@pytest.mark.parametrize("fp32", [True, False])
+def test_stencil_grouped_by_default(orc, grouping, fp32):
+    """A 27-point stencil on a 32^3 grid (2048 panels, 72 nonzeros per tile in natural order):
+    the default layout groups its rows, and the product matches the oracle in both launch modes.
+    Natural order puts half an x line in a panel (up to 18 x 3 x 3 = 162 columns, 6 tiles;
+    4.875 per panel with the grid's faces); a 4 x 2 x 2 block touches at most 6 x 4 x 4 = 96
+    (3 tiles), so grouping that finds such blocks stays within 3 tiles per panel."""
+    rng = np.random.default_rng(31 + fp32)
+    g = 32
+    rp, c = stencil27(g)
+    v = rng.uniform(-1, 1, c.size).astype(np.float32)
+    M = N = g ** 3
+    O = 128
+    B = rng.uniform(-1, 1, (N, O)).astype(np.float32)
+    if not fp32:
+        B = B.astype(np.float16).astype(np.float32)
+    C0 = rng.uniform(-1, 1, (M, O)).astype(np.float32)
+    grouping(vm.ROW_GROUPING_OFF)
+    with vm.DeviceFormat.from_device_csr(dev(rp), dev(c), dev(v), M, N, fp32, 32) as f:
+        natural = f.info()
+    assert natural["row_grouped"] == 0
+    assert natural["num_chunks"] >= 4.8 * natural["num_panels"], natural
+    grouping(vm.ROW_GROUPING_AUTO)
+    for overwrite in (False, True):
+        say("stencil grouped", fp32, overwrite)
+        info = run(orc, rp, c, v, M, N, B, fp32, 128, O, C0, overwrite)
+        assert info["row_grouped"] == 1
+        assert info["num_chunks"] <= 3 * info["num_panels"], info
+
+
+def test_uniform_rows_keep_natural_order(grouping):
+    """Uniform random rows (about one nonzero per tile column) keep natural order by default;
+    ROW_GROUPING_OFF never groups; other modes are refused."""
+    rng = np.random.default_rng(5)
+    M = N = 40000
+    rp, c, v = random_csr(rng, M, N, nnz_per_row=12)
+    say("uniform natural order")
+    with vm.DeviceFormat.from_device_csr(dev(rp), dev(c), dev(v), M, N, True, 32) as f:
+        assert f.info()["row_grouped"] == 0
+    grouping(vm.ROW_GROUPING_ALWAYS)
+    with vm.DeviceFormat.from_device_csr(dev(rp), dev(c), dev(v), M, N, True, 32) as f:
+        assert f.info()["row_grouped"] == 1
+    grouping(vm.ROW_GROUPING_OFF)
+    with vm.DeviceFormat.from_device_csr(dev(rp), dev(c), dev(v), M, N, True, 32) as f:
+        assert f.info()["row_grouped"] == 0
+    with pytest.raises(vm.VCSRMCError):
+        vm.set_row_grouping(3)

@@ -47,7 +47,7 @@ class _Info(C.Structure):
         ("num_segments", C.c_int), ("num_groups", C.c_int), ("nval", C.c_longlong),
         ("num_items", C.c_int), ("scale", C.c_float), ("fp32", C.c_int), ("nnz", C.c_longlong),
         ("num_panels", C.c_int), ("num_chunks", C.c_int), ("num_units", C.c_int),
-        ("device", C.c_int), ("num_dense", C.c_int),
+        ("device", C.c_int), ("num_dense", C.c_int), ("row_grouped", C.c_int),
     ]
 
 
@@ -87,6 +87,7 @@ def lib():
         L.vcsrmc_spmm_noalloc.argtypes = [vp, vp, C.c_int, C.c_int, C.c_int, vp, C.c_int, vp]
         L.vcsrmc_rcm_order.argtypes = [vp, vp, C.c_int, C.c_int, C.c_int, vp, vp]
         L.vcsrmc_set_rcm_limits.argtypes = [C.c_longlong, C.c_longlong]
+        L.vcsrmc_set_row_grouping.argtypes = [C.c_int]
         L.vcsrmc_apply_column_permutation.argtypes = [vp, vp, vp, C.c_int, C.c_int, C.c_int, vp,
                                                       vp, C.c_int, vp, vp]
         L.vcsrmc_status_string.restype = C.c_char_p
@@ -95,7 +96,8 @@ def lib():
         for f in ("vcsrmc_create", "vcsrmc_destroy", "vcsrmc_half_scale", "vcsrmc_build_csr",
                   "vcsrmc_upload", "vcsrmc_get_info", "vcsrmc_download", "vcsrmc_spmm",
                   "vcsrmc_spmm_ex", "vcsrmc_spmm_noalloc", "vcsrmc_rcm_order",
-                  "vcsrmc_set_rcm_limits", "vcsrmc_apply_column_permutation"):
+                  "vcsrmc_set_rcm_limits", "vcsrmc_set_row_grouping",
+                  "vcsrmc_apply_column_permutation"):
             getattr(L, f).restype = C.c_int
         _lib_handle = L
     return _lib_handle
@@ -371,6 +373,18 @@ def destroy_vcsr_mc_device(stream=None) -> None:
         _global["fmt"].close()
     _global["fmt"] = None
     _global["uploaded"] = False
+
+
+# ---- execution layout ----------------------------------------------------------------------
+ROW_GROUPING_OFF, ROW_GROUPING_AUTO, ROW_GROUPING_ALWAYS = 0, 1, 2
+
+
+def set_row_grouping(mode: int) -> None:
+    """Row order of the execution layout for later builds (process-wide): ROW_GROUPING_OFF
+    (natural order), ROW_GROUPING_AUTO (the default: rows grouped by shared columns where that
+    saves tiles) or ROW_GROUPING_ALWAYS.  DeviceFormat.info()["row_grouped"] tells which a
+    format holds."""
+    _check(lib().vcsrmc_set_row_grouping(int(mode)), "set_row_grouping")
 
 
 # ---- column reordering (include/reorder.hpp:17-108), computed on the GPU -------------------

@@ -136,6 +136,13 @@ int vcsrmc_set_rcm_limits(long long max_levels, long long max_rounds) {
     });
 }
 
+int vcsrmc_set_row_grouping(int mode) {
+    return guarded([&] {
+        need(mode >= 0 && mode <= 2, "row grouping mode must be 0, 1 or 2");
+        vcsrmc::set_row_grouping(mode);
+    });
+}
+
 int vcsrmc_apply_column_permutation(const int* d_row_ptr, int* d_col, float* d_val, int M, int N,
                                     int nnz, const int* d_position, const float* d_B, int O,
                                     float* d_B_out, void* stream) {
@@ -192,6 +199,7 @@ int vcsrmc_get_info(vcsrmc_t h, vcsrmc_info* out) {
         out->num_panels = F.num_panels; out->num_chunks = F.num_chunks;
         out->num_units = F.num_units; out->device = h->device;
         out->num_dense = F.num_dense;
+        out->row_grouped = F.row_map.n > 0;
     });
 }
 

@@ -81,6 +81,10 @@ struct DeviceFormat {
     // Light units [num_heavy + xcd_start[x], num_heavy + xcd_start[x + 1]) run on XCD x.
     int xcd_start[9] = {0, 0, 0, 0, 0, 0, 0, 0, 0};
     DevBuf<int4> units;
+    // Row map (empty: natural order).  The layout's panels are 16 consecutive positions of a row
+    // order; row_map[p] = the row at position p (-1 past the last row).  Units, row masks and
+    // the entries' row-in-panel refer to positions; the kernels write C row row_map[p].
+    DevBuf<int> row_map;
     DevBuf<int> chunk_eptr, chunk_cols;
     DevBuf<uint32_t> entries;
     int num_dense = 0;
@@ -99,6 +103,16 @@ struct DeviceFormat {
 // binary evaluates it; see half_scale_from_amax).
 float half_scale_from_amax(float amax);
 float device_absmax(const float* d_val, long long n, hipStream_t st);
+
+// A row order that groups rows sharing columns into 16-row panels (row_groups.hip), from the
+// (row, col) of n nonzeros: rowpos[row] = position, row_map[position] = row (-1 past the last
+// of M rows; M rounded up to 16 entries).  False when it found nothing to work with.
+bool group_rows(const int* trow, const int* tcol, long long n, int M, int N, hipStream_t st,
+                DevBuf<int>& rowpos, DevBuf<int>& row_map);
+// Row grouping in the execution layout: 0 natural order, 1 grouped where it saves tiles (the
+// default; format_build.hip, build_exec_layout), 2 always grouped.  Read by later builds.
+void set_row_grouping(int mode);
+int row_grouping();
 
 // GPU format pipeline from a device CSR (src/vcsr_mc.cu:25-123).
 void build_from_csr(DeviceFormat& F, const int* d_row_ptr, const int* d_col, const float* d_val,

@@ -105,6 +105,27 @@ __device__ __forceinline__ void wave_lds_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// The C rows of a unit's 16 panel rows: U.x .. U.x + 15 for a layout in natural row order;
+// for a layout with a row map (rows grouped by shared columns), rmap[U.x + r], which lane r
+// loads once per unit and row() reads across lanes -- so every lane of the wave executes row()
+// together, outside branches that depend on the lane.
+struct PanelRows {
+    int base;   // U.x
+    int mine;   // mapped: the C row of panel row (lane & 15)
+    bool mapped;
+    __device__ __forceinline__ long long row(int r) const {
+        return mapped ? (long long)__shfl(mine, r) : (long long)(base + r);
+    }
+};
+
+__device__ __forceinline__ PanelRows panel_rows(const int4& U, const int* __restrict__ rmap) {
+    PanelRows p;
+    p.base = U.x;
+    p.mapped = rmap != nullptr;
+    p.mine = p.mapped ? rmap[U.x + (threadIdx.x & 15)] : 0;
+    return p;
+}
+
 // C of a unit's output tile, read ahead of the merge (C += A.B needs it) so that its latency
 // overlaps the tile loop.  W == 1 (light): just before the wave's last tile is multiplied; for a
 // whole, aligned, unsplit tile (the staged merge below) lane l reads the float4s at l*4 + 256 j of
@@ -121,9 +142,9 @@ struct CAhead {
 };
 
 template <int TK, int W>
-__device__ __forceinline__ void read_c_ahead(CAhead<TK, W>& ca, const int4& U, int k0, int O,
-                                             bool c4, bool accumulate,
-                                             const float* __restrict__ C) {
+__device__ __forceinline__ void read_c_ahead(CAhead<TK, W>& ca, const int4& U,
+                                             const PanelRows& pr, int k0, int O, bool c4,
+                                             bool accumulate, const float* __restrict__ C) {
     constexpr int VEC = TK / 16;
     constexpr int N = CAhead<TK, W>::N;
     const int lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
@@ -137,8 +158,9 @@ __device__ __forceinline__ void read_c_ahead(CAhead<TK, W>& ca, const int4& U, i
             for (int j = 0; j < N; ++j) {
                 const int e = lane * 4 + 256 * j;
                 const int row = e / TK, col = e % TK;
+                const long long cr = pr.row(row);
                 const bool in = accumulate && ((U.w >> row) & 1);
-                const float* src = in ? C + (long long)(U.x + row) * OL + k0 + col : kZeroRow;
+                const float* src = in ? C + cr * OL + k0 + col : kZeroRow;
                 ca.v[j] = *reinterpret_cast<const floatx4*>(src);
             }
         } else if constexpr (VEC >= 4) {
@@ -147,8 +169,9 @@ __device__ __forceinline__ void read_c_ahead(CAhead<TK, W>& ca, const int4& U, i
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int rl = 4 * g + i;
+                const long long cr = pr.row(rl);
                 const bool in = lane_ok && ((U.w >> rl) & 1);
-                const float* src = in ? C + (long long)(U.x + rl) * OL + c0 : kZeroRow;
+                const float* src = in ? C + cr * OL + c0 : kZeroRow;
 #pragma unroll
                 for (int h = 0; h < VEC / 4; ++h)
                     ca.v[i * (VEC / 4) + h] = *reinterpret_cast<const floatx4*>(src + 4 * h);
@@ -159,8 +182,9 @@ __device__ __forceinline__ void read_c_ahead(CAhead<TK, W>& ca, const int4& U, i
         for (int j = 0; j < N; ++j) {
             const int e = threadIdx.x * 4 + j * 256 * W;
             const int row = (e / TK) & 15, cc = k0 + e % TK;
+            const long long cr = pr.row(row);
             const bool in = ok && e < 16 * TK && ((U.w >> row) & 1) && cc + 4 <= O;
-            const float* src = in ? C + (long long)(U.x + row) * OL + cc : kZeroRow;
+            const float* src = in ? C + cr * OL + cc : kZeroRow;
             ca.v[j] = *reinterpret_cast<const floatx4*>(src);
         }
     }
@@ -193,8 +217,8 @@ __device__ __forceinline__ void store_c4(float* p, const floatx4& v) {
 // panel's row mask are never touched.
 template <int TK, int W, bool ACC>
 __device__ __forceinline__ void merge_into_c(const floatx4 (&acc)[TK / 16], float scale,
-                                             const int4& U, int k0, int O, bool c4,
-                                             float* __restrict__ C, float* P,
+                                             const int4& U, const PanelRows& pr, int k0, int O,
+                                             bool c4, float* __restrict__ C, float* P,
                                              const CAhead<TK, W>& ca) {
     constexpr int VEC = TK / 16;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, n = lane & 15, g = lane >> 4;
@@ -213,10 +237,10 @@ __device__ __forceinline__ void merge_into_c(const floatx4 (&acc)[TK / 16], floa
             for (int j = 0; j < 16 * TK / 256; ++j) {
                 const int e = lane * 4 + 256 * j;
                 const int row = e / TK, col = e % TK;
+                const long long cr = pr.row(row);
                 floatx4 v = *reinterpret_cast<const floatx4*>(Pw + e);
                 if constexpr (ACC) v += ca.v[j];
-                if ((U.w >> row) & 1)
-                    store_c4<false>(C + (long long)(U.x + row) * OL + k0 + col, v);
+                if ((U.w >> row) & 1) store_c4<false>(C + cr * OL + k0 + col, v);
             }
             return;
         }
@@ -224,8 +248,9 @@ __device__ __forceinline__ void merge_into_c(const floatx4 (&acc)[TK / 16], floa
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int rl = 4 * g + i;
+            const long long cr = pr.row(rl);
             if (!((U.w >> rl) & 1)) continue;
-            float* crow = C + (long long)(U.x + rl) * OL + c0;
+            float* crow = C + cr * OL + c0;
             if (split) {
 #pragma unroll
                 for (int q = 0; q < VEC; ++q)
@@ -256,6 +281,7 @@ __device__ __forceinline__ void merge_into_c(const floatx4 (&acc)[TK / 16], floa
             const int e = threadIdx.x * 4 + j * 256 * W;
             if (e >= 16 * TK) break;
             const int row = e / TK, col = e % TK;
+            const long long cr = pr.row(row);
             if (!((U.w >> row) & 1)) continue;
             floatx4 sum = *reinterpret_cast<const floatx4*>(P + e);
 #pragma unroll
@@ -265,7 +291,7 @@ __device__ __forceinline__ void merge_into_c(const floatx4 (&acc)[TK / 16], floa
             }
             const int cc = k0 + col;
             if (cc >= O) continue;
-            float* crow = C + (long long)(U.x + row) * OL + cc;
+            float* crow = C + cr * OL + cc;
             if (split) {
 #pragma unroll
                 for (int jj = 0; jj < 4; ++jj)
@@ -446,7 +472,7 @@ constexpr int f16_min_waves() { return (sizeof(TB) == 2 && ALIGNED) ? 3 : 2; }
 
 template <int TK, typename TB, bool ALIGNED, bool ACC>
 __global__ __launch_bounds__(64 * kWaves, (f16_min_waves<TB, ALIGNED>())) void k_spmm_f16(
-    const int4* __restrict__ units, int num_heavy, XcdSplit xs,
+    const int4* __restrict__ units, const int* __restrict__ rmap, int num_heavy, XcdSplit xs,
     const int* __restrict__ chunk_eptr, const int* __restrict__ chunk_cols,
     const int* __restrict__ chunk_dense, const uint32_t* __restrict__ entries,
     const _Float16* __restrict__ dense_a, const TB* __restrict__ B, int O, float scale, bool c4,
@@ -462,6 +488,7 @@ __global__ __launch_bounds__(64 * kWaves, (f16_min_waves<TB, ALIGNED>())) void k
     bool heavy;
     if (!schedule(num_heavy, xs, wave, u, heavy, ot)) return;
     const int4 U = units[u];
+    const PanelRows pr = panel_rows(U, rmap);
     const int k0 = ((blockIdx.y << (3 - xs.lgp)) + ot) * TK;
     const int c0 = k0 + VEC * n;
     floatx4 acc[VEC];
@@ -471,17 +498,17 @@ __global__ __launch_bounds__(64 * kWaves, (f16_min_waves<TB, ALIGNED>())) void k
     // counting sees one fixed sequence of loads on each.
     if (heavy) {
         CAhead<TK, kWaves> ca;
-        read_c_ahead<TK, kWaves>(ca, U, k0, O, c4, ACC, C);
+        read_c_ahead<TK, kWaves>(ca, U, pr, k0, O, c4, ACC, C);
         tiles_f16<TK, TB, ALIGNED>(U.y + wave, U.z, kWaves, lane, n, g, c0, (long long)O,
                                    chunk_eptr, chunk_cols, chunk_dense, entries, dense_a, B,
                                    As[wave], acc, [] {});
-        merge_into_c<TK, kWaves, ACC>(acc, scale, U, k0, O, c4, C, P, ca);
+        merge_into_c<TK, kWaves, ACC>(acc, scale, U, pr, k0, O, c4, C, P, ca);
     } else {
         CAhead<TK, 1> ca;
         tiles_f16<TK, TB, ALIGNED>(U.y, U.z, 1, lane, n, g, c0, (long long)O, chunk_eptr,
                                    chunk_cols, chunk_dense, entries, dense_a, B, As[wave], acc,
-                                   [&] { read_c_ahead<TK, 1>(ca, U, k0, O, c4, ACC, C); });
-        merge_into_c<TK, 1, ACC>(acc, scale, U, k0, O, c4, C, P, ca);
+                                   [&] { read_c_ahead<TK, 1>(ca, U, pr, k0, O, c4, ACC, C); });
+        merge_into_c<TK, 1, ACC>(acc, scale, U, pr, k0, O, c4, C, P, ca);
     }
 }
 
@@ -685,7 +712,7 @@ __device__ __forceinline__ void tiles_f32(int first, int end, int W, int lane, i
 
 template <int TK, bool ALIGNED, bool ACC>
 __global__ __launch_bounds__(64 * kWaves, 3) void k_spmm_f32(
-    const int4* __restrict__ units, int num_heavy, XcdSplit xs,
+    const int4* __restrict__ units, const int* __restrict__ rmap, int num_heavy, XcdSplit xs,
     const int* __restrict__ chunk_eptr, const int* __restrict__ chunk_cols,
     const int* __restrict__ chunk_dense, const uint32_t* __restrict__ entries,
     const float* __restrict__ dense_a, const float* __restrict__ B, int O, bool c4,
@@ -699,6 +726,7 @@ __global__ __launch_bounds__(64 * kWaves, 3) void k_spmm_f32(
     bool heavy;
     if (!schedule(num_heavy, xs, wave, u, heavy, ot)) return;
     const int4 U = units[u];
+    const PanelRows pr = panel_rows(U, rmap);
     const int k0 = ((blockIdx.y << (3 - xs.lgp)) + ot) * TK;
     const int c0 = k0 + VEC * n;
     floatx4 acc[VEC];
@@ -706,16 +734,16 @@ __global__ __launch_bounds__(64 * kWaves, 3) void k_spmm_f32(
     for (int q = 0; q < VEC; ++q) acc[q] = floatx4{0.f, 0.f, 0.f, 0.f};
     if (heavy) {
         CAhead<TK, kWaves> ca;
-        read_c_ahead<TK, kWaves>(ca, U, k0, O, c4, ACC, C);
+        read_c_ahead<TK, kWaves>(ca, U, pr, k0, O, c4, ACC, C);
         tiles_f32<TK, ALIGNED>(U.y + wave, U.z, kWaves, lane, n, g, c0, (long long)O, chunk_eptr,
                                chunk_cols, chunk_dense, entries, dense_a, B, At[wave], acc, [] {});
-        merge_into_c<TK, kWaves, ACC>(acc, 1.0f, U, k0, O, c4, C, P, ca);
+        merge_into_c<TK, kWaves, ACC>(acc, 1.0f, U, pr, k0, O, c4, C, P, ca);
     } else {
         CAhead<TK, 1> ca;
         tiles_f32<TK, ALIGNED>(U.y, U.z, 1, lane, n, g, c0, (long long)O, chunk_eptr, chunk_cols,
                                chunk_dense, entries, dense_a, B, At[wave], acc,
-                               [&] { read_c_ahead<TK, 1>(ca, U, k0, O, c4, ACC, C); });
-        merge_into_c<TK, 1, ACC>(acc, 1.0f, U, k0, O, c4, C, P, ca);
+                               [&] { read_c_ahead<TK, 1>(ca, U, pr, k0, O, c4, ACC, C); });
+        merge_into_c<TK, 1, ACC>(acc, 1.0f, U, pr, k0, O, c4, C, P, ca);
     }
 }
 
@@ -742,36 +770,38 @@ static void launch_tk_mode(const DeviceFormat& F, const void* dB, bool b_f16, in
     const dim3 grid((unsigned)(hwg + 8 * per_xcd), (unsigned)(otiles / G));
     const dim3 block(64 * kWaves);
     const int NH = F.num_heavy;
+    const int* rmap = F.row_map.n ? F.row_map.p : nullptr;
+    const int4* U = F.units.p;
+    const int *eptr = F.chunk_eptr.p, *cols = F.chunk_cols.p, *dense = F.chunk_dense.p;
+    const uint32_t* ent = F.entries.p;
     if (F.fp32) {
         const float* B = static_cast<const float*>(dB);
         if (aligned)
-            hipLaunchKernelGGL((k_spmm_f32<TK, true, ACC>), grid, block, 0, st, F.units.p, NH, xs,
-                               F.chunk_eptr.p, F.chunk_cols.p, F.chunk_dense.p, F.entries.p,
-                               F.dense_a32.p, B, O, c4, dC);
+            hipLaunchKernelGGL((k_spmm_f32<TK, true, ACC>), grid, block, 0, st, U, rmap, NH, xs,
+                               eptr, cols, dense, ent, F.dense_a32.p, B, O, c4, dC);
         else
-            hipLaunchKernelGGL((k_spmm_f32<TK, false, ACC>), grid, block, 0, st, F.units.p, NH, xs,
-                               F.chunk_eptr.p, F.chunk_cols.p, F.chunk_dense.p, F.entries.p,
-                               F.dense_a32.p, B, O, c4, dC);
+            hipLaunchKernelGGL((k_spmm_f32<TK, false, ACC>), grid, block, 0, st, U, rmap, NH, xs,
+                               eptr, cols, dense, ent, F.dense_a32.p, B, O, c4, dC);
     } else if (b_f16) {
         const _Float16* B = static_cast<const _Float16*>(dB);
         if (aligned)
-            hipLaunchKernelGGL((k_spmm_f16<TK, _Float16, true, ACC>), grid, block, 0, st, F.units.p, NH,
-                               xs, F.chunk_eptr.p, F.chunk_cols.p, F.chunk_dense.p, F.entries.p,
-                               F.dense_a16.p, B, O, F.scale, c4, dC);
+            hipLaunchKernelGGL((k_spmm_f16<TK, _Float16, true, ACC>), grid, block, 0, st, U, rmap,
+                               NH, xs, eptr, cols, dense, ent, F.dense_a16.p, B, O, F.scale, c4,
+                               dC);
         else
-            hipLaunchKernelGGL((k_spmm_f16<TK, _Float16, false, ACC>), grid, block, 0, st, F.units.p, NH,
-                               xs, F.chunk_eptr.p, F.chunk_cols.p, F.chunk_dense.p, F.entries.p,
-                               F.dense_a16.p, B, O, F.scale, c4, dC);
+            hipLaunchKernelGGL((k_spmm_f16<TK, _Float16, false, ACC>), grid, block, 0, st, U,
+                               rmap, NH, xs, eptr, cols, dense, ent, F.dense_a16.p, B, O,
+                               F.scale, c4, dC);
     } else if constexpr (TK <= 64) {
         const float* B = static_cast<const float*>(dB);
         if (aligned)
-            hipLaunchKernelGGL((k_spmm_f16<TK, float, true, ACC>), grid, block, 0, st, F.units.p, NH,
-                               xs, F.chunk_eptr.p, F.chunk_cols.p, F.chunk_dense.p, F.entries.p,
-                               F.dense_a16.p, B, O, F.scale, c4, dC);
+            hipLaunchKernelGGL((k_spmm_f16<TK, float, true, ACC>), grid, block, 0, st, U, rmap,
+                               NH, xs, eptr, cols, dense, ent, F.dense_a16.p, B, O, F.scale, c4,
+                               dC);
         else
-            hipLaunchKernelGGL((k_spmm_f16<TK, float, false, ACC>), grid, block, 0, st, F.units.p, NH,
-                               xs, F.chunk_eptr.p, F.chunk_cols.p, F.chunk_dense.p, F.entries.p,
-                               F.dense_a16.p, B, O, F.scale, c4, dC);
+            hipLaunchKernelGGL((k_spmm_f16<TK, float, false, ACC>), grid, block, 0, st, U, rmap,
+                               NH, xs, eptr, cols, dense, ent, F.dense_a16.p, B, O, F.scale, c4,
+                               dC);
     } else {
         // o_tile_width never gives an FP16 format reading FP32 B an O tile of 128.
         throw Error(VCSRMC_ERR_STATE, "no O tile of 128 for FP32 B with an FP16 format");
@@ -790,6 +820,7 @@ static void launch_tk(const DeviceFormat& F, const void* dB, bool b_f16, int O, 
 // units add into them through atomics.  One work-group per heavy unit; only a panel's first unit
 // (kUnitSplitFirst) writes, its masked rows over columns [0, O).
 __global__ __launch_bounds__(256) void k_zero_split_rows(const int4* __restrict__ units,
+                                                         const int* __restrict__ rmap,
                                                          int num_heavy, int O,
                                                          float* __restrict__ C) {
     const int u = blockIdx.x;
@@ -799,7 +830,7 @@ __global__ __launch_bounds__(256) void k_zero_split_rows(const int4* __restrict_
     const long long OL = O;
     for (int r = 0; r < kPanelRows; ++r) {
         if (!((U.w >> r) & 1)) continue;
-        float* row = C + (long long)(U.x + r) * OL;
+        float* row = C + (long long)(rmap ? rmap[U.x + r] : U.x + r) * OL;
         for (int c = threadIdx.x; c < O; c += 256) row[c] = 0.0f;
     }
 }
@@ -898,7 +929,7 @@ void spmm_launch(const DeviceFormat& F, const void* dB, bool b_f16, int O, int t
     }
     if (!accumulate && F.num_split_panels > 0) {
         hipLaunchKernelGGL(k_zero_split_rows, dim3((unsigned)F.num_heavy), dim3(256), 0, st,
-                           F.units.p, F.num_heavy, O, dC);
+                           F.units.p, F.row_map.n ? F.row_map.p : nullptr, F.num_heavy, O, dC);
         VCSRMC_HIP(hipGetLastError());
     }
     switch (o_tile_width(F, b_f16, O, tileK)) {
