@@ -50,7 +50,7 @@ typedef struct vcsrmc_info {
     int num_units;         /* kernel work units                         */
     int device;            /* HIP device the format lives on            */
     int num_dense;         /* tiles stored as dense 16 x 32 copies      */
-    int row_grouped;       /* 1: panels of rows grouped by shared columns */
+    int row_grouped;       /* 1: the layout's panels follow a row map      */
 } vcsrmc_info;
 
 /* Handle holding one device-resident format (the reference keeps one format in
@@ -163,12 +163,13 @@ int vcsrmc_rcm_order(const int *d_row_ptr, const int *d_col, int M, int N, int n
 int vcsrmc_set_rcm_limits(long long max_levels, long long max_rounds);
 
 /* Row order of the execution layout that later builds and uploads use (process-wide): 0 natural
- * order; 1 (the default) rows grouped by shared columns into 16-row panels where the natural
- * layout's tiles hold 48-256 nonzeros on average over at least 2048 panels and grouping saves
- * at least a tenth of the tiles; 2 always grouped.  Only the execution layout changes: the
- * format arrays, C's rows and the product are the same (up to rounding: the sums of a row are
- * formed in another order).  vcsrmc_info.row_grouped tells which a handle holds.  No
- * counterpart in the reference. */
+ * order; 1 (the default) rows without nonzeros after the others when they are at least an
+ * eighth of the rows, and rows grouped by shared columns into 16-row panels where the layout's
+ * tiles hold 48-256 nonzeros on average and grouping saves at least a tenth of the tiles; 2
+ * always grouped.  Only the execution layout changes: the format arrays, C's rows and the
+ * product are the same (up to rounding: the sums of a row are formed in another order).
+ * vcsrmc_info.row_grouped is 1 when a handle's layout has any row map.  No counterpart in the
+ * reference. */
 int vcsrmc_set_row_grouping(int mode);
 
 /* Relabels the columns of a device CSR in place, col[p] = position[col[p]], with every row

@@ -220,12 +220,14 @@ def test_mixed_tile_fill(orc, fp32, tileK):
 @pytest.mark.parametrize("tileK", [16, 32, 64, 128])
 def test_fp32_entry_tiles(orc, tileK):
     """FP32 formats of more than 256 panels keep their sparse tiles as entry lists, scattered
-    into the matrix-core operand through LDS: that path over 4,200-6,000-row matrices with empty
-    rows, two heavy rows (split panels) and sparse rows, O from 1 to 257, C starting non-zero."""
+    into the matrix-core operand through LDS: that path over 8,000-10,000-row matrices with
+    about a quarter of the rows empty (moved after the others: at least ~6,000 rows, 375 panels,
+    remain), two heavy rows (split panels) and sparse rows, O from 1 to 257, C starting
+    non-zero."""
     rng = np.random.default_rng(900 + tileK)
     for O in (1, 7, 100, 128, 257):
-        M, N = int(rng.integers(4200, 6000)), int(rng.integers(300, 9000))
-        rp, c, v = random_csr(rng, M, N, density=float(rng.choice([0.0005, 0.003])),
+        M, N = int(rng.integers(8000, 10000)), int(rng.integers(300, 9000))
+        rp, c, v = random_csr(rng, M, N, nnz_per_row=float(rng.choice([3.0, 8.0])),
                               empty_frac=0.2, heavy_rows=2, heavy_nnz=3000)
         B = rng.uniform(-1, 1, (N, O)).astype(np.float32)
         C0 = rng.uniform(-1, 1, (M, O)).astype(np.float32)

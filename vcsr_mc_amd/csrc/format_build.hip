@@ -686,23 +686,30 @@ static int g_row_grouping = 1;  // 0 off, 1 when it pays (default), 2 always
 void set_row_grouping(int mode) { g_row_grouping = mode; }
 int row_grouping() { return g_row_grouping; }
 
-// The execution layout in natural row order, or with rows grouped by shared columns
-// (row_groups.hip) where that gives fewer tiles.  By default the grouping is tried when the
-// natural layout's tiles hold 48-256 nonzeros on average (rows already sharing columns within
-// panels, tiles not yet full: grids and meshes in natural order) and at least 2048 panels
-// (smaller launches are latency-bound), and kept when it saves at least a tenth of the tiles.
-// Measured on gfx950 (27-point stencil 100^3 FP32 in 4 x 2 x 2 blocks, unchanged kernel: tiles
-// 365,224 -> 187,016, 564 -> 429 us accumulating, 508 -> 342 us overwriting).  Uniform random,
-// power-law and R-MAT matrices (about 31 nonzeros per tile: no shared columns to gather) and
-// 32 x 32 blocks (full tiles) keep natural order without the cost of trying.
+// The execution layout's row order.  Mode 0: natural.  Otherwise, first, rows without nonzeros
+// go after the others when they are at least an eighth of the rows (compact_rows; R-MAT scale
+// 22, about 45% of its rows empty: panels 231,761 -> 125,559, kernel 2.60 -> 2.54 ms
+// accumulating, scale 20 508 -> 488 us).  Then rows are grouped by shared columns
+// (row_groups.hip), always in mode 2, and in mode 1 (the default) when the layout's tiles hold
+// 48-256 nonzeros on average -- rows already sharing columns within panels, tiles not yet full:
+// grids and meshes in natural order -- keeping the grouped layout when it saves at least a
+// tenth of the tiles.  Measured on gfx950, kernel us natural -> grouped (C += A.B / C = A.B):
+// 27-point stencil FP32 20^3 7.97 / 7.49 -> 6.00 / 5.60, 60^3 126 / 109 -> 89 / 69, 100^3 564 /
+// 510 -> 447 / 359 (tiles 365,224 -> 187,016, 4 x 2 x 2 blocks), FP16 100^3 337 / 300 -> 316 /
+// 251; 16^3 (256 panels) within 2% either way.  Uniform random, power-law and R-MAT matrices
+// (about 31 nonzeros per tile: little shared between rows; grouping them anyway saved 1-7% of
+// the tiles and ran from 6% faster to 13% slower) and 32 x 32 blocks (full tiles) are not tried.
 static void build_exec_layout(DeviceFormat& F, const int* trow, const int* tcol, const float* tval,
                               long long n, hipStream_t st) {
     F.row_map.release();
-    build_layout_in_order(F, trow, tcol, tval, nullptr, n, st);
     const int mode = g_row_grouping;
+    DevBuf<int> cpos, cmap;
+    const bool compact = mode != 0 && compact_rows(trow, n, F.M, st, cpos, cmap);
+    build_layout_in_order(F, trow, tcol, tval, compact ? cpos.p : nullptr, n, st);
+    if (compact) F.row_map = std::move(cmap);
     if (mode == 0 || F.num_chunks == 0) return;
     const long long NC = F.num_chunks;
-    if (mode == 1 && !(F.num_panels >= kFewPanels && n >= 48 * NC && n < 256 * NC)) return;
+    if (mode == 1 && !(n >= 48 * NC && n < 256 * NC)) return;
     DevBuf<int> rowpos, row_map;
     if (!group_rows(trow, tcol, n, F.M, F.N, st, rowpos, row_map)) return;
     DeviceFormat G;

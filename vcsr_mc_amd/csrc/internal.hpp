@@ -109,8 +109,14 @@ float device_absmax(const float* d_val, long long n, hipStream_t st);
 // of M rows; M rounded up to 16 entries).  False when it found nothing to work with.
 bool group_rows(const int* trow, const int* tcol, long long n, int M, int N, hipStream_t st,
                 DevBuf<int>& rowpos, DevBuf<int>& row_map);
-// Row grouping in the execution layout: 0 natural order, 1 grouped where it saves tiles (the
-// default; format_build.hip, build_exec_layout), 2 always grouped.  Read by later builds.
+// The same maps for natural order with the rows that hold no nonzero moved after the others,
+// when they are at least an eighth of the rows (false otherwise): panels then hold 16 rows
+// with nonzeros instead of, on average, as many as the empty rows leave.
+bool compact_rows(const int* trow, long long n, int M, hipStream_t st, DevBuf<int>& rowpos,
+                  DevBuf<int>& row_map);
+// Row order of the execution layout: 0 natural order, 1 empty rows moved last and rows grouped
+// where that saves tiles (the default; format_build.hip, build_exec_layout), 2 always grouped.
+// Read by later builds.
 void set_row_grouping(int mode);
 int row_grouping();
 

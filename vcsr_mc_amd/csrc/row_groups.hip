@@ -325,7 +325,43 @@ void sort_keys(DevBuf<u64>& keys, DevBuf<u64>& alt, DevBuf<uint32_t>& pay,
     }
 }
 
+__global__ void k_flag_rows(const int* __restrict__ trow, long long n, int* __restrict__ flag) {
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) flag[trow[i]] = 1;
+}
+
+// Rows with nonzeros keep their order at positions 0..NE-1, the others follow in order.
+__global__ void k_compact_positions(const int* __restrict__ flag, const int* __restrict__ rank,
+                                    int M, int NE, int* __restrict__ rowpos,
+                                    int* __restrict__ row_map) {
+    const long long r = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (r >= M) return;
+    const int p = flag[r] ? rank[r] : NE + ((int)r - rank[r]);
+    rowpos[r] = p;
+    row_map[p] = (int)r;
+}
+
 }  // namespace
+
+bool compact_rows(const int* trow, long long n, int M, hipStream_t st, DevBuf<int>& rowpos,
+                  DevBuf<int>& row_map) {
+    if (M < 1 || n < 1) return false;
+    DevBuf<int> flag(M), rank((size_t)M + 1);
+    fill<int>(flag.p, M, 0, st);
+    hipLaunchKernelGGL(k_flag_rows, dim3(grid256(n)), dim3(256), 0, st, trow, n, flag.p);
+    VCSRMC_HIP(hipGetLastError());
+    exclusive_sum<int, int>(flag.p, rank.p, M, st);
+    const int NE = read_scalar(rank.p + M, st);
+    if (8LL * (M - NE) < M) return false;
+    const int P = ((M + kPanelRows - 1) / kPanelRows) * kPanelRows;
+    rowpos.alloc(M);
+    row_map.alloc(P);
+    fill<int>(row_map.p, P, -1, st);
+    hipLaunchKernelGGL(k_compact_positions, dim3(grid256(M)), dim3(256), 0, st, flag.p, rank.p, M,
+                       NE, rowpos.p, row_map.p);
+    VCSRMC_HIP(hipGetLastError());
+    return true;
+}
 
 bool group_rows(const int* trow, const int* tcol, long long n, int M, int N, hipStream_t st,
                 DevBuf<int>& rowpos, DevBuf<int>& row_map) {
