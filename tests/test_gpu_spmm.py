@@ -487,7 +487,8 @@ def test_overwrite_equals_zero_then_accumulate(orc, fp32, tileK, O):
     """C = A.B (the overwrite flag, C never read) against C zeroed and C += A.B: bit for bit on
     every row outside split panels; split panels (several units adding through atomics into
     rows the launcher clears first) within the parity norm of the oracle.  Rows without
-    nonzeros keep what C held, bit for bit."""
+    nonzeros keep what C held, bit for bit.  The layout is kept in natural row order, where
+    _split_rows knows which panels are split (row maps: tests/test_gpu_row_groups.py)."""
     import torch
     rng = np.random.default_rng(31 + tileK + O + fp32)
     M, N = 900, 5000
@@ -497,7 +498,13 @@ def test_overwrite_equals_zero_then_accumulate(orc, fp32, tileK, O):
     split = _split_rows(rp, c, M, N)
     assert split.any()
     say("overwrite vs accumulate", fp32, tileK, O)
-    with vm.DeviceFormat.from_device_csr(dev(rp), dev(c), dev(v), M, N, fp32, 32) as f:
+    vm.set_row_grouping(vm.ROW_GROUPING_OFF)
+    try:
+        f = vm.DeviceFormat.from_device_csr(dev(rp), dev(c), dev(v), M, N, fp32, 32)
+    finally:
+        vm.set_row_grouping(vm.ROW_GROUPING_AUTO)
+    assert f.info()["row_grouped"] == 0
+    with f:
         dB = dev(B) if fp32 else dev(B).half()
         Ca = torch.zeros((M, O), dtype=torch.float32, device="cuda")
         f.spmm(dB, Ca, tileK=tileK)

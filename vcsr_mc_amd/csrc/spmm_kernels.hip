@@ -106,23 +106,28 @@ __device__ __forceinline__ void wave_lds_sync() {
 }
 
 // The C rows of a unit's 16 panel rows: U.x .. U.x + 15 for a layout in natural row order;
-// for a layout with a row map (rows grouped by shared columns), rmap[U.x + r], which lane r
-// loads once per unit and row() reads across lanes -- so every lane of the wave executes row()
-// together, outside branches that depend on the lane.
+// for a layout with a row map (MAPPED), rmap[U.x + r], which lane r loads once per unit and
+// row() reads across lanes -- so every lane of the wave executes row() together, outside
+// branches that depend on the lane.  MAPPED is a kernel template parameter: with a run-time
+// flag the natural-order kernels still paid for the cross-lane reads (power-law 36,692^2
+// 15.0 -> 15.6 us).
+template <bool MAPPED>
 struct PanelRows {
-    int base;   // U.x
-    int mine;   // mapped: the C row of panel row (lane & 15)
-    bool mapped;
+    int base;  // U.x
+    int mine;  // MAPPED: the C row of panel row (lane & 15)
     __device__ __forceinline__ long long row(int r) const {
-        return mapped ? (long long)__shfl(mine, r) : (long long)(base + r);
+        if constexpr (MAPPED) return (long long)__shfl(mine, r);
+        else return (long long)(base + r);
     }
 };
 
-__device__ __forceinline__ PanelRows panel_rows(const int4& U, const int* __restrict__ rmap) {
-    PanelRows p;
+template <bool MAPPED>
+__device__ __forceinline__ PanelRows<MAPPED> panel_rows(const int4& U,
+                                                        const int* __restrict__ rmap) {
+    PanelRows<MAPPED> p;
     p.base = U.x;
-    p.mapped = rmap != nullptr;
-    p.mine = p.mapped ? rmap[U.x + (threadIdx.x & 15)] : 0;
+    if constexpr (MAPPED) p.mine = rmap[U.x + (threadIdx.x & 15)];
+    else p.mine = 0;
     return p;
 }
 
@@ -141,9 +146,9 @@ struct CAhead {
     floatx4 v[N > 0 ? N : 1];
 };
 
-template <int TK, int W>
+template <int TK, int W, typename PR>
 __device__ __forceinline__ void read_c_ahead(CAhead<TK, W>& ca, const int4& U,
-                                             const PanelRows& pr, int k0, int O, bool c4,
+                                             const PR& pr, int k0, int O, bool c4,
                                              bool accumulate, const float* __restrict__ C) {
     constexpr int VEC = TK / 16;
     constexpr int N = CAhead<TK, W>::N;
@@ -215,9 +220,9 @@ __device__ __forceinline__ void store_c4(float* p, const floatx4& v) {
 // consecutive threads on consecutive columns.  Split panels merge through atomics; other rows
 // are a read-modify-write (C += A.B) whose read came from read_c_ahead.  Rows outside the
 // panel's row mask are never touched.
-template <int TK, int W, bool ACC>
+template <int TK, int W, bool ACC, typename PR>
 __device__ __forceinline__ void merge_into_c(const floatx4 (&acc)[TK / 16], float scale,
-                                             const int4& U, const PanelRows& pr, int k0, int O,
+                                             const int4& U, const PR& pr, int k0, int O,
                                              bool c4, float* __restrict__ C, float* P,
                                              const CAhead<TK, W>& ca) {
     constexpr int VEC = TK / 16;
@@ -470,7 +475,7 @@ __device__ __forceinline__ void tiles_f16(int first, int end, int W, int lane, i
 template <typename TB, bool ALIGNED>
 constexpr int f16_min_waves() { return (sizeof(TB) == 2 && ALIGNED) ? 3 : 2; }
 
-template <int TK, typename TB, bool ALIGNED, bool ACC>
+template <int TK, typename TB, bool ALIGNED, bool ACC, bool MAPPED>
 __global__ __launch_bounds__(64 * kWaves, (f16_min_waves<TB, ALIGNED>())) void k_spmm_f16(
     const int4* __restrict__ units, const int* __restrict__ rmap, int num_heavy, XcdSplit xs,
     const int* __restrict__ chunk_eptr, const int* __restrict__ chunk_cols,
@@ -488,7 +493,7 @@ __global__ __launch_bounds__(64 * kWaves, (f16_min_waves<TB, ALIGNED>())) void k
     bool heavy;
     if (!schedule(num_heavy, xs, wave, u, heavy, ot)) return;
     const int4 U = units[u];
-    const PanelRows pr = panel_rows(U, rmap);
+    const PanelRows<MAPPED> pr = panel_rows<MAPPED>(U, rmap);
     const int k0 = ((blockIdx.y << (3 - xs.lgp)) + ot) * TK;
     const int c0 = k0 + VEC * n;
     floatx4 acc[VEC];
@@ -710,7 +715,7 @@ __device__ __forceinline__ void tiles_f32(int first, int end, int W, int lane, i
     }
 }
 
-template <int TK, bool ALIGNED, bool ACC>
+template <int TK, bool ALIGNED, bool ACC, bool MAPPED>
 __global__ __launch_bounds__(64 * kWaves, 3) void k_spmm_f32(
     const int4* __restrict__ units, const int* __restrict__ rmap, int num_heavy, XcdSplit xs,
     const int* __restrict__ chunk_eptr, const int* __restrict__ chunk_cols,
@@ -726,7 +731,7 @@ __global__ __launch_bounds__(64 * kWaves, 3) void k_spmm_f32(
     bool heavy;
     if (!schedule(num_heavy, xs, wave, u, heavy, ot)) return;
     const int4 U = units[u];
-    const PanelRows pr = panel_rows(U, rmap);
+    const PanelRows<MAPPED> pr = panel_rows<MAPPED>(U, rmap);
     const int k0 = ((blockIdx.y << (3 - xs.lgp)) + ot) * TK;
     const int c0 = k0 + VEC * n;
     floatx4 acc[VEC];
@@ -747,7 +752,7 @@ __global__ __launch_bounds__(64 * kWaves, 3) void k_spmm_f32(
     }
 }
 
-template <int TK, bool ACC>
+template <int TK, bool ACC, bool MAPPED>
 static void launch_tk_mode(const DeviceFormat& F, const void* dB, bool b_f16, int O, float* dC,
                            hipStream_t st) {
     constexpr int VEC = TK / 16;
@@ -777,29 +782,29 @@ static void launch_tk_mode(const DeviceFormat& F, const void* dB, bool b_f16, in
     if (F.fp32) {
         const float* B = static_cast<const float*>(dB);
         if (aligned)
-            hipLaunchKernelGGL((k_spmm_f32<TK, true, ACC>), grid, block, 0, st, U, rmap, NH, xs,
+            hipLaunchKernelGGL((k_spmm_f32<TK, true, ACC, MAPPED>), grid, block, 0, st, U, rmap, NH, xs,
                                eptr, cols, dense, ent, F.dense_a32.p, B, O, c4, dC);
         else
-            hipLaunchKernelGGL((k_spmm_f32<TK, false, ACC>), grid, block, 0, st, U, rmap, NH, xs,
+            hipLaunchKernelGGL((k_spmm_f32<TK, false, ACC, MAPPED>), grid, block, 0, st, U, rmap, NH, xs,
                                eptr, cols, dense, ent, F.dense_a32.p, B, O, c4, dC);
     } else if (b_f16) {
         const _Float16* B = static_cast<const _Float16*>(dB);
         if (aligned)
-            hipLaunchKernelGGL((k_spmm_f16<TK, _Float16, true, ACC>), grid, block, 0, st, U, rmap,
+            hipLaunchKernelGGL((k_spmm_f16<TK, _Float16, true, ACC, MAPPED>), grid, block, 0, st, U, rmap,
                                NH, xs, eptr, cols, dense, ent, F.dense_a16.p, B, O, F.scale, c4,
                                dC);
         else
-            hipLaunchKernelGGL((k_spmm_f16<TK, _Float16, false, ACC>), grid, block, 0, st, U,
+            hipLaunchKernelGGL((k_spmm_f16<TK, _Float16, false, ACC, MAPPED>), grid, block, 0, st, U,
                                rmap, NH, xs, eptr, cols, dense, ent, F.dense_a16.p, B, O,
                                F.scale, c4, dC);
     } else if constexpr (TK <= 64) {
         const float* B = static_cast<const float*>(dB);
         if (aligned)
-            hipLaunchKernelGGL((k_spmm_f16<TK, float, true, ACC>), grid, block, 0, st, U, rmap,
+            hipLaunchKernelGGL((k_spmm_f16<TK, float, true, ACC, MAPPED>), grid, block, 0, st, U, rmap,
                                NH, xs, eptr, cols, dense, ent, F.dense_a16.p, B, O, F.scale, c4,
                                dC);
         else
-            hipLaunchKernelGGL((k_spmm_f16<TK, float, false, ACC>), grid, block, 0, st, U, rmap,
+            hipLaunchKernelGGL((k_spmm_f16<TK, float, false, ACC, MAPPED>), grid, block, 0, st, U, rmap,
                                NH, xs, eptr, cols, dense, ent, F.dense_a16.p, B, O, F.scale, c4,
                                dC);
     } else {
@@ -812,8 +817,14 @@ static void launch_tk_mode(const DeviceFormat& F, const void* dB, bool b_f16, in
 template <int TK>
 static void launch_tk(const DeviceFormat& F, const void* dB, bool b_f16, int O, float* dC,
                       bool accumulate, hipStream_t st) {
-    if (accumulate) launch_tk_mode<TK, true>(F, dB, b_f16, O, dC, st);
-    else launch_tk_mode<TK, false>(F, dB, b_f16, O, dC, st);
+    const bool mapped = F.row_map.n > 0;
+    if (accumulate) {
+        if (mapped) launch_tk_mode<TK, true, true>(F, dB, b_f16, O, dC, st);
+        else launch_tk_mode<TK, true, false>(F, dB, b_f16, O, dC, st);
+    } else {
+        if (mapped) launch_tk_mode<TK, false, true>(F, dB, b_f16, O, dC, st);
+        else launch_tk_mode<TK, false, false>(F, dB, b_f16, O, dC, st);
+    }
 }
 
 // Before an overwriting launch (C = A.B), the rows of every split panel are set to zero: their
