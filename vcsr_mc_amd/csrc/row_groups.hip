@@ -20,8 +20,8 @@
 // Finally the rows are ordered by their group's first row (rows in a group by index); rows
 // without nonzeros go last, so they fill no panel.
 //
-// Every loop is bounded (levels, rounds, probes, insertions per cluster), and the same input
-// gives the same order: candidate tables are per cluster and the sorts are stable.
+// Every loop is bounded (levels, rounds, probes, insertions per cluster: a cluster whose
+// candidates overflow its table keeps the ones it counted first), and the sorts are stable.
 #include <algorithm>
 #include <climits>
 
