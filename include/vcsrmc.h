@@ -164,9 +164,10 @@ int vcsrmc_set_rcm_limits(long long max_levels, long long max_rounds);
 
 /* Row order of the execution layout that later builds and uploads use (process-wide): 0 natural
  * order; 1 (the default) rows without nonzeros after the others when they are at least an
- * eighth of the rows, and rows grouped by shared columns into 16-row panels where the layout's
- * tiles hold 48-256 nonzeros on average and grouping saves at least a tenth of the tiles; 2
- * always grouped.  Only the execution layout changes: the format arrays, C's rows and the
+ * eighth of the rows, and rows grouped by shared columns into 16-row panels where the rows of a
+ * panel already share columns (at least 1.3 nonzeros per distinct column of a panel: grids and
+ * meshes), tiles are not full and grouping saves at least a tenth of the tiles; 2 always
+ * grouped.  Only the execution layout changes: the format arrays, C's rows and the
  * product are the same (up to rounding: the sums of a row are formed in another order).
  * vcsrmc_info.row_grouped is 1 when a handle's layout has any row map.  No counterpart in the
  * reference. */

@@ -78,3 +78,16 @@ def test_upload_refuses_short_arrays_without_gpu(field, delta):
     with pytest.raises(vm.VCSRMCError) as e:
         vm.DeviceFormat.from_host_format(V)
     assert e.value.status == vm.ERR_FORMAT and field in str(e.value)
+
+
+def test_row_grouping_mode_checked_without_gpu():
+    """vcsrmc_set_row_grouping accepts 0, 1 and 2 and refuses anything else before any device
+    work; the default (1) is restored."""
+    import vcsr_mc_amd as vm
+    for mode in (vm.ROW_GROUPING_OFF, vm.ROW_GROUPING_ALWAYS, vm.ROW_GROUPING_AUTO):
+        vm.set_row_grouping(mode)
+    for bad in (-1, 3):
+        with pytest.raises(vm.VCSRMCError) as e:
+            vm.set_row_grouping(bad)
+        assert e.value.status == vm.ERR_ARG
+    vm.set_row_grouping(vm.ROW_GROUPING_AUTO)

@@ -163,3 +163,45 @@ def test_uniform_rows_keep_natural_order(grouping):
         assert f.info()["row_grouped"] == 0
     with pytest.raises(vm.VCSRMCError):
         vm.set_row_grouping(3)
+
+
+def grid5(g):
+    """5-point stencil on a g x g grid in natural order (x fastest)."""
+    idx = np.arange(g * g)
+    x, y = idx % g, idx // g
+    cols = []
+    for dx, dy in ((0, -1), (-1, 0), (0, 0), (1, 0), (0, 1)):
+        xx, yy = x + dx, y + dy
+        cols.append(np.where((xx >= 0) & (xx < g) & (yy >= 0) & (yy < g), xx + g * yy, -1))
+    C = np.sort(np.stack(cols, axis=1), axis=1)
+    keep = C >= 0
+    rp = np.zeros(g * g + 1, np.int32)
+    rp[1:] = np.cumsum(keep.sum(axis=1))
+    return rp, C[keep].astype(np.int32)
+
+
+@pytest.mark.parametrize("fp32", [True, False])
+def test_grid2d_grouped_by_default(orc, grouping, fp32):
+    """A 5-point stencil on a 256^2 grid (1.6 nonzeros per distinct column of a panel in natural
+    order, 40 per tile): the default layout groups it, 16-row strips (50 columns, 2 tiles)
+    becoming 4 x 4 blocks (32 columns, 1 tile), and the product matches the oracle in both
+    launch modes."""
+    rng = np.random.default_rng(57 + fp32)
+    g = 256
+    rp, c = grid5(g)
+    v = rng.uniform(-1, 1, c.size).astype(np.float32)
+    M = N = g * g
+    O = 64
+    B = rng.uniform(-1, 1, (N, O)).astype(np.float32)
+    if not fp32:
+        B = B.astype(np.float16).astype(np.float32)
+    C0 = rng.uniform(-1, 1, (M, O)).astype(np.float32)
+    grouping(vm.ROW_GROUPING_OFF)
+    with vm.DeviceFormat.from_device_csr(dev(rp), dev(c), dev(v), M, N, fp32, 32) as f:
+        natural = f.info()
+    grouping(vm.ROW_GROUPING_AUTO)
+    for overwrite in (False, True):
+        say("grid2d grouped", fp32, overwrite)
+        info = run(orc, rp, c, v, M, N, B, fp32, 64, O, C0, overwrite)
+        assert info["row_grouped"] == 1
+        assert info["num_chunks"] <= 0.55 * natural["num_chunks"], (info, natural)

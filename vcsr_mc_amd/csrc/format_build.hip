@@ -555,6 +555,7 @@ static void build_exec_layout_k(DeviceFormat& F, const int* trow, const int* tco
     inclusive_sum<int, int>(hpanel.p, pin.p, n, st);
     check_err(err.p, st);
     const int NP = read_scalar(pin.p + (n - 1), st);
+    F.num_pairs = read_scalar(dc.p + (n - 1), st);
 
     DevBuf<int> pstart(NP + 1), ppanel(NP), nch(NP), cbase(NP + 1), pmask(NP);
     LAUNCH((k_panel_starts<K>), n, kp, hpanel.p, pin.p, n, cbits, pstart.p, ppanel.p);
@@ -651,6 +652,7 @@ static void build_layout_in_order(DeviceFormat& F, const int* trow, const int* t
                                   const float* tval, const int* rowpos, long long n,
                                   hipStream_t st) {
     F.num_panels = F.num_chunks = F.num_units = F.num_dense = 0;
+    F.num_pairs = 0;
     if (n == 0) return;
     const int num_panels_all = (F.M + kPanelRows - 1) / kPanelRows;
     const int cbits = bits_for(F.N > 0 ? (unsigned long long)(F.N - 1) : 0ull);
@@ -670,6 +672,7 @@ static void swap_layout(DeviceFormat& a, DeviceFormat& b) {
     std::swap(a.light_max, b.light_max);
     std::swap(a.heavy_tiles, b.heavy_tiles);
     std::swap(a.num_split_panels, b.num_split_panels);
+    std::swap(a.num_pairs, b.num_pairs);
     std::swap(a.xcd_start, b.xcd_start);
     std::swap(a.units, b.units);
     std::swap(a.row_map, b.row_map);
@@ -690,15 +693,17 @@ int row_grouping() { return g_row_grouping; }
 // go after the others when they are at least an eighth of the rows (compact_rows; R-MAT scale
 // 22, about 45% of its rows empty: panels 231,761 -> 125,559, kernel 2.60 -> 2.54 ms
 // accumulating, scale 20 508 -> 488 us).  Then rows are grouped by shared columns
-// (row_groups.hip), always in mode 2, and in mode 1 (the default) when the layout's tiles hold
-// 48-256 nonzeros on average -- rows already sharing columns within panels, tiles not yet full:
-// grids and meshes in natural order -- keeping the grouped layout when it saves at least a
-// tenth of the tiles.  Measured on gfx950, kernel us natural -> grouped (C += A.B / C = A.B):
-// 27-point stencil FP32 20^3 7.97 / 7.49 -> 6.00 / 5.60, 60^3 126 / 109 -> 89 / 69, 100^3 564 /
-// 510 -> 447 / 359 (tiles 365,224 -> 187,016, 4 x 2 x 2 blocks), FP16 100^3 337 / 300 -> 316 /
-// 251; 16^3 (256 panels) within 2% either way.  Uniform random, power-law and R-MAT matrices
-// (about 31 nonzeros per tile: little shared between rows; grouping them anyway saved 1-7% of
-// the tiles and ran from 6% faster to 13% slower) and 32 x 32 blocks (full tiles) are not tried.
+// (row_groups.hip), always in mode 2, and in mode 1 (the default) when the rows of a panel
+// already share columns -- at least 1.3 nonzeros per distinct (panel, column) pair, as in grids
+// and meshes in natural order (2D 5-point 1.6, 3D 7-point 1.37, 27-point 2.66) and not in
+// uniform random, power-law or R-MAT matrices (1.01-1.23 at scales 16-22) -- and the tiles are
+// not full (fewer than 256 nonzeros on average), keeping the grouped layout when it saves at
+// least a tenth of the tiles.  Measured on gfx950, kernel us natural -> grouped (C += A.B /
+// C = A.B): 27-point stencil FP32 20^3 7.97 / 7.49 -> 6.00 / 5.60, 60^3 126 / 109 -> 89 / 69,
+// 100^3 564 / 510 -> 447 / 359 (tiles 365,224 -> 187,016, 4 x 2 x 2 blocks), FP16 100^3 337 /
+// 300 -> 316 / 251; 2D 5-point 1000^2 FP32 312 / 234 -> 297 / 196 (tiles halved); 3D 7-point
+// 100^3 FP32 390 / 328 -> 373 / 255; 27-point 16^3 (256 panels) within 2% either way.  Grouping
+// the excluded classes anyway saved 1-7% of their tiles and ran from 6% faster to 13% slower.
 static void build_exec_layout(DeviceFormat& F, const int* trow, const int* tcol, const float* tval,
                               long long n, hipStream_t st) {
     F.row_map.release();
@@ -709,7 +714,18 @@ static void build_exec_layout(DeviceFormat& F, const int* trow, const int* tcol,
     if (compact) F.row_map = std::move(cmap);
     if (mode == 0 || F.num_chunks == 0) return;
     const long long NC = F.num_chunks;
-    if (mode == 1 && !(n >= 48 * NC && n < 256 * NC)) return;
+    if (mode == 1) {
+        if (!(10 * n >= 13 * F.num_pairs && n < 256 * NC)) return;
+        // Grouping is an optimisation here: it is skipped, natural order kept, unless its buffers
+        // (at most ~64 bytes per nonzero and per row, for the sorts and a second layout) fit
+        // in half the free device memory.
+        size_t free_b = 0, total_b = 0;
+        if (hipMemGetInfo(&free_b, &total_b) != hipSuccess) {
+            (void)hipGetLastError();
+            return;
+        }
+        if (64.0 * (double)n + 64.0 * (double)F.M > 0.5 * (double)free_b) return;
+    }
     DevBuf<int> rowpos, row_map;
     if (!group_rows(trow, tcol, n, F.M, F.N, st, rowpos, row_map)) return;
     DeviceFormat G;

@@ -77,6 +77,7 @@ struct DeviceFormat {
 
     int num_panels = 0, num_chunks = 0, num_units = 0, num_heavy = 0, light_max = 0;
     int heavy_tiles = 0;       // largest heavy unit, in tiles
+    long long num_pairs = 0;   // distinct (panel, column) pairs: the tiles' filled columns
     int num_split_panels = 0;  // panels cut into several units
     // Light units [num_heavy + xcd_start[x], num_heavy + xcd_start[x + 1]) run on XCD x.
     int xcd_start[9] = {0, 0, 0, 0, 0, 0, 0, 0, 0};

@@ -190,13 +190,14 @@ __global__ __launch_bounds__(256) void k_score(const u64* __restrict__ crk,
         }
         int b = -1;
         if (best != 0 && m == best && ms >= 0) {
-            // the lane holding the maximum (keys are distinct: the hash and nearness differ)
+            // a lane holding the maximum; keys of two candidates tie only if their nearness,
+            // phase and 18-bit pair hash all agree, and then the lowest lane's candidate is kept
+            // and the other dropped
             b = K[lane + 64 * ms];
 #pragma unroll
             for (int s = 0; s < kTable / 64; ++s)
                 if (s == ms) score[s] = 0;
         }
-        // broadcast b from the owner lane (at most one lane has b >= 0)
         const unsigned long long own = __ballot(b >= 0);
         int chosen = -1;
         if (own) chosen = __shfl(b, (int)__builtin_ctzll(own));
