@@ -205,3 +205,67 @@ def test_grid2d_grouped_by_default(orc, grouping, fp32):
         info = run(orc, rp, c, v, M, N, B, fp32, 64, O, C0, overwrite)
         assert info["row_grouped"] == 1
         assert info["num_chunks"] <= 0.55 * natural["num_chunks"], (info, natural)
+
+
+def test_grouping_edge_cases(orc, grouping):
+    """Always-grouped layouts on inputs the matching has to step around: one column shared by
+    every row (a hub, so nothing to match on), a single column, rows of more than 512 columns
+    beside short ones, 31 and 32 rows, and a matrix whose rows are almost all empty."""
+    grouping(vm.ROW_GROUPING_ALWAYS)
+    rng = np.random.default_rng(71)
+    cases = []
+    M, N = 500, 100
+    rows = [np.array([7]) for _ in range(M)]
+    cases.append(("one shared column", M, N, rows))
+    M, N = 200, 1
+    cases.append(("single column", M, N, [np.array([0]) for _ in range(M)]))
+    M, N = 300, 2000
+    rows = [np.sort(rng.choice(N, size=5, replace=False)) for _ in range(M)]
+    for r in (3, 77, 150, 151, 299):
+        rows[r] = np.sort(rng.choice(N, size=1500, replace=False))
+    cases.append(("long rows", M, N, rows))
+    for M in (31, 32):
+        cases.append((f"{M} rows", M, 64, [np.sort(rng.choice(64, size=6, replace=False))
+                                           for _ in range(M)]))
+    M, N = 5000, 300
+    rows = [np.zeros(0, np.int64) for _ in range(M)]
+    for r in rng.choice(M, size=40, replace=False):
+        rows[r] = np.sort(rng.choice(N, size=int(rng.integers(1, 30)), replace=False))
+    cases.append(("almost all rows empty", M, N, rows))
+    for name, M, N, rows in cases:
+        rp = np.zeros(M + 1, np.int32)
+        rp[1:] = np.cumsum([len(x) for x in rows])
+        c = np.concatenate(rows).astype(np.int32)
+        v = rng.uniform(-1, 1, c.size).astype(np.float32)
+        for fp32 in (True, False):
+            O = 40
+            B = rng.uniform(-1, 1, (N, O)).astype(np.float32)
+            if not fp32:
+                B = B.astype(np.float16).astype(np.float32)
+            C0 = rng.uniform(-1, 1, (M, O)).astype(np.float32)
+            say("grouping edge case", name, fp32)
+            run(orc, rp, c, v, M, N, B, fp32, 64, O, C0, False)
+
+
+def test_noalloc_on_grouped_layout(grouping):
+    """vcsrmc_spmm_noalloc reads the same row map as vcsrmc_spmm_ex: equal results, bit for bit
+    (a 5-point grid has no split panels), on two calls in a row, the second with a smaller O."""
+    import torch
+    rp, c = grid5(96)
+    M = N = 96 * 96
+    rng = np.random.default_rng(73)
+    v = rng.uniform(-1, 1, c.size).astype(np.float32)
+    grouping(vm.ROW_GROUPING_ALWAYS)
+    with vm.DeviceFormat.from_device_csr(dev(rp), dev(c), dev(v), M, N, True, 32) as f:
+        assert f.info()["row_grouped"] == 1
+        stream = int(torch.cuda.current_stream().cuda_stream)
+        for O in (128, 40):
+            say("noalloc grouped", O)
+            dB = dev(rng.uniform(-1, 1, (N, O)).astype(np.float32))
+            want = torch.zeros((M, O), dtype=torch.float32, device="cuda")
+            got = torch.zeros_like(want)
+            f.spmm(dB, want, tileK=128)
+            assert vm.lib().vcsrmc_spmm_noalloc(f.handle, dB.data_ptr(), vm.B_F32, O, 128,
+                                                got.data_ptr(), 0, stream) == vm.OK
+            torch.cuda.synchronize()
+            assert torch.equal(got, want)
