@@ -42,10 +42,12 @@ struct XcdSplit {
 // item_gend.
 //
 // Execution layout (what the multiply kernels read), derived from the same matrix:
-//   units[u]        = {row0, chunk_begin, chunk_end, rowmask | flags}
-//                     a run of chunks of one 16-row panel; kUnitSplit = the panel has several
-//                     units, whose partial sums meet in C through atomics, kUnitSplitFirst =
-//                     the first of them.  The first
+//   units[u]        = {pos0, chunk_begin, chunk_end, rowmask | flags}
+//                     a run of chunks of one panel, the 16 row-order positions pos0 .. pos0 + 15
+//                     (rows pos0 + r in natural order, row_map[pos0 + r] with a row map;
+//                     rowmask bit r = that position holds a row with nonzeros); kUnitSplit =
+//                     the panel has several units, whose partial sums meet in C through
+//                     atomics, kUnitSplitFirst = the first of them.  The first
 //                     num_heavy units are heavy (one work-group each, larger first), the rest
 //                     light (one wave each, four per work-group, in panel order; XCD x runs
 //                     the range starting at xcd_start[x], cut for equal tile counts).

@@ -1,7 +1,8 @@
 // spmm_kernels.hip -- C += A.B for the VCSR-MC format on gfx950 MFMA.
 //
 // Work decomposition (atomic-free for all but split panels):
-//   a work unit is a run of compacted tiles of one 16-row panel, for one tileK-wide slice of
+//   a work unit is a run of compacted tiles of one 16-row panel (16 consecutive rows, or the
+//   16 rows the layout's row map groups), for one tileK-wide slice of
 //   the output columns.  A light unit is one 64-lane wave, which keeps the 16 x tileK
 //   accumulator tile in registers across its tiles and writes C once; a heavy unit is shared by
 //   the four waves of a work-group, which take its tiles round robin and sum their partial tiles
@@ -770,7 +771,8 @@ static void launch_tk_mode(const DeviceFormat& F, const void* dB, bool b_f16, in
     for (int x = 0; x < 9; ++x) xs.start[x] = F.xcd_start[x];
     int per_xcd = 0;  // light work-groups per XCD
     for (int r = 0; r < parts; ++r)
-        per_xcd = std::max(per_xcd, (xs.start[(r + 1) * G] - xs.start[r * G] + kWaves - 1) / kWaves);
+        per_xcd = std::max(per_xcd,
+                           (xs.start[(r + 1) * G] - xs.start[r * G] + kWaves - 1) / kWaves);
     const int hwg = 8 * ((F.num_heavy + parts - 1) / parts);
     const dim3 grid((unsigned)(hwg + 8 * per_xcd), (unsigned)(otiles / G));
     const dim3 block(64 * kWaves);
@@ -782,31 +784,31 @@ static void launch_tk_mode(const DeviceFormat& F, const void* dB, bool b_f16, in
     if (F.fp32) {
         const float* B = static_cast<const float*>(dB);
         if (aligned)
-            hipLaunchKernelGGL((k_spmm_f32<TK, true, ACC, MAPPED>), grid, block, 0, st, U, rmap, NH, xs,
-                               eptr, cols, dense, ent, F.dense_a32.p, B, O, c4, dC);
+            hipLaunchKernelGGL((k_spmm_f32<TK, true, ACC, MAPPED>), grid, block, 0, st, U, rmap,
+                               NH, xs, eptr, cols, dense, ent, F.dense_a32.p, B, O, c4, dC);
         else
-            hipLaunchKernelGGL((k_spmm_f32<TK, false, ACC, MAPPED>), grid, block, 0, st, U, rmap, NH, xs,
-                               eptr, cols, dense, ent, F.dense_a32.p, B, O, c4, dC);
+            hipLaunchKernelGGL((k_spmm_f32<TK, false, ACC, MAPPED>), grid, block, 0, st, U, rmap,
+                               NH, xs, eptr, cols, dense, ent, F.dense_a32.p, B, O, c4, dC);
     } else if (b_f16) {
         const _Float16* B = static_cast<const _Float16*>(dB);
         if (aligned)
-            hipLaunchKernelGGL((k_spmm_f16<TK, _Float16, true, ACC, MAPPED>), grid, block, 0, st, U, rmap,
-                               NH, xs, eptr, cols, dense, ent, F.dense_a16.p, B, O, F.scale, c4,
-                               dC);
+            hipLaunchKernelGGL((k_spmm_f16<TK, _Float16, true, ACC, MAPPED>), grid, block, 0, st,
+                               U, rmap, NH, xs, eptr, cols, dense, ent, F.dense_a16.p, B, O,
+                               F.scale, c4, dC);
         else
-            hipLaunchKernelGGL((k_spmm_f16<TK, _Float16, false, ACC, MAPPED>), grid, block, 0, st, U,
-                               rmap, NH, xs, eptr, cols, dense, ent, F.dense_a16.p, B, O,
+            hipLaunchKernelGGL((k_spmm_f16<TK, _Float16, false, ACC, MAPPED>), grid, block, 0, st,
+                               U, rmap, NH, xs, eptr, cols, dense, ent, F.dense_a16.p, B, O,
                                F.scale, c4, dC);
     } else if constexpr (TK <= 64) {
         const float* B = static_cast<const float*>(dB);
         if (aligned)
-            hipLaunchKernelGGL((k_spmm_f16<TK, float, true, ACC, MAPPED>), grid, block, 0, st, U, rmap,
-                               NH, xs, eptr, cols, dense, ent, F.dense_a16.p, B, O, F.scale, c4,
-                               dC);
+            hipLaunchKernelGGL((k_spmm_f16<TK, float, true, ACC, MAPPED>), grid, block, 0, st, U,
+                               rmap, NH, xs, eptr, cols, dense, ent, F.dense_a16.p, B, O, F.scale,
+                               c4, dC);
         else
-            hipLaunchKernelGGL((k_spmm_f16<TK, float, false, ACC, MAPPED>), grid, block, 0, st, U, rmap,
-                               NH, xs, eptr, cols, dense, ent, F.dense_a16.p, B, O, F.scale, c4,
-                               dC);
+            hipLaunchKernelGGL((k_spmm_f16<TK, float, false, ACC, MAPPED>), grid, block, 0, st, U,
+                               rmap, NH, xs, eptr, cols, dense, ent, F.dense_a16.p, B, O, F.scale,
+                               c4, dC);
     } else {
         // o_tile_width never gives an FP16 format reading FP32 B an O tile of 128.
         throw Error(VCSRMC_ERR_STATE, "no O tile of 128 for FP32 B with an FP16 format");
