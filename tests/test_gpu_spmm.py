@@ -617,3 +617,19 @@ def test_failed_conversion_allocation_leaves_handle_usable(orc):
     R, L1 = orc.spmm_csr(rp, c, v, M, B, mode=1, scale=scale)
     ok, worst, row = row_l1_parity(Cn, R, L1, TAU[False])
     assert ok, f"row {row}: {worst:.3g}"
+
+
+@pytest.mark.parametrize("fp32", [False, True])
+@pytest.mark.parametrize("O", [1024, 1500, 2048])
+def test_wide_o(orc, fp32, O):
+    """Wide B and C: 8 or more O tiles, so every XCD group takes its own O tile and the rest
+    become launch rows (O = 2048: 16 tiles of 128), with O not a multiple of the tile width
+    (1500), C starting non-zero."""
+    rng = np.random.default_rng(O + fp32)
+    M, N = 700, 900
+    rp, c, v = random_csr(rng, M, N, density=0.01, heavy_rows=2, heavy_nnz=600,
+                          empty_frac=0.1)
+    B = rng.uniform(-1, 1, (N, O)).astype(np.float32)
+    C0 = rng.uniform(-1, 1, (M, O)).astype(np.float32)
+    say("wide O", fp32, O)
+    check(orc, rp, c, v, M, N, B, fp32, tileK=128, C0=C0)
