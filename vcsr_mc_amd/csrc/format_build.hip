@@ -13,6 +13,7 @@
 // Part 2 derives the execution layout read by the multiply kernels (16-row panels cut into
 // compacted 32-column tiles; see internal.hpp) from the same nonzeros.
 #include <algorithm>
+#include <atomic>
 #include <climits>
 #include <cmath>
 #include <cstring>
@@ -685,9 +686,10 @@ static void swap_layout(DeviceFormat& a, DeviceFormat& b) {
     std::swap(a.dense_a32, b.dense_a32);
 }
 
-static int g_row_grouping = 1;  // 0 off, 1 when it pays (default), 2 always
-void set_row_grouping(int mode) { g_row_grouping = mode; }
-int row_grouping() { return g_row_grouping; }
+// 0 off, 1 when it pays (the default), 2 always; read once by each build.
+static std::atomic<int> g_row_grouping{1};
+void set_row_grouping(int mode) { g_row_grouping.store(mode, std::memory_order_relaxed); }
+int row_grouping() { return g_row_grouping.load(std::memory_order_relaxed); }
 
 // The execution layout's row order.  Mode 0: natural.  Otherwise, first, rows without nonzeros
 // go after the others when they are at least an eighth of the rows (compact_rows; R-MAT scale
@@ -707,7 +709,7 @@ int row_grouping() { return g_row_grouping; }
 static void build_exec_layout(DeviceFormat& F, const int* trow, const int* tcol, const float* tval,
                               long long n, hipStream_t st) {
     F.row_map.release();
-    const int mode = g_row_grouping;
+    const int mode = row_grouping();
     DevBuf<int> cpos, cmap;
     const bool compact = mode != 0 && compact_rows(trow, n, F.M, st, cpos, cmap);
     build_layout_in_order(F, trow, tcol, tval, compact ? cpos.p : nullptr, n, st);

@@ -26,6 +26,7 @@
 //   5. order: vertices sorted by (component rank, level, index in level) give the
 //      Cuthill-McKee order; position = N - 1 - that index (reorder.hpp:72-76).
 #include <algorithm>
+#include <atomic>
 #include <climits>
 #include <cstdint>
 #include <string>
@@ -1048,13 +1049,14 @@ void sort_groups(const int* gstart, int ngroups, int n, u64* packed, SortJobs& J
 }
 
 // Iteration limits of the ordering's loops; 0 selects the proven maxima (see rcm_order_device).
-long long g_max_level = 0, g_max_rounds = 0;
+// Process-wide, read once by each ordering.
+std::atomic<long long> g_max_level{0}, g_max_rounds{0};
 
 }  // namespace
 
 void set_rcm_limits(long long max_level, long long max_rounds) {
-    g_max_level = max_level;
-    g_max_rounds = max_rounds;
+    g_max_level.store(max_level, std::memory_order_relaxed);
+    g_max_rounds.store(max_rounds, std::memory_order_relaxed);
 }
 
 void rcm_order_device(const int* rp, const int* col, int M, int N, int nnz, int* position,
@@ -1117,9 +1119,11 @@ void rcm_order_device(const int* rp, const int* col, int M, int N, int nnz, int*
     // pointer jumping alone halves every depth, so after ceil(lg N) + 1 rounds all trees are
     // stars and the next round either hooks or changes nothing: at most
     // N (ceil(lg N) + 2) + 1 rounds.
-    const long long max_level = g_max_level > 0 ? g_max_level : (long long)N + 1;
+    const long long lim_level = g_max_level.load(std::memory_order_relaxed);
+    const long long lim_rounds = g_max_rounds.load(std::memory_order_relaxed);
+    const long long max_level = lim_level > 0 ? lim_level : (long long)N + 1;
     const long long max_rounds =
-        g_max_rounds > 0 ? g_max_rounds : (long long)N * (bits_for((u64)N) + 2) + 1;
+        lim_rounds > 0 ? lim_rounds : (long long)N * (bits_for((u64)N) + 2) + 1;
 
     // 3. components
     DevBuf<int> comp(N);
