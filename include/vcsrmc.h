@@ -51,6 +51,8 @@ typedef struct vcsrmc_info {
     int device;            /* HIP device the format lives on            */
     int num_dense;         /* tiles stored as dense 16 x 32 copies      */
     int row_grouped;       /* 1: the layout's panels follow a row map      */
+    int num_heavy;         /* units shared by the four waves of a work-group */
+    int num_split_panels;  /* panels cut into several heavy units (merged through atomics) */
 } vcsrmc_info;
 
 /* Handle holding one device-resident format (the reference keeps one format in

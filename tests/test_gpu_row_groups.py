@@ -269,3 +269,42 @@ def test_noalloc_on_grouped_layout(grouping):
                                                 got.data_ptr(), 0, stream) == vm.OK
             torch.cuda.synchronize()
             assert torch.equal(got, want)
+
+
+@pytest.mark.parametrize("fp32", [True, False])
+def test_graph_replay_grouped(grouping, fp32):
+    """Both launch modes on a grouped layout with rows of 4000 nonzeros (panels of more than 64
+    tiles, cut into several units, which C = A.B clears with a kernel before they merge)
+    captured in a HIP graph: every replay, with eager work and synchronisation between replays,
+    matches the eager call."""
+    import torch
+    rng = np.random.default_rng(79 + fp32)
+    M, N, O = 900, 5000, 72
+    rp, c, v = random_csr(rng, M, N, density=0.002, heavy_rows=5, heavy_nnz=4000,
+                          empty_frac=0.1)
+    B = rng.uniform(-1, 1, (N, O)).astype(np.float32)
+    C0 = dev(rng.uniform(-1, 1, (M, O)).astype(np.float32))
+    grouping(vm.ROW_GROUPING_ALWAYS)
+    with vm.DeviceFormat.from_device_csr(dev(rp), dev(c), dev(v), M, N, fp32, 32) as f:
+        info = f.info()
+        assert info["row_grouped"] == 1 and info["num_split_panels"] > 0, info
+        dB = dev(B) if fp32 else dev(B).half()
+        for overwrite in (False, True):
+            say("graph replay grouped", fp32, overwrite)
+            ref = C0.clone()
+            f.spmm(dB, ref, tileK=64, overwrite=overwrite)
+            torch.cuda.synchronize()
+            C = C0.clone()
+            stream = torch.cuda.Stream()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=stream):
+                f.spmm(dB, C, tileK=64, overwrite=overwrite, stream=stream)
+            for it in range(4):
+                C.copy_(C0)
+                junk = torch.randn(1000, device="cuda").sum()  # eager work between replays
+                torch.cuda.synchronize()
+                g.replay()
+                torch.cuda.synchronize()
+                assert float(junk) == float(junk)
+                # split panels merge with atomics: only their order may differ
+                assert torch.allclose(C, ref, rtol=1e-5, atol=1e-5), (overwrite, it)

@@ -504,6 +504,7 @@ def test_overwrite_equals_zero_then_accumulate(orc, fp32, tileK, O):
     finally:
         vm.set_row_grouping(vm.ROW_GROUPING_AUTO)
     assert f.info()["row_grouped"] == 0
+    assert f.info()["num_split_panels"] == np.unique(np.nonzero(split)[0] // 16).size
     with f:
         dB = dev(B) if fp32 else dev(B).half()
         Ca = torch.zeros((M, O), dtype=torch.float32, device="cuda")

@@ -48,6 +48,7 @@ class _Info(C.Structure):
         ("num_items", C.c_int), ("scale", C.c_float), ("fp32", C.c_int), ("nnz", C.c_longlong),
         ("num_panels", C.c_int), ("num_chunks", C.c_int), ("num_units", C.c_int),
         ("device", C.c_int), ("num_dense", C.c_int), ("row_grouped", C.c_int),
+        ("num_heavy", C.c_int), ("num_split_panels", C.c_int),
     ]
 
 

@@ -200,6 +200,8 @@ int vcsrmc_get_info(vcsrmc_t h, vcsrmc_info* out) {
         out->num_units = F.num_units; out->device = h->device;
         out->num_dense = F.num_dense;
         out->row_grouped = F.row_map.n > 0;
+        out->num_heavy = F.num_heavy;
+        out->num_split_panels = F.num_split_panels;
     });
 }
 
