@@ -7,6 +7,13 @@
  * The C++ drop-in surface of the reference (include/vcsr_formats.hpp) is a thin layer over
  * these functions.
  *
+ * Threads: a handle holds all of its format's state, so different handles may be used from
+ * different host threads at the same time; one handle must not be used by two threads at once
+ * (its FP16 copy of an FP32 B is allocated on first use).  State shared by all handles is the
+ * row-grouping mode and the RCM limits (atomics, read once per call) and the per-device
+ * scratch of vcsrmc_spmm_noalloc (see there).  The C++ drop-in keeps the reference's single
+ * library-global format and is not re-entrant, like the reference (src/vcsr_mc.cu:126-131).
+ *
  * Each entry point names the reference interface it replaces (MuuSeoTia/VCSR_MC,
  * path:line relative to that repository).
  */
