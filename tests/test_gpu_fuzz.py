@@ -1,8 +1,9 @@
 """Seeded random inputs through the whole device path -- format build, execution layout in each
 row-order mode, SpMM in both launch modes -- against the oracle with the parity gate of
-test_gpu_spmm.py: uniform and Poisson rows with heavy rows and empty rows, bands and 2D 5-point
-grids; FP16 / FP32 formats, FP16 or FP32 B, segw 16-64, tileK 16-128, O from 1 to 256.  Rows A
-does not touch must keep C's values."""
+test_gpu_spmm.py: uniform and Poisson rows with heavy rows and empty rows, bands, 2D 5-point
+grids and dense blocks at random block columns (light units in column order); FP16 / FP32
+formats, FP16 or FP32 B, segw 16-64, tileK 16-128, O from 1 to 256.  Rows A does not touch must
+keep C's values."""
 import numpy as np
 import pytest
 
@@ -39,6 +40,21 @@ def _grid5(rng, g):
     return rp, c, rng.uniform(-1, 1, c.size).astype(np.float32)
 
 
+def _blocks(rng, M, N, b, per_row):
+    """Dense b x b blocks at `per_row` distinct random block columns of every block row."""
+    nbc = max(1, N // b)
+    rows = []
+    for br in range((M + b - 1) // b):
+        bc = np.sort(rng.choice(nbc, size=min(per_row, nbc), replace=False))
+        cols = (bc[:, None] * b + np.arange(b)[None, :]).ravel()
+        cols = cols[cols < N]
+        rows += [cols] * min(b, M - br * b)
+    rp = np.zeros(M + 1, np.int32)
+    rp[1:] = np.cumsum([len(x) for x in rows])
+    c = np.concatenate(rows).astype(np.int32)
+    return rp, c, rng.uniform(-1, 1, c.size).astype(np.float32)
+
+
 @pytest.mark.parametrize("seed", range(4))
 def test_fuzz_all_row_orders(orc, seed):
     import torch
@@ -48,7 +64,7 @@ def test_fuzz_all_row_orders(orc, seed):
             mode = int(rng.integers(0, 3))
             vm.set_row_grouping(mode)
             M, N = int(rng.integers(1, 5000)), int(rng.integers(1, 5000))
-            kind = int(rng.integers(0, 4))
+            kind = int(rng.integers(0, 5))
             if kind == 0:
                 rp, c, v = random_csr(rng, M, N, density=float(rng.choice([0.0005, 0.003, 0.02])),
                                       empty_frac=float(rng.uniform(0, 0.5)))
@@ -58,10 +74,13 @@ def test_fuzz_all_row_orders(orc, seed):
                                       heavy_nnz=int(rng.integers(1, N + 1)))
             elif kind == 2:
                 rp, c, v = _band(rng, M, N, int(rng.integers(0, 20)))
-            else:
+            elif kind == 3:
                 g = int(rng.integers(2, 60))
                 M = N = g * g
                 rp, c, v = _grid5(rng, g)
+            else:
+                rp, c, v = _blocks(rng, M, N, int(rng.choice([4, 8, 16, 32])),
+                                   int(rng.integers(1, 6)))
             fp32 = bool(rng.integers(0, 2))
             segw = int(rng.choice([16, 32, 48, 64]))
             tileK = int(rng.choice([16, 32, 64, 128]))
