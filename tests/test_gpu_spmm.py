@@ -373,6 +373,40 @@ def test_workloads_row_sample(orc, config):
     assert ok, f"row {rows[row]}: {worst:.3g}"
 
 
+@pytest.mark.parametrize("config", [2, 3, 4])
+def test_workload_upload_path(config):
+    """The reference's upload_vcsr_mc_device path at full size: the format arrays a build returns
+    (csr_to_vcsr_mc's output), uploaded back (vcsrmc_upload validates them on the device and
+    derives the execution layout from them), give the same layout and, with no split panels
+    (no atomics), the same C bit for bit as the format built from the CSR, in both launch modes
+    -- so the row-sample parity of the build path holds for the upload path too."""
+    import torch
+    w = vm.WORKLOADS[config]
+    fp32 = w["precision"] == "fp32"
+    A = vm.generate(config, 0)
+    O = w["O"]
+    B = vm.dense(A.N, O, seed=vm.SEED_BASE + 300 + config, fp16_exact=not fp32)
+    dB = dev(B) if fp32 else dev(B).half()
+    say("workload upload path", config, A.M, A.nnz, O)
+    with vm.DeviceFormat.from_device_csr(dev(A.row_ptr), dev(A.col), dev(A.val), A.M, A.N,
+                                         fp32, 32) as f:
+        V = f.download()
+        built = f.info()
+        assert built["num_split_panels"] == 0, built
+        want = []
+        for overwrite in (False, True):
+            C = torch.zeros((A.M, O), dtype=torch.float32, device="cuda") + 0.5
+            f.spmm(dB, C, tileK=128, overwrite=overwrite)
+            want.append(C)
+    with vm.DeviceFormat.from_host_format(V) as g:
+        assert g.info() == built
+        for overwrite, Cw in zip((False, True), want):
+            C = torch.zeros((A.M, O), dtype=torch.float32, device="cuda") + 0.5
+            g.spmm(dB, C, tileK=128, overwrite=overwrite)
+            torch.cuda.synchronize()
+            assert torch.equal(C, Cw), overwrite
+
+
 @pytest.mark.parametrize("config", [1, 2, 3, 4, 5])
 def test_workloads_second_precision_row_sample(orc, config):
     """The reference's driver runs both kernels on every matrix (src/main.cpp:345): each
