@@ -49,8 +49,9 @@ struct XcdSplit {
 //                     the panel has several units, whose partial sums meet in C through
 //                     atomics, kUnitSplitFirst = the first of them.  The first
 //                     num_heavy units are heavy (one work-group each, larger first), the rest
-//                     light (one wave each, four per work-group, in panel order; XCD x runs
-//                     the range starting at xcd_start[x], cut for equal tile counts).
+//                     light (one wave each, four per work-group, in panel order, or in the
+//                     order of the panels' first columns for blocks; XCD x runs the range
+//                     starting at xcd_start[x], cut for equal tile counts).
 //   chunk_eptr[c]   = first entry of chunk c (chunk_eptr[num_chunks] = nnz)
 //   chunk_cols[32c+k] = column of the chunk's k-th distinct column, -1 past the end (FP32
 //                   formats: slot (k & 3) * 8 + (k >> 2), the order the FP32 kernel's lanes read)

@@ -356,7 +356,8 @@ __device__ __forceinline__ uint4 load_a16(const TileMeta& m, int lane, int a_off
 // slice is fetched by at most P XCDs.  Heavy work-groups come first (8 per P heavy units): the
 // four waves share one unit's tiles.  The others run light units, one per wave; light
 // work-group j takes the next four units of its row part, a range of units in panel order
-// (neighbouring panels share B rows) cut for equal tile counts.  Sets `ot`, the O tile within
+// (neighbouring panels share B rows; panels of blocks: in the order of their first column)
+// cut for equal tile counts.  Sets `ot`, the O tile within
 // the launch row.  Returns false if this wave has nothing to do.
 __device__ __forceinline__ bool schedule(int num_heavy, const XcdSplit& xs, int wave, int& u,
                                          bool& heavy, int& ot) {
