@@ -182,6 +182,13 @@ int vcsrmc_set_rcm_limits(long long max_levels, long long max_rounds);
  * reference. */
 int vcsrmc_set_row_grouping(int mode);
 
+/* The row order of h's execution layout, for inspection: *length = the number of positions
+ * (a multiple of 16; 0 when the layout keeps natural order, row r at position r), and, when
+ * *length > 0 and row_of_position is not NULL, row_of_position[p] = the row at position p, or
+ * -1 for padding past the last row (host buffer of `capacity` ints, at least *length; NULL:
+ * only *length is set).  No counterpart in the reference. */
+int vcsrmc_get_row_map(vcsrmc_t h, int *row_of_position, long long capacity, long long *length);
+
 /* Relabels the columns of a device CSR in place, col[p] = position[col[p]], with every row
  * re-sorted by its new columns (values follow), and, when d_B is non-NULL, writes
  * d_B_out[position[r], :] = d_B[r, :] (N x O floats, d_B_out distinct from d_B), so that

@@ -121,7 +121,7 @@ def test_stencil_grouped_by_default(orc, grouping, fp32):
     """A 27-point stencil on a 32^3 grid (2048 panels, 72 nonzeros per tile in natural order):
     the default layout groups its rows, and the product matches the oracle in both launch modes.
     Natural order puts half an x line in a panel (up to 18 x 3 x 3 = 162 columns, 6 tiles;
-    4.875 per panel with the grid's faces); a 4 x 2 x 2 block touches at most 6 x 4 x 4 = 96
+    4.875 per panel with the grid's faces); a 2 x 2 x 4 block touches at most 4 x 4 x 6 = 96
     (3 tiles), so grouping that finds such blocks stays within 3 tiles per panel."""
     rng = np.random.default_rng(31 + fp32)
     g = 32
@@ -144,6 +144,68 @@ def test_stencil_grouped_by_default(orc, grouping, fp32):
         info = run(orc, rp, c, v, M, N, B, fp32, 128, O, C0, overwrite)
         assert info["row_grouped"] == 1
         assert info["num_chunks"] <= 3 * info["num_panels"], info
+
+
+def check_row_map(f, rp):
+    """The layout's row map places every row exactly once, -1 only as padding after the last
+    row, in whole 16-row panels, rows without nonzeros after all the others."""
+    M = rp.size - 1
+    rm = f.row_map()
+    assert rm is not None and rm.size % 16 == 0 and rm.size >= M
+    rows = rm[rm >= 0]
+    assert rows.size == M and np.array_equal(np.sort(rows), np.arange(M))
+    assert np.all(rm[M:] == -1)
+    empty = np.diff(rp)[rm[:M]] == 0
+    if empty.any():
+        assert not np.any(~empty[int(np.argmax(empty)):]), "a row with nonzeros after an empty one"
+    return rm
+
+
+def test_row_maps_are_permutations(grouping):
+    """Grouped and compacted layouts (random, heavy-row, banded and grid patterns with empty
+    rows, always-grouped and default modes) keep every row exactly once."""
+    seen = 0
+    for t in range(12):
+        rng = np.random.default_rng(9700 + t)
+        grouping(vm.ROW_GROUPING_ALWAYS if t % 2 else vm.ROW_GROUPING_AUTO)
+        M, N = int(rng.integers(17, 4000)), int(rng.integers(16, 4000))
+        kind = t % 3
+        if kind == 0:
+            rp, c, v = random_csr(rng, M, N, density=0.01, empty_frac=float(rng.uniform(0.2, 0.6)))
+        elif kind == 1:
+            rp, c, v = random_csr(rng, M, N, nnz_per_row=4, heavy_rows=2, heavy_nnz=min(N, 900),
+                                  empty_frac=0.3)
+        else:
+            g = int(rng.integers(5, 60))
+            rp, c = grid5(g)
+            M = N = g * g
+            v = rng.uniform(-1, 1, c.size).astype(np.float32)
+        say("row map permutation", t, M, N, c.size)
+        with vm.DeviceFormat.from_device_csr(dev(rp), dev(c), dev(v), M, N, bool(t % 2), 32) as f:
+            if f.info()["row_grouped"]:
+                check_row_map(f, rp)
+                seen += 1
+            else:
+                assert f.row_map() is None
+    assert seen >= 8
+
+
+def test_stencil_panels_are_blocks(grouping):
+    """On a 27-point stencil in natural order (x fastest) the matching's panels are 2 x 2 x 4
+    blocks: x and y extents 2, z extent 4 (equally good partners at the last level are taken
+    farthest in natural order, so a panel spans the slowest direction)."""
+    g = 16
+    rp, c = stencil27(g)
+    v = np.ones(c.size, np.float32)
+    grouping(vm.ROW_GROUPING_ALWAYS)
+    say("stencil panel shapes")
+    with vm.DeviceFormat.from_device_csr(dev(rp), dev(c), dev(v), g ** 3, g ** 3, True, 32) as f:
+        rm = check_row_map(f, rp)
+    panels = rm.reshape(-1, 16)
+    x, y, z = panels % g, (panels // g) % g, panels // (g * g)
+    ext = np.stack([a.max(1) - a.min(1) + 1 for a in (x, y, z)], axis=1)
+    blocks = np.all(ext == np.array([2, 2, 4]), axis=1)
+    assert blocks.mean() >= 0.95, np.unique(ext, axis=0, return_counts=True)
 
 
 def test_uniform_rows_keep_natural_order(grouping):

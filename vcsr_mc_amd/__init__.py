@@ -89,6 +89,7 @@ def lib():
         L.vcsrmc_rcm_order.argtypes = [vp, vp, C.c_int, C.c_int, C.c_int, vp, vp]
         L.vcsrmc_set_rcm_limits.argtypes = [C.c_longlong, C.c_longlong]
         L.vcsrmc_set_row_grouping.argtypes = [C.c_int]
+        L.vcsrmc_get_row_map.argtypes = [vp, vp, C.c_longlong, C.POINTER(C.c_longlong)]
         L.vcsrmc_apply_column_permutation.argtypes = [vp, vp, vp, C.c_int, C.c_int, C.c_int, vp,
                                                       vp, C.c_int, vp, vp]
         L.vcsrmc_status_string.restype = C.c_char_p
@@ -97,7 +98,7 @@ def lib():
         for f in ("vcsrmc_create", "vcsrmc_destroy", "vcsrmc_half_scale", "vcsrmc_build_csr",
                   "vcsrmc_upload", "vcsrmc_get_info", "vcsrmc_download", "vcsrmc_spmm",
                   "vcsrmc_spmm_ex", "vcsrmc_spmm_noalloc", "vcsrmc_rcm_order",
-                  "vcsrmc_set_rcm_limits", "vcsrmc_set_row_grouping",
+                  "vcsrmc_set_rcm_limits", "vcsrmc_set_row_grouping", "vcsrmc_get_row_map",
                   "vcsrmc_apply_column_permutation"):
             getattr(L, f).restype = C.c_int
         _lib_handle = L
@@ -284,6 +285,18 @@ class DeviceFormat:
         i = _Info()
         _check(lib().vcsrmc_get_info(self.handle, C.byref(i)), "vcsrmc_get_info")
         return {k: getattr(i, k) for k, _ in _Info._fields_}
+
+    def row_map(self):
+        """The execution layout's row order: an int32 array, row_map[p] = the row at position p
+        (-1 for padding), or None when the layout keeps natural order."""
+        n = C.c_longlong(0)
+        _check(lib().vcsrmc_get_row_map(self.handle, None, 0, C.byref(n)), "vcsrmc_get_row_map")
+        if n.value == 0:
+            return None
+        out = np.zeros(n.value, np.int32)
+        _check(lib().vcsrmc_get_row_map(self.handle, out.ctypes.data, out.size, C.byref(n)),
+               "vcsrmc_get_row_map")
+        return out
 
     def download(self) -> VCSRMC:
         i = self.info()

@@ -205,6 +205,20 @@ int vcsrmc_get_info(vcsrmc_t h, vcsrmc_info* out) {
     });
 }
 
+int vcsrmc_get_row_map(vcsrmc_t h, int* row_of_position, long long capacity, long long* length) {
+    return guarded([&] {
+        need(h != nullptr && length != nullptr, "null argument");
+        if (!h->F.ready) throw vcsrmc::Error(VCSRMC_ERR_STATE, "no format in this handle");
+        const auto& F = h->F;
+        *length = (long long)F.row_map.n;
+        if (F.row_map.n == 0 || row_of_position == nullptr) return;
+        need(capacity >= (long long)F.row_map.n, "row map buffer smaller than its length");
+        DeviceScope ds(h->device);
+        VCSRMC_HIP(hipMemcpy(row_of_position, F.row_map.p, sizeof(int) * F.row_map.n,
+                             hipMemcpyDeviceToHost));
+    });
+}
+
 int vcsrmc_download(vcsrmc_t h, int* group_ptr, int* group_depth, int* group_seg_base,
                     int* group_rows, int* lcol, float* val, int* item_gbeg, int* item_gend) {
     return guarded([&] {

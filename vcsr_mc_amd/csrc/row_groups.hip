@@ -13,10 +13,18 @@
 // rows without telling them apart), keeps its best few, and clusters whose first choices are
 // each other merge; a few rounds let clusters whose partner was taken try their next choice.
 // The score is the number of shared columns; ties go to the pair whose first rows r < s satisfy
-// floor(r / (s - r)) even, then to the nearer pair, then to a hash of the pair.  The parity rule
-// makes chains of equally good partners pair up in phase (rows 0-1, 2-3, ... rather than a
-// pairing that shifts from one chain to the next), which is what lets the next level merge the
-// pairs into compact blocks; the distance rule keeps pairs near in the original order.
+// floor(r / (s - r)) even, then to the nearer pair (the farther at the last level), then to a
+// hash of the pair.  The parity rule makes chains of equally good partners pair up in phase
+// (rows 0-1, 2-3, ... rather than a pairing that shifts from one chain to the next), which is
+// what lets the next level merge the pairs into compact blocks; the distance rule keeps pairs
+// near in the original order, except at the last level, where the farther of equally good
+// partners makes a panel span more of the slowest direction of the natural order (z of a 3D
+// grid: 2 x 2 x 4 blocks of a 27-point stencil, not 4 x 2 x 2; the same 96 columns): the B
+// rows of a z-plane, reused by the panels one plane away long after one XCD's L2 has dropped
+// them, are then fetched by 1.5 slabs of panels instead of 2.  Measured on gfx950 (kernel us,
+// C += A.B / C = A.B): 27-point 100^3 FP32 444 / 347 -> 424 / 343, FP16 306 / 233 -> 308 /
+// 225; 7-point 100^3 FP32 367 / 254 -> 354 / 253, FP16 268 / 194 -> 272 / 185; 7-point 60^3
+// FP32 65.7 / 53.6 -> 60.7 / 48.1, FP16 48.3 / 29.8 -> 45.9 / 31.5; 2D 5-point grids unchanged.
 // Finally the rows are ordered by their group's first row (rows in a group by index); rows
 // without nonzeros go last, so they fill no panel.
 //
@@ -107,7 +115,7 @@ __global__ __launch_bounds__(256) void k_score(const u64* __restrict__ crk,
                                                const int* __restrict__ rc_ptr, int cbits,
                                                int clbits, const int* __restrict__ size,
                                                const int* __restrict__ cmin, int nc, int maxsz,
-                                               int* __restrict__ cand) {
+                                               bool far, int* __restrict__ cand) {
     __shared__ int tkey[4][kTable];
     __shared__ int tcnt[4][kTable];
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -163,7 +171,7 @@ __global__ __launch_bounds__(256) void k_score(const u64* __restrict__ crk,
             const int lo = min(ma, mb), d = max(ma, mb) - lo;  // d >= 1: distinct first rows
             const u64 cnt = (u64)min(Cn[slot], 8191);
             const u64 phase = ((lo / d) & 1) == 0;
-            const u64 near = (u64)(0x7fffffff - d);
+            const u64 near = far ? (u64)d : (u64)(0x7fffffff - d);
             const u64 tie = mix32((unsigned)min((int)a, b) * 0x9e3779b9u ^ (unsigned)max((int)a, b)) &
                             0x3ffffu;
             key = (cnt << 50) | (phase << 49) | (near << 18) | tie;
@@ -428,7 +436,8 @@ bool group_rows(const int* trow, const int* tcol, long long n, int M, int N, hip
         const int maxsz = 2 << level;  // clusters of 2^level rows pair into 2^(level+1)
         DevBuf<int> cand((size_t)nc * kCand), mate(nc), prop(nc);
         hipLaunchKernelGGL(k_score, dim3(grid_for(nc, 4)), dim3(256), 0, st, keys.p, cr_ptr.p,
-                           rck.p, rc_ptr.p, cbits, clbits, size.p, cmin.p, nc, maxsz, cand.p);
+                           rck.p, rc_ptr.p, cbits, clbits, size.p, cmin.p, nc, maxsz,
+                           level == kLevels - 1, cand.p);
         VCSRMC_HIP(hipGetLastError());
         fill<int>(mate.p, nc, -1, st);
         for (int round = 0; round < kRounds; ++round) {
