@@ -48,6 +48,9 @@ def test_bench_json_line():
     assert d["parity_row_sample"] is True
     (p,) = d["per_config"]
     assert p["config"] == 1 and p["O"] == 128 and p["precision"] == "fp32"
+    lay = p["layout"]
+    assert 0 < lay["num_panels"] <= lay["num_units"] <= lay["num_chunks"]
+    assert lay["num_heavy"] <= lay["num_units"] and lay["row_grouped"] in (0, 1)
     for mode in ("accumulate", "overwrite"):
         m = p[mode]
         assert m["parity_row_sample"] is True
