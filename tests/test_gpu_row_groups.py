@@ -3,6 +3,8 @@ rows) against the oracle, with the parity gate of test_gpu_spmm.py: random shape
 patterns in both precisions, every O tile width, C += A.B and C = A.B, split panels; the
 automatic choice on a 27-point stencil grid (grouped: far fewer tiles) and on uniform random
 rows (kept in natural order); the format arrays are the same either way."""
+import ctypes
+
 import numpy as np
 import pytest
 
@@ -185,6 +187,11 @@ def test_row_maps_are_permutations(grouping):
             if f.info()["row_grouped"]:
                 check_row_map(f, rp)
                 seen += 1
+                n = ctypes.c_longlong(0)
+                small = np.zeros(15, np.int32)
+                assert vm.lib().vcsrmc_get_row_map(f.handle, small.ctypes.data, small.size,
+                                                   ctypes.byref(n)) == vm.ERR_ARG
+                assert n.value % 16 == 0 and n.value >= M and not small.any()
             else:
                 assert f.row_map() is None
     assert seen >= 8
