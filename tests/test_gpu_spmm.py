@@ -257,12 +257,12 @@ def test_small_fp32_formats_all_dense():
 @pytest.mark.parametrize("keep", [1.0, 0.4])
 @pytest.mark.parametrize("O", [100, 128])
 def test_fp32_full_tiles_many_panels(orc, keep, O):
-    """FP32 formats take O tiles of 128 only with at least 2048 panels and tiles of 48 or more
-    nonzeros on average: a band of 49 diagonals over 2100 panels (keep = 1: dense tile copies;
+    """FP32 formats take O tiles of 128 only with at least 8192 panels and tiles of 48 or more
+    nonzeros on average: a band of 49 diagonals over 8300 panels (keep = 1: dense tile copies;
     keep = 0.4: entry lists), O = 100 (B and C past the vector width) and 128, C starting
     non-zero, the whole product against the oracle."""
     rng = np.random.default_rng(int(O + 10 * keep))
-    M = N = 2100 * 16
+    M = N = 8300 * 16
     rp, c, v = band_csr(rng, M, N, 24, 1.0)
     if keep < 1.0:
         row = np.repeat(np.arange(M), np.diff(rp))
@@ -274,7 +274,7 @@ def test_fp32_full_tiles_many_panels(orc, keep, O):
     C0 = rng.uniform(-1, 1, (M, O)).astype(np.float32)
     say("fp32 full tiles, many panels", keep, O, c.size)
     C, info = run_spmm(rp, c, v, M, N, B, True, C0=C0)
-    assert info["num_panels"] >= 2048 and info["nnz"] >= 48 * info["num_chunks"]
+    assert info["num_panels"] >= 8192 and info["nnz"] >= 48 * info["num_chunks"]
     R, L1 = orc.spmm_csr(rp, c, v, M, B, mode=0, scale=info["scale"])
     R = R + C0.astype(np.float64)
     L1 = L1 + np.abs(C0.astype(np.float64)).sum(axis=1)

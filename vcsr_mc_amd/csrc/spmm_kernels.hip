@@ -871,9 +871,13 @@ __global__ void k_b_to_half(const float* __restrict__ B, _Float16* __restrict__ 
 //     7.0 us, power-law 36,692^2 33.0 -> 30.2, R-MAT scale 22 5.91 -> 5.70 ms) or B is larger
 //     than the 32 MB of L2 on the 8 XCDs (two O halves on separate XCD groups each fetch half of
 //     every B row, over a union of fewer row ranges: FP16 R-MAT 3.05 -> 2.86 ms);
-//   * 64 for FP32 formats with fewer than kFewPanels panels, where the launch at 128 holds too
-//     few waves and each one a long FP32 chain (27-point stencil 18^3 8.22 -> 7.09 us, 30^3
-//     26.6 -> 24.5; 32 x 32 blocks, 96 block rows 6.59 -> 5.97, 512 block rows 26.6 -> 24.7).
+//   * 64 for FP32 formats with fewer than kFewPanels32 panels, where the launch at 128 holds
+//     under three rounds of the ~3072 waves the GPU keeps resident, each wave a long FP32
+//     chain (27-point stencil 18^3 8.22 -> 7.09 us, 30^3 26.6 -> 24.5, 40^3 30.3 -> 29.7;
+//     32 x 32 blocks, 96 block rows 6.59 -> 5.97, 512 block rows 26.6 -> 24.7, 1024 block rows
+//     24.0 -> 22.8; 4 x 4 blocks, 20,000 block rows 46.3 -> 43.7; a band of 33 per row,
+//     50,000 rows 23.8 -> 22.6; an arrow matrix, 100,000 rows 45.6 -> 39.5 us; 2D 9-point
+//     300^2 32.7 -> 31.8; 5-point 500^2 (15,625 panels) and 7-point 60^3 (13,500) within 1%);
 //   * 64 for FP16 formats reading FP32 B rows: at 128 that kernel needs 222 VGPRs (two waves
 //     per SIMD; three would spill), at 64 139 (three waves), which outweighs repeating the A
 //     side (uniform 4096^2 7.9 -> 7.4 us, uniform 20,000^2 with 8 per row 17.9 -> 16.2,
@@ -881,13 +885,15 @@ __global__ void k_b_to_half(const float* __restrict__ B, _Float16* __restrict__ 
 //   Otherwise fuller tiles keep 128, since every O tile repeats the A side of each tile
 //   (27-point stencil 100^3 and 32 x 32 blocks at 8192 block rows: 2-14% slower at 64), as do
 //   FP16 formats with a cache-resident FP16 B (power-law: 15.4 -> 17.4 us at 64).
+constexpr int kFewPanels32 = 8192;
+
 static int o_tile_width(const DeviceFormat& F, bool b_f16, int O, int tileK) {
     int tk = tileK;
     while (tk > 16 && tk / 2 >= O) tk /= 2;
     if (tk == 128 && F.num_chunks > 0) {
         const bool sparse_tiles = F.nnz < 48LL * F.num_chunks;
         const long long b_bytes = (long long)F.N * O * (b_f16 ? 2 : 4);
-        if (F.fp32 && (sparse_tiles || F.num_panels < kFewPanels)) tk = 64;
+        if (F.fp32 && (sparse_tiles || F.num_panels < kFewPanels32)) tk = 64;
         else if (!F.fp32 && !b_f16) tk = 64;
         else if (sparse_tiles && b_bytes > (32LL << 20)) tk = 64;
     }
