@@ -110,6 +110,8 @@ int vcsrmc_download(vcsrmc_t h, int *group_ptr, int *group_depth, int *group_seg
  *   - 64 instead of 128 for formats whose tiles hold few nonzeros (fewer than 48 on average)
  *     that are FP32 or whose B exceeds the GPU's 32 MB of L2;
  *   - 64 for FP32 formats of fewer than 8192 16-row panels;
+ *   - 64 for FP16 B above 4 MB with sparse tiles and no panel of more than three times the
+ *     average tile count (uniform random matrices);
  *   - 64 for an FP16 format reading FP32 B directly (at 128 that kernel holds too many
  *     registers for three waves per SIMD).
  * Rows of C that A does not touch are left as they are.  If ms is non-NULL the launch is

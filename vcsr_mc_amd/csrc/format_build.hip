@@ -583,6 +583,11 @@ static void build_exec_layout_k(DeviceFormat& F, const int* trow, const int* tco
     LAUNCH(k_panel_chunks, NP, pstart.p, dc.p, NP, nch.p);
     exclusive_sum<int, int>(nch.p, cbase.p, NP, st);
     const int NC = read_scalar(cbase.p + NP, st);
+    {
+        DevBuf<int> nmax(NP);
+        inclusive_max(nch.p, nmax.p, NP, st);
+        F.max_panel_tiles = read_scalar(nmax.p + (NP - 1), st);
+    }
 
     F.chunk_eptr.alloc(NC + 1);
     F.chunk_cols.alloc((size_t)NC * kChunkCols);
@@ -672,7 +677,7 @@ static void build_exec_layout_k(DeviceFormat& F, const int* trow, const int* tco
 static void build_layout_in_order(DeviceFormat& F, const int* trow, const int* tcol,
                                   const float* tval, const int* rowpos, long long n,
                                   hipStream_t st) {
-    F.num_panels = F.num_chunks = F.num_units = F.num_dense = 0;
+    F.num_panels = F.num_chunks = F.num_units = F.num_dense = F.max_panel_tiles = 0;
     F.num_pairs = 0;
     if (n == 0) return;
     const int num_panels_all = (F.M + kPanelRows - 1) / kPanelRows;
@@ -693,6 +698,7 @@ static void swap_layout(DeviceFormat& a, DeviceFormat& b) {
     std::swap(a.light_max, b.light_max);
     std::swap(a.heavy_tiles, b.heavy_tiles);
     std::swap(a.num_split_panels, b.num_split_panels);
+    std::swap(a.max_panel_tiles, b.max_panel_tiles);
     std::swap(a.num_pairs, b.num_pairs);
     std::swap(a.xcd_start, b.xcd_start);
     std::swap(a.units, b.units);

@@ -82,6 +82,7 @@ struct DeviceFormat {
     int heavy_tiles = 0;       // largest heavy unit, in tiles
     long long num_pairs = 0;   // distinct (panel, column) pairs: the tiles' filled columns
     int num_split_panels = 0;  // panels cut into several units
+    int max_panel_tiles = 0;   // tiles of the largest panel
     // Light units [num_heavy + xcd_start[x], num_heavy + xcd_start[x + 1]) run on XCD x.
     int xcd_start[9] = {0, 0, 0, 0, 0, 0, 0, 0, 0};
     DevBuf<int4> units;

@@ -878,6 +878,13 @@ __global__ void k_b_to_half(const float* __restrict__ B, _Float16* __restrict__ 
 //     24.0 -> 22.8; 4 x 4 blocks, 20,000 block rows 46.3 -> 43.7; a band of 33 per row,
 //     50,000 rows 23.8 -> 22.6; an arrow matrix, 100,000 rows 45.6 -> 39.5 us; 2D 9-point
 //     300^2 32.7 -> 31.8; 5-point 500^2 (15,625 panels) and 7-point 60^3 (13,500) within 1%);
+//   * 64 for FP16 B above 4 MB with sparse tiles whose panels are alike (no panel more than three
+//     times the average tile count, as in uniform random matrices; power-law and R-MAT
+//     matrices have panels of hub rows 10x the average and keep 128): their B rows are used a
+//     similar number of times from all over the matrix, so each XCD's L2 holds a larger share
+//     of the half rows of its O half than of full rows (uniform random, 50,000^2 with 32 per row
+//     53.7 -> 47.2 us, 20,000 x 100,000 22.0 -> 20.7, 100,000^2 with 16 per row 70.3 -> 68.3;
+//     power-law, R-MAT, grids, bands and blocks unchanged);
 //   * 64 for FP16 formats reading FP32 B rows: at 128 that kernel needs 222 VGPRs (two waves
 //     per SIMD; three would spill), at 64 139 (three waves), which outweighs repeating the A
 //     side (uniform 4096^2 7.9 -> 7.4 us, uniform 20,000^2 with 8 per row 17.9 -> 16.2,
@@ -896,6 +903,9 @@ static int o_tile_width(const DeviceFormat& F, bool b_f16, int O, int tileK) {
         if (F.fp32 && (sparse_tiles || F.num_panels < kFewPanels32)) tk = 64;
         else if (!F.fp32 && !b_f16) tk = 64;
         else if (sparse_tiles && b_bytes > (32LL << 20)) tk = 64;
+        else if (sparse_tiles && b_bytes > (4LL << 20) &&
+                 (long long)F.max_panel_tiles * F.num_panels <= 3LL * F.num_chunks)
+            tk = 64;
     }
     return tk;
 }
