@@ -1030,7 +1030,11 @@ void sort_groups(const int* gstart, int ngroups, int n, u64* packed, SortJobs& J
     VCSRMC_HIP(hipStreamSynchronize(st));
     int nbig = counts[0], nsmall = counts[2];
     const bool passes = nbig > 0;
+    // Every pass lowers the depth of the ranges it keeps, which starts at 2 floor(lg n) < 63:
+    // more passes than that means a broken partition step, reported instead of looping.
+    int pass = 0;
     while (nbig > 0) {
+        if (++pass > 64) throw Error(VCSRMC_ERR_STATE, "RCM child sort did not converge");
         VCSRMC_HIP(hipMemsetAsync(cnxt, 0, sizeof(int), st));
         hipLaunchKernelGGL(k_partition_pass, dim3(nbig), dim3(256), 0, st, cur, nxt, cnxt,
                            J.small.p, J.counts.p + 2, packed, J.lpos.p, J.rpos.p);
