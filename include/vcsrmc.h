@@ -60,6 +60,7 @@ typedef struct vcsrmc_info {
     int row_grouped;       /* 1: the layout's panels follow a row map      */
     int num_heavy;         /* units shared by the four waves of a work-group */
     int num_split_panels;  /* panels cut into several heavy units (merged through atomics) */
+    int num_row_step_batches; /* FP32: batches of 8 row steps (vcsrmc_set_fp32_row_steps) */
 } vcsrmc_info;
 
 /* Handle holding one device-resident format (the reference keeps one format in
@@ -183,6 +184,18 @@ int vcsrmc_set_rcm_limits(long long max_levels, long long max_rounds);
  * vcsrmc_info.row_grouped is 1 when a handle's layout has any row map.  No counterpart in the
  * reference. */
 int vcsrmc_set_row_grouping(int mode);
+
+/* Product of FP32 panels that later builds and uploads lay out (process-wide).  A tile step,
+ * v_mfma_f32_16x16x4_f32, multiplies all 16 rows of a panel at 4 columns, however few of those
+ * rows hold them; a row step, v_mfma_f32_4x4x1_16b_f32 with its blocks as 4 row groups x 4
+ * groups of output columns, lets each group of 4 rows take its own next column, at a quarter of
+ * the cycles, so a panel whose rows rarely share a column needs about as many row steps as tile
+ * steps.  0: tile steps only; 1 (the default): row steps for every FP32 panel that needs at
+ * most 3/2 as many batches of 8 row steps as it has tiles; 2: row steps for every FP32 panel.
+ * The product is the same up to rounding (each row's sum is formed in another order).
+ * vcsrmc_info.num_row_step_batches counts a format's batches.  No counterpart in the
+ * reference. */
+int vcsrmc_set_fp32_row_steps(int mode);
 
 /* The row order of h's execution layout, for inspection: *length = the number of positions
  * (a multiple of 16; 0 when the layout keeps natural order, row r at position r), and, when

@@ -80,6 +80,19 @@ def test_upload_refuses_short_arrays_without_gpu(field, delta):
     assert e.value.status == vm.ERR_FORMAT and field in str(e.value)
 
 
+def test_fp32_row_steps_mode_checked_without_gpu():
+    """vcsrmc_set_fp32_row_steps accepts 0, 1 and 2 and refuses anything else before any device
+    work; the default (1) is restored."""
+    import vcsr_mc_amd as vm
+    for mode in (vm.FP32_ROW_STEPS_OFF, vm.FP32_ROW_STEPS_ALWAYS, vm.FP32_ROW_STEPS_AUTO):
+        vm.set_fp32_row_steps(mode)
+    for bad in (-1, 3):
+        with pytest.raises(vm.VCSRMCError) as e:
+            vm.set_fp32_row_steps(bad)
+        assert e.value.status == vm.ERR_ARG
+    vm.set_fp32_row_steps(vm.FP32_ROW_STEPS_AUTO)
+
+
 def test_row_grouping_mode_checked_without_gpu():
     """vcsrmc_set_row_grouping accepts 0, 1 and 2 and refuses anything else before any device
     work; the default (1) is restored."""

@@ -1,5 +1,5 @@
 """Seeded random inputs through the whole device path -- format build, execution layout in each
-row-order mode, SpMM in both launch modes -- against the oracle with the parity gate of
+row-order mode and FP32 row-step mode, SpMM in both launch modes -- against the oracle with the parity gate of
 test_gpu_spmm.py: uniform and Poisson rows with heavy rows and empty rows, bands, 2D 5-point
 grids and dense blocks at random block columns (light units in column order); FP16 / FP32
 formats, FP16 or FP32 B, segw 16-64, tileK 16-128, O from 1 to 256.  Rows A does not touch must
@@ -59,10 +59,13 @@ def _blocks(rng, M, N, b, per_row):
 def test_fuzz_all_row_orders(orc, seed):
     import torch
     rng = np.random.default_rng(30000 + seed)
+    rng_steps = np.random.default_rng(40000 + seed)  # its own stream: the cases stay as they were
     try:
         for t in range(50):
             mode = int(rng.integers(0, 3))
             vm.set_row_grouping(mode)
+            steps = int(rng_steps.integers(0, 3))
+            vm.set_fp32_row_steps(steps)
             M, N = int(rng.integers(1, 5000)), int(rng.integers(1, 5000))
             kind = int(rng.integers(0, 5))
             if kind == 0:
@@ -91,7 +94,8 @@ def test_fuzz_all_row_orders(orc, seed):
             if not fp32:
                 B = B.astype(np.float16).astype(np.float32)
             C0 = rng.uniform(-1, 1, (M, O)).astype(np.float32)
-            say("fuzz", seed, t, mode, kind, M, N, c.size, fp32, segw, tileK, O, overwrite, b16)
+            say("fuzz", seed, t, mode, steps, kind, M, N, c.size, fp32, segw, tileK, O,
+                overwrite, b16)
             with vm.DeviceFormat.from_device_csr(dev(rp), dev(c), dev(v), M, N, fp32, segw) as f:
                 scale = f.info()["scale"]
                 dB = dev(B).half() if b16 else dev(B)
@@ -110,3 +114,4 @@ def test_fuzz_all_row_orders(orc, seed):
             assert np.array_equal(Cg[~touched], C0[~touched]), f"case {t}: untouched rows"
     finally:
         vm.set_row_grouping(vm.ROW_GROUPING_AUTO)
+        vm.set_fp32_row_steps(vm.FP32_ROW_STEPS_AUTO)

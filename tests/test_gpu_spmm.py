@@ -142,12 +142,13 @@ def test_upload_path_matches_build_path(orc, fp32):
     check(orc, rp, c, v, 500, 500, B, fp32, upload=V)
 
 
-@pytest.mark.parametrize("fp32", [False, True])
-def test_nonfinite_b_reach(fp32):
-    """An Inf in B reaches exactly the 16-row panels that use its column: row 0 uses column 3
-    (Inf row), row 1 of the same panel does not (0 * Inf = NaN there), row 17 in the next panel
-    never touches column 3 and stays finite; column 9's Inf row is used by no nonzero and
-    reaches nothing."""
+@pytest.mark.parametrize("fp32,row_steps,reach", [(False, 1, 16), (True, 0, 16), (True, 1, 4)])
+def test_nonfinite_b_reach(fp32, row_steps, reach):
+    """An Inf in B reaches exactly the rows multiplied together with its column: row 0 uses
+    column 3 (Inf row); the other rows of its 16-row panel (tile steps) or of its 4-row group
+    (FP32 row steps, the default for this matrix) do not (0 * Inf = NaN there); the rest of the
+    panel, and row 17 in the next panel, never meet column 3 and stay finite; column 9's Inf
+    row is used by no nonzero and reaches nothing."""
     import torch
     M, N, O = 40, 12, 32
     rows = {r: [5] for r in range(M)}
@@ -160,17 +161,22 @@ def test_nonfinite_b_reach(fp32):
     B = np.ones((N, O), np.float32)
     B[3, :] = np.inf
     B[9, :] = np.inf
-    say("non-finite B", fp32)
-    with vm.DeviceFormat.from_device_csr(dev(rp), dev(c), dev(v), M, N, fp32, 32) as f:
-        Cd = torch.zeros((M, O), dtype=torch.float32, device="cuda")
-        f.spmm(dev(B) if fp32 else dev(B).half(), Cd, tileK=32)
-        torch.cuda.synchronize()
-        C = Cd.cpu().numpy()
+    say("non-finite B", fp32, row_steps)
+    vm.set_fp32_row_steps(row_steps)
+    try:
+        with vm.DeviceFormat.from_device_csr(dev(rp), dev(c), dev(v), M, N, fp32, 32) as f:
+            assert (f.info()["num_row_step_batches"] > 0) == (fp32 and row_steps == 1)
+            Cd = torch.zeros((M, O), dtype=torch.float32, device="cuda")
+            f.spmm(dev(B) if fp32 else dev(B).half(), Cd, tileK=32)
+            torch.cuda.synchronize()
+            C = Cd.cpu().numpy()
+    finally:
+        vm.set_fp32_row_steps(vm.FP32_ROW_STEPS_AUTO)
     assert np.all(np.isposinf(C[0]))
-    assert np.all(np.isnan(C[1:16]))
-    expect = np.full((M - 16, O), 0.5, np.float32)
-    expect[17 - 16] = 1.0  # row 17: columns 4 and 5
-    assert np.array_equal(C[16:], expect)
+    assert np.all(np.isnan(C[1:reach]))
+    expect = np.full((M - reach, O), 0.5, np.float32)
+    expect[17 - reach] = 1.0  # row 17: columns 4 and 5
+    assert np.array_equal(C[reach:], expect)
 
 
 def test_empty_matrix():

@@ -49,6 +49,7 @@ class _Info(C.Structure):
         ("num_panels", C.c_int), ("num_chunks", C.c_int), ("num_units", C.c_int),
         ("device", C.c_int), ("num_dense", C.c_int), ("row_grouped", C.c_int),
         ("num_heavy", C.c_int), ("num_split_panels", C.c_int),
+        ("num_row_step_batches", C.c_int),
     ]
 
 
@@ -89,6 +90,7 @@ def lib():
         L.vcsrmc_rcm_order.argtypes = [vp, vp, C.c_int, C.c_int, C.c_int, vp, vp]
         L.vcsrmc_set_rcm_limits.argtypes = [C.c_longlong, C.c_longlong]
         L.vcsrmc_set_row_grouping.argtypes = [C.c_int]
+        L.vcsrmc_set_fp32_row_steps.argtypes = [C.c_int]
         L.vcsrmc_get_row_map.argtypes = [vp, vp, C.c_longlong, C.POINTER(C.c_longlong)]
         L.vcsrmc_apply_column_permutation.argtypes = [vp, vp, vp, C.c_int, C.c_int, C.c_int, vp,
                                                       vp, C.c_int, vp, vp]
@@ -99,7 +101,7 @@ def lib():
                   "vcsrmc_upload", "vcsrmc_get_info", "vcsrmc_download", "vcsrmc_spmm",
                   "vcsrmc_spmm_ex", "vcsrmc_spmm_noalloc", "vcsrmc_rcm_order",
                   "vcsrmc_set_rcm_limits", "vcsrmc_set_row_grouping", "vcsrmc_get_row_map",
-                  "vcsrmc_apply_column_permutation"):
+                  "vcsrmc_apply_column_permutation", "vcsrmc_set_fp32_row_steps"):
             getattr(L, f).restype = C.c_int
         _lib_handle = L
     return _lib_handle
@@ -399,6 +401,17 @@ def set_row_grouping(mode: int) -> None:
     saves tiles) or ROW_GROUPING_ALWAYS.  DeviceFormat.info()["row_grouped"] tells which a
     format holds."""
     _check(lib().vcsrmc_set_row_grouping(int(mode)), "set_row_grouping")
+
+
+FP32_ROW_STEPS_OFF, FP32_ROW_STEPS_AUTO, FP32_ROW_STEPS_ALWAYS = 0, 1, 2
+
+
+def set_fp32_row_steps(mode: int) -> None:
+    """Product of FP32 panels for later builds (process-wide): FP32_ROW_STEPS_OFF (tiles of
+    16 x 16 x 4 matrix-core steps only), FP32_ROW_STEPS_AUTO (the default: panels whose rows
+    rarely share a column run row steps of v_mfma_f32_4x4x1_16b_f32) or FP32_ROW_STEPS_ALWAYS.
+    DeviceFormat.info()["num_row_step_batches"] tells how many batches a format holds."""
+    _check(lib().vcsrmc_set_fp32_row_steps(int(mode)), "set_fp32_row_steps")
 
 
 # ---- column reordering (include/reorder.hpp:17-108), computed on the GPU -------------------

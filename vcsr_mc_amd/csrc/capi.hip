@@ -143,6 +143,13 @@ int vcsrmc_set_row_grouping(int mode) {
     });
 }
 
+int vcsrmc_set_fp32_row_steps(int mode) {
+    return guarded([&] {
+        need(mode >= 0 && mode <= 2, "FP32 row-step mode must be 0, 1 or 2");
+        vcsrmc::set_fp32_row_steps(mode);
+    });
+}
+
 int vcsrmc_apply_column_permutation(const int* d_row_ptr, int* d_col, float* d_val, int M, int N,
                                     int nnz, const int* d_position, const float* d_B, int O,
                                     float* d_B_out, void* stream) {
@@ -202,6 +209,7 @@ int vcsrmc_get_info(vcsrmc_t h, vcsrmc_info* out) {
         out->row_grouped = F.row_map.n > 0;
         out->num_heavy = F.num_heavy;
         out->num_split_panels = F.num_split_panels;
+        out->num_row_step_batches = F.num_row_step_batches;
     });
 }
 

@@ -418,6 +418,73 @@ __global__ void k_dense_fill(const uint32_t* __restrict__ entries,
     }
 }
 
+// Row steps of FP32 panels (the layout is described with DeviceFormat).  rsmask[4c + g] = the
+// columns k of tile c that row group g (rows 4g .. 4g + 3) holds, as a 32-bit set; one thread per
+// tile.
+__global__ void k_row_step_masks(const int* __restrict__ eptr, const uint32_t* __restrict__ entries,
+                                 int NC, uint32_t* __restrict__ rsmask) {
+    const long long c = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= NC) return;
+    uint32_t m[4] = {0u, 0u, 0u, 0u};
+    for (int e = eptr[c]; e < eptr[c + 1]; ++e) {
+        const uint32_t w = entries[2 * (long long)e];
+        m[(w & 15) >> 2] |= 1u << ((w >> 4) & 31);
+    }
+    for (int g = 0; g < 4; ++g) rsmask[4 * c + g] = m[g];
+}
+
+// Per panel j (tiles cbase[j] .. cbase[j + 1]): rspre[4c + g] = row group g's columns in the
+// panel's tiles before c, and nbat[j] = the panel's batches of 8 row steps (its busiest row
+// group's columns / 8, rounded up) where it takes row steps, else 0: always (`all`), or when
+// they are at most num / den per tile.  One thread per panel.
+__global__ void k_row_step_counts(const int* __restrict__ cbase, const uint32_t* __restrict__ rsmask,
+                                  int NP, bool all, int num, int den, int* __restrict__ rspre,
+                                  int* __restrict__ nbat) {
+    const long long j = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= NP) return;
+    const int c0 = cbase[j], c1 = cbase[j + 1];
+    int cnt[4] = {0, 0, 0, 0};
+    for (int c = c0; c < c1; ++c)
+        for (int g = 0; g < 4; ++g) {
+            rspre[4LL * c + g] = cnt[g];
+            cnt[g] += __popc(rsmask[4LL * c + g]);
+        }
+    const int steps = max(max(cnt[0], cnt[1]), max(cnt[2], cnt[3]));
+    const int nb = (steps + 7) / 8;
+    nbat[j] = (all || (long long)nb * den <= (long long)num * (c1 - c0)) ? nb : 0;
+}
+
+// Writes the row steps of the panels that take them: entry (row 4g + x, tile column k of tile
+// c) becomes step s = (row group g's columns before it in the panel) of batch rbase[j] + s / 8.
+// The slots were set to column -1 and value 0 before.  One thread per panel.
+__global__ void k_row_step_fill(const int* __restrict__ cbase, const int* __restrict__ rbase,
+                                const int* __restrict__ nbat, const uint32_t* __restrict__ rsmask,
+                                const int* __restrict__ rspre, const int* __restrict__ eptr,
+                                const uint32_t* __restrict__ entries,
+                                const int* __restrict__ chunk_cols, int NP,
+                                int* __restrict__ rs_cols, float* __restrict__ rs_vals) {
+    const long long j = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= NP || nbat[j] == 0) return;
+    const long long b0 = rbase[j];
+    for (int c = cbase[j]; c < cbase[j + 1]; ++c) {
+        for (int e = eptr[c]; e < eptr[c + 1]; ++e) {
+            const uint32_t w = entries[2 * (long long)e];
+            const int r = w & 15, k = (w >> 4) & 31, g = r >> 2, x = r & 3;
+            const int s = rspre[4LL * c + g] + __popc(rsmask[4LL * c + g] & ((1u << k) - 1u));
+            const long long b = b0 + s / 8;
+            const int t = s & 7;
+            // FP32 tiles keep their columns in K-step order: column k at slot (k & 3) * 8 + k / 4
+            rs_cols[32 * b + 8 * g + t] = chunk_cols[(long long)c * kChunkCols + (k & 3) * 8 + (k >> 2)];
+            rs_vals[256 * b + 64 * g + 8 * x + t] = __uint_as_float(entries[2 * (long long)e + 1]);
+        }
+    }
+}
+
+__global__ void k_pick_work(const int* __restrict__ nbat, int NP, int* __restrict__ nch) {
+    const long long j = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (j < NP && nbat[j] > 0) nch[j] = nbat[j];
+}
+
 // Units.  A panel with at most `light_max` tiles is one light unit (one wave); a larger panel
 // is cut into heavy units of at most `heavy_tiles` tiles (the waves of a work-group share them).
 // nsplit[j] = 1 for a panel cut into several units.
@@ -440,7 +507,11 @@ __global__ void k_units_per_panel(const int* __restrict__ nch, int NP, int light
 // that panels reading the same B rows run close together on one XCD (see light_by_column).
 // The first unit of a split panel also carries kUnitSplitFirst (it clears the panel's rows before
 // an overwriting launch, see spmm_launch).
-__global__ void k_make_units(const int* __restrict__ cbase, const int* __restrict__ ubase,
+// A panel's work items are its tiles cbase[j] .. cbase[j + 1], or, where nbat[j] > 0, its
+// row-step batches rbase[j] .. rbase[j] + nbat[j] (units flagged kUnitRowSteps); `nch` counts
+// them either way.
+__global__ void k_make_units(const int* __restrict__ cbase, const int* __restrict__ rbase,
+                             const int* __restrict__ nbat, const int* __restrict__ ubase,
                              const int* __restrict__ ppanel, const int* __restrict__ pmask,
                              const int* __restrict__ nch, int NP, int light_max, int heavy_tiles,
                              const int* __restrict__ chunk_cols, bool by_column,
@@ -448,20 +519,23 @@ __global__ void k_make_units(const int* __restrict__ cbase, const int* __restric
                              uint32_t* __restrict__ pay) {
     const long long j = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     if (j >= NP) return;
-    const int c0 = cbase[j], c1 = cbase[j + 1];
+    const bool rows = nbat != nullptr && nbat[j] > 0;
+    const int c0 = rows ? rbase[j] : cbase[j], c1 = c0 + nch[j];
     const int u0 = ubase[j], nu = ubase[j + 1] - u0;
     const bool heavy = nch[j] > light_max;
     const int split = nu > 1 ? kUnitSplit : 0;
+    const int kind = rows ? kUnitRowSteps : 0;
     const int step = heavy ? heavy_tiles : (c1 - c0);
     for (int u = 0; u < nu; ++u) {
         const int cb = c0 + u * step;
         const int ce = min(cb + step, c1);
         const int first = (split && u == 0) ? kUnitSplitFirst : 0;
         units[u0 + u] =
-            make_int4(ppanel[j] * kPanelRows, cb, ce, (pmask[j] & 0xffff) | split | first);
+            make_int4(ppanel[j] * kPanelRows, cb, ce, (pmask[j] & 0xffff) | split | first | kind);
         // a panel's tile columns ascend, so slot 0 of its first tile is its smallest column
         const uint32_t light =
-            by_column ? 0x80000000u | (uint32_t)chunk_cols[(long long)cb * kChunkCols] : 1u << 16;
+            by_column ? 0x80000000u | (uint32_t)chunk_cols[(long long)cbase[j] * kChunkCols]
+                      : 1u << 16;
         key[u0 + u] = heavy ? (uint32_t)(0xffff - min(ce - cb, 0xffff)) : light;
         pay[u0 + u] = (uint32_t)(u0 + u);
     }
@@ -632,6 +706,36 @@ static void build_exec_layout_k(DeviceFormat& F, const int* trow, const int* tco
         }
     }
 
+    // row steps of FP32 panels whose rows rarely share a column; their units count batches
+    DevBuf<int> nbat, rbase;
+    int NB = 0;
+    // (in the default mode only in formats whose launches take O tiles of 64 anyway: the
+    // multiply kernel carries the row-step path only at that width)
+    int rs_mode = F.fp32 ? fp32_row_steps() : 0;
+    if (rs_mode == 1 && !fp32_narrow_o_tiles(n, NC, NP)) rs_mode = 0;
+    if (rs_mode != 0) {
+        DevBuf<uint32_t> rsmask((size_t)NC * 4);
+        DevBuf<int> rspre((size_t)NC * 4);
+        nbat.alloc(NP);
+        rbase.alloc(NP + 1);
+        LAUNCH(k_row_step_masks, NC, F.chunk_eptr.p, F.entries.p, NC, rsmask.p);
+        LAUNCH(k_row_step_counts, NP, cbase.p, rsmask.p, NP, rs_mode == 2, kRowStepRatioNum,
+               kRowStepRatioDen, rspre.p, nbat.p);
+        exclusive_sum<int, int>(nbat.p, rbase.p, NP, st);
+        NB = read_scalar(rbase.p + NP, st);
+        if (NB > 0) {
+            F.rs_cols.alloc((size_t)NB * kChunkCols);
+            F.rs_vals.alloc((size_t)NB * 256);
+            fill<int>(F.rs_cols.p, (long long)NB * kChunkCols, -1, st);
+            fill<float>(F.rs_vals.p, (long long)NB * 256, 0.0f, st);
+            LAUNCH(k_row_step_fill, NP, cbase.p, rbase.p, nbat.p, rsmask.p, rspre.p,
+                   F.chunk_eptr.p, F.entries.p, F.chunk_cols.p, NP, F.rs_cols.p, F.rs_vals.p);
+            // a panel's work items: its batches where it takes row steps, else its tiles
+            LAUNCH(k_pick_work, NP, nbat.p, NP, nch.p);
+        }
+    }
+    F.num_row_step_batches = NB;
+
     const int light_max = light_tile_limit(NP);
     const int heavy_tiles = heavy_tile_limit(NC);
     DevBuf<int> nu(NP), ubase(NP + 1), nheavy(NP), hbase(NP + 1), nsplit(NP), sbase(NP + 1);
@@ -646,7 +750,8 @@ static void build_exec_layout_k(DeviceFormat& F, const int* trow, const int* tco
         DevBuf<int4> raw(NU);
         DevBuf<uint32_t> k1(NU), k2(NU), v1(NU), v2(NU);
         const bool by_column = light_by_column(n, F.num_pairs);
-        LAUNCH(k_make_units, NP, cbase.p, ubase.p, ppanel.p, pmask.p, nch.p, NP, light_max,
+        LAUNCH(k_make_units, NP, cbase.p, NB > 0 ? rbase.p : nullptr,
+               NB > 0 ? nbat.p : nullptr, ubase.p, ppanel.p, pmask.p, nch.p, NP, light_max,
                heavy_tiles, F.chunk_cols.p, by_column, raw.p, k1.p, v1.p);
         uint32_t *kp2 = k1.p, *ka2 = k2.p, *vp2 = v1.p, *va2 = v2.p;
         radix_sort_pairs<uint32_t>(kp2, vp2, ka2, va2, NU, by_column ? 32 : 17, st);
@@ -678,6 +783,7 @@ static void build_layout_in_order(DeviceFormat& F, const int* trow, const int* t
                                   const float* tval, const int* rowpos, long long n,
                                   hipStream_t st) {
     F.num_panels = F.num_chunks = F.num_units = F.num_dense = F.max_panel_tiles = 0;
+    F.num_row_step_batches = 0;
     F.num_pairs = 0;
     if (n == 0) return;
     const int num_panels_all = (F.M + kPanelRows - 1) / kPanelRows;
@@ -710,12 +816,20 @@ static void swap_layout(DeviceFormat& a, DeviceFormat& b) {
     std::swap(a.chunk_dense, b.chunk_dense);
     std::swap(a.dense_a16, b.dense_a16);
     std::swap(a.dense_a32, b.dense_a32);
+    std::swap(a.num_row_step_batches, b.num_row_step_batches);
+    std::swap(a.rs_cols, b.rs_cols);
+    std::swap(a.rs_vals, b.rs_vals);
 }
 
 // 0 off, 1 when it pays (the default), 2 always; read once by each build.
 static std::atomic<int> g_row_grouping{1};
 void set_row_grouping(int mode) { g_row_grouping.store(mode, std::memory_order_relaxed); }
 int row_grouping() { return g_row_grouping.load(std::memory_order_relaxed); }
+
+// 0 tiles only, 1 row steps where they pay (the default), 2 always; read once by each build.
+static std::atomic<int> g_fp32_row_steps{1};
+void set_fp32_row_steps(int mode) { g_fp32_row_steps.store(mode, std::memory_order_relaxed); }
+int fp32_row_steps() { return g_fp32_row_steps.load(std::memory_order_relaxed); }
 
 // The execution layout's row order.  Mode 0: natural.  Otherwise, first, rows without nonzeros
 // go after the others when they are at least an eighth of the rows (compact_rows; R-MAT scale

@@ -27,6 +27,10 @@ constexpr int kHeavyTiles = 64;
 // Flag bits of units[u].w above the 16-bit row mask.
 constexpr int kUnitSplit = 1 << 16;       // the panel has several units (merge through atomics)
 constexpr int kUnitSplitFirst = 1 << 17;  // ... and this is its first unit
+constexpr int kUnitRowSteps = 1 << 18;    // the unit runs row-step batches, not tiles (FP32)
+// Row steps of an FP32 panel, kept where a panel needs at most this many batches per tile
+// (as numerator / denominator), in the default mode (format_build.hip, k_row_step_counts).
+constexpr int kRowStepRatioNum = 3, kRowStepRatioDen = 2;
 constexpr int kWaves = 4;
 
 // Light-unit ranges per XCD, passed to the multiply kernels by value.
@@ -47,7 +51,8 @@ struct XcdSplit {
 //                     (rows pos0 + r in natural order, row_map[pos0 + r] with a row map;
 //                     rowmask bit r = that position holds a row with nonzeros); kUnitSplit =
 //                     the panel has several units, whose partial sums meet in C through
-//                     atomics, kUnitSplitFirst = the first of them.  The first
+//                     atomics, kUnitSplitFirst = the first of them; with kUnitRowSteps,
+//                     chunk_begin .. chunk_end are row-step batches (below).  The first
 //                     num_heavy units are heavy (one work-group each, larger first), the rest
 //                     light (one wave each, four per work-group, in panel order, or in the
 //                     order of the panels' first columns for blocks; XCD x runs the range
@@ -58,6 +63,20 @@ struct XcdSplit {
 //   entries[e]      FP16 format: f16 value | row-in-panel << 16 | k << 20
 //                   FP32 format: two words per entry, entries[2e] = row-in-panel | k << 4 and
 //                   entries[2e+1] = the value's bits
+//   row steps       (FP32 formats, panels whose rows rarely share a column): instead of tiles,
+//                   a unit runs batches of 8 steps of v_mfma_f32_4x4x1_16b_f32, whose 16
+//                   blocks are the panel's 4 row groups (rows 4g..4g+3) x 4 groups of output
+//                   columns.  At each step every row group g takes its own next column: the
+//                   row group's distinct columns in ascending order, one per step, padded with
+//                   -1 after the last; a panel has as many steps as its busiest row group has
+//                   columns, rounded up to 8.  rs_cols[32b + 8g + t] = the column of step t of
+//                   batch b for row group g (the slots the tile path's lane group g reads), and
+//                   rs_vals[256b + 64g + 8x + t] = the value of row 4g + x at that column (0 if
+//                   the row does not hold it), so a lane reads its eight A values with two
+//                   128-bit loads.  A panel takes row steps when its batches are at most
+//                   kRowStepRatioNum / kRowStepRatioDen times its tiles: each step costs a
+//                   quarter of the matrix-core cycles of a 16x16x4 K step and the same one B
+//                   row load per lane.
 //   chunk_dense[c]  -1, or the index of the tile's dense copy when more than kDenseMin of its
 //                   512 slots are filled (every tile of a small FP32 format, kSmallPanels):
 //                   dense_a16[512 d + 32 row + k] (FP16), or
@@ -67,6 +86,15 @@ struct XcdSplit {
 // panel: every multi-tile panel is then shared by a work-group (format_build.hip), and FP32
 // formats take O tiles of 64 (spmm_kernels.hip).
 constexpr int kFewPanels = 2048;
+// Tiles holding fewer nonzeros than this on average are sparse (about one gathered B row per
+// nonzero); FP32 formats with sparse tiles, or with fewer than kFewPanels32 panels, take O
+// tiles of 64 (spmm_kernels.hip, o_tile_width), and only such formats take row steps in the
+// default mode (format_build.hip).
+constexpr int kSparseTileNnz = 48;
+constexpr int kFewPanels32 = 8192;
+inline bool fp32_narrow_o_tiles(long long nnz, int num_chunks, int num_panels) {
+    return nnz < (long long)kSparseTileNnz * num_chunks || num_panels < kFewPanels32;
+}
 
 struct DeviceFormat {
     int M = 0, N = 0, segw = 16, bundle = 16, num_segments = 0;
@@ -96,6 +124,9 @@ struct DeviceFormat {
     DevBuf<int> chunk_dense;
     DevBuf<_Float16> dense_a16;
     DevBuf<float> dense_a32;
+    int num_row_step_batches = 0;
+    DevBuf<int> rs_cols;
+    DevBuf<float> rs_vals;
 
     // FP32 B converted to binary16 for an FP16 format (spmm_launch), reused across calls.
     mutable DevBuf<_Float16> b_half;
@@ -124,6 +155,11 @@ bool compact_rows(const int* trow, long long n, int M, hipStream_t st, DevBuf<in
 // Read by later builds.
 void set_row_grouping(int mode);
 int row_grouping();
+// Product of FP32 panels: 0 tiles only, 1 row steps where they take at most kRowStepRatioNum /
+// kRowStepRatioDen batches per tile (the default), 2 row steps for every FP32 panel.  Read by
+// later builds.
+void set_fp32_row_steps(int mode);
+int fp32_row_steps();
 
 // GPU format pipeline from a device CSR (src/vcsr_mc.cu:25-123).
 void build_from_csr(DeviceFormat& F, const int* d_row_ptr, const int* d_col, const float* d_val,

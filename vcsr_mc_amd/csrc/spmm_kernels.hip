@@ -566,6 +566,25 @@ __device__ __forceinline__ void mfma_half_f32(const float (&a)[8], int s0, const
     }
 }
 
+// Row steps s0 .. s0 + 3 of one batch on v_mfma_f32_4x4x1_16b_f32: block b = lane / 4 is row
+// group g = b / 4 (rows 4g .. 4g + 3) and output columns c0 of lanes 4b .. 4b + 3; lane 4b + i
+// gives A row i (a[s] = the value of row 4g + i at row group g's step-s column) and lane 4b + j
+// B column j (R.r[s][q] = that column's B row at output column c0 + q), so register i of lane
+// (n, g) accumulates row 4g + i at output column c0 + q -- where the 16x16x4 steps of a tile
+// leave it, and the same epilogue applies.  Steps whose four columns are all padding end the
+// batch.
+template <int VEC>
+__device__ __forceinline__ void mfma_half_rs(const float (&a)[8], int s0, const int (&cols)[8],
+                                             const FRows<VEC>& R, floatx4 (&acc)[VEC]) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+        if (__ballot(cols[s0 + s] >= 0) == 0) return;
+#pragma unroll
+        for (int q = 0; q < VEC; ++q)
+            acc[q] = __builtin_amdgcn_mfma_f32_4x4x1f32(a[s0 + s], R.r[s][q], acc[q], 0, 0, 0);
+    }
+}
+
 // A state of an FP32 tile in eight words per lane, three loads either way: the dense operand
 // (8 floats), or this lane's (entry, value) pairs eb + lane, eb + 64 + lane, eb + 128 + lane
 // (clamped into the tile; the scatter skips the ones past ee).
@@ -650,7 +669,11 @@ __device__ __forceinline__ void a_operand_f32(const TileMeta& m, const AState32&
 //   2. load X (d), A state (d);  multiply steps 4-7 of c (Y); load columns of c + 2W
 //   3. load Y (d);               multiply steps 0-3 of d (X)
 //   4. load X (c + 2W), A state; multiply steps 4-7 of d (Y); load columns of c + 3W
-template <int TK, bool ALIGNED, typename Pre>
+//
+// RS: the unit's work items are row-step batches instead (column slots in chunk_cols = rs_cols,
+// A values in dense_a = rs_vals, 256 per batch, this lane's eight at 64 g + 8 (lane & 3)), with
+// the same loads of columns and B rows and mfma_half_rs as the product.
+template <int TK, bool ALIGNED, bool RS, typename Pre>
 __device__ __forceinline__ void tiles_f32(int first, int end, int W, int lane, int n, int g,
                                           int c0, long long OL, const int* __restrict__ chunk_eptr,
                                           const int* __restrict__ chunk_cols,
@@ -662,58 +685,89 @@ __device__ __forceinline__ void tiles_f32(int first, int end, int W, int lane, i
     constexpr int VEC = TK / 16;
     if (first >= end) return;
     const int a_off = g * 128 + n * 8;  // in a dense copy
+    const int rs_off = g * 64 + (lane & 3) * 8;  // in a row-step batch
     float* my_a = &Aw[g * kAgroup32 + n * kApitch32];
+    auto meta = [&](int c) {
+        if constexpr (RS) return TileMeta{c, 0, 0};
+        else return tile_meta(c, chunk_dense, chunk_eptr);
+    };
+    auto load_a = [&](const TileMeta& m) {
+        if constexpr (RS) {
+            const float* p = dense_a + (long long)m.d * 256 + rs_off;
+            return AState32{*reinterpret_cast<const uint4*>(p),
+                            *reinterpret_cast<const uint4*>(p + 4)};
+        } else {
+            return load_a32(m, lane, a_off, entries, dense_a);
+        }
+    };
+    auto operand = [&](const TileMeta& m, const AState32& st, float (&a)[8]) {
+        if constexpr (RS) {
+            const floatx4 lo = __builtin_bit_cast(floatx4, st.lo);
+            const floatx4 hi = __builtin_bit_cast(floatx4, st.hi);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                a[i] = lo[i];
+                a[4 + i] = hi[i];
+            }
+        } else {
+            a_operand_f32(m, st, lane, Aw, my_a, a);
+        }
+    };
+    auto mma = [&](const float (&a)[8], int s0, const int (&cols)[8], const FRows<VEC>& R) {
+        if constexpr (RS) mfma_half_rs<VEC>(a, s0, cols, R, acc);
+        else mfma_half_f32<VEC>(a, s0, cols, R, acc);
+    };
     const int last = first + (end - 1 - first) / W * W;
     int c = first;
     FRows<VEC> X, Y;
     int colsA[8], colsB[8];
     float a[8];
-    TileMeta mA = tile_meta(c, chunk_dense, chunk_eptr);
+    TileMeta mA = meta(c);
     load_cols8(chunk_cols, c, g, colsA);
     const int c1 = min(c + W, last);
     load_cols8(chunk_cols, c1, g, colsB);
-    TileMeta mB = tile_meta(c1, chunk_dense, chunk_eptr);
+    TileMeta mB = meta(c1);
     load_b_half_f32<VEC, ALIGNED>(B, colsA, 0, OL, c0, X);
-    AState32 sA = load_a32(mA, lane, a_off, entries, dense_a), sB;
+    AState32 sA = load_a(mA), sB;
     for (; c + W < last; c += 2 * W) {
         load_b_half_f32<VEC, ALIGNED>(B, colsA, 4, OL, c0, Y);
-        a_operand_f32(mA, sA, lane, Aw, my_a, a);
-        mfma_half_f32<VEC>(a, 0, colsA, X, acc);
+        operand(mA, sA, a);
+        mma(a, 0, colsA, X);
 
         load_b_half_f32<VEC, ALIGNED>(B, colsB, 0, OL, c0, X);
-        sB = load_a32(mB, lane, a_off, entries, dense_a);
-        mfma_half_f32<VEC>(a, 4, colsA, Y, acc);
+        sB = load_a(mB);
+        mma(a, 4, colsA, Y);
         load_cols8(chunk_cols, c + 2 * W, g, colsA);
-        const TileMeta mA2 = tile_meta(c + 2 * W, chunk_dense, chunk_eptr);
+        const TileMeta mA2 = meta(c + 2 * W);
 
         load_b_half_f32<VEC, ALIGNED>(B, colsB, 4, OL, c0, Y);
-        a_operand_f32(mB, sB, lane, Aw, my_a, a);
-        mfma_half_f32<VEC>(a, 0, colsB, X, acc);
+        operand(mB, sB, a);
+        mma(a, 0, colsB, X);
 
         load_b_half_f32<VEC, ALIGNED>(B, colsA, 0, OL, c0, X);
-        sA = load_a32(mA2, lane, a_off, entries, dense_a);
-        mfma_half_f32<VEC>(a, 4, colsB, Y, acc);
+        sA = load_a(mA2);
+        mma(a, 4, colsB, Y);
         const int c3 = min(c + 3 * W, last);
         load_cols8(chunk_cols, c3, g, colsB);
-        mB = tile_meta(c3, chunk_dense, chunk_eptr);
+        mB = meta(c3);
         mA = mA2;
     }
     load_b_half_f32<VEC, ALIGNED>(B, colsA, 4, OL, c0, Y);
-    a_operand_f32(mA, sA, lane, Aw, my_a, a);
-    mfma_half_f32<VEC>(a, 0, colsA, X, acc);
+    operand(mA, sA, a);
+    mma(a, 0, colsA, X);
     // `pre` runs before the last half tile is multiplied, once X is free (see read_c_ahead).
     if (c < last) {  // two tiles left: c and c + W = last
         load_b_half_f32<VEC, ALIGNED>(B, colsB, 0, OL, c0, X);
-        sB = load_a32(mB, lane, a_off, entries, dense_a);
-        mfma_half_f32<VEC>(a, 4, colsA, Y, acc);
+        sB = load_a(mB);
+        mma(a, 4, colsA, Y);
         load_b_half_f32<VEC, ALIGNED>(B, colsB, 4, OL, c0, Y);
-        a_operand_f32(mB, sB, lane, Aw, my_a, a);
-        mfma_half_f32<VEC>(a, 0, colsB, X, acc);
+        operand(mB, sB, a);
+        mma(a, 0, colsB, X);
         pre();
-        mfma_half_f32<VEC>(a, 4, colsB, Y, acc);
+        mma(a, 4, colsB, Y);
     } else {
         pre();
-        mfma_half_f32<VEC>(a, 4, colsA, Y, acc);
+        mma(a, 4, colsA, Y);
     }
 }
 
@@ -722,7 +776,8 @@ __global__ __launch_bounds__(64 * kWaves, 3) void k_spmm_f32(
     const int4* __restrict__ units, const int* __restrict__ rmap, int num_heavy, XcdSplit xs,
     const int* __restrict__ chunk_eptr, const int* __restrict__ chunk_cols,
     const int* __restrict__ chunk_dense, const uint32_t* __restrict__ entries,
-    const float* __restrict__ dense_a, const float* __restrict__ B, int O, bool c4,
+    const float* __restrict__ dense_a, const int* __restrict__ rs_cols,
+    const float* __restrict__ rs_vals, const float* __restrict__ B, int O, bool c4,
     float* __restrict__ C) {
     constexpr int VEC = TK / 16;
     __shared__ __attribute__((aligned(16))) float At[kWaves][4 * kAgroup32];
@@ -739,17 +794,32 @@ __global__ __launch_bounds__(64 * kWaves, 3) void k_spmm_f32(
     floatx4 acc[VEC];
 #pragma unroll
     for (int q = 0; q < VEC; ++q) acc[q] = floatx4{0.f, 0.f, 0.f, 0.f};
+    // The unit's work items, tiles or row-step batches (wave-uniform: U is a scalar load).  A
+    // format with row steps always launches O tiles of at most 64 (o_tile_width): at 128 the
+    // second path would make the kernel spill.
+    const bool rs = TK <= 64 && (U.w & kUnitRowSteps);
+    // Runs the unit's work items from `first` in strides of W, then `pre`.
+    auto run = [&](int first, int W, auto&& pre) {
+        if constexpr (TK <= 64) {
+            if (rs) {
+                tiles_f32<TK, ALIGNED, true>(first, U.z, W, lane, n, g, c0, (long long)O,
+                                             chunk_eptr, rs_cols, chunk_dense, entries, rs_vals,
+                                             B, At[wave], acc, pre);
+                return;
+            }
+        }
+        tiles_f32<TK, ALIGNED, false>(first, U.z, W, lane, n, g, c0, (long long)O, chunk_eptr,
+                                      chunk_cols, chunk_dense, entries, dense_a, B, At[wave], acc,
+                                      pre);
+    };
     if (heavy) {
         CAhead<TK, kWaves> ca;
         read_c_ahead<TK, kWaves>(ca, U, pr, k0, O, c4, ACC, C);
-        tiles_f32<TK, ALIGNED>(U.y + wave, U.z, kWaves, lane, n, g, c0, (long long)O, chunk_eptr,
-                               chunk_cols, chunk_dense, entries, dense_a, B, At[wave], acc, [] {});
+        run(U.y + wave, kWaves, [] {});
         merge_into_c<TK, kWaves, ACC>(acc, 1.0f, U, pr, k0, O, c4, C, P, ca);
     } else {
         CAhead<TK, 1> ca;
-        tiles_f32<TK, ALIGNED>(U.y, U.z, 1, lane, n, g, c0, (long long)O, chunk_eptr, chunk_cols,
-                               chunk_dense, entries, dense_a, B, At[wave], acc,
-                               [&] { read_c_ahead<TK, 1>(ca, U, pr, k0, O, c4, ACC, C); });
+        run(U.y, 1, [&] { read_c_ahead<TK, 1>(ca, U, pr, k0, O, c4, ACC, C); });
         merge_into_c<TK, 1, ACC>(acc, 1.0f, U, pr, k0, O, c4, C, P, ca);
     }
 }
@@ -783,13 +853,20 @@ static void launch_tk_mode(const DeviceFormat& F, const void* dB, bool b_f16, in
     const int *eptr = F.chunk_eptr.p, *cols = F.chunk_cols.p, *dense = F.chunk_dense.p;
     const uint32_t* ent = F.entries.p;
     if (F.fp32) {
+        // row-step units exist only in kernels of O tiles up to 64 (o_tile_width keeps to that)
+        if (TK > 64 && F.num_row_step_batches > 0)
+            throw Error(VCSRMC_ERR_STATE, "row steps need O tiles of at most 64");
         const float* B = static_cast<const float*>(dB);
+        const int* rsc = F.rs_cols.p;
+        const float* rsv = F.rs_vals.p;
         if (aligned)
             hipLaunchKernelGGL((k_spmm_f32<TK, true, ACC, MAPPED>), grid, block, 0, st, U, rmap,
-                               NH, xs, eptr, cols, dense, ent, F.dense_a32.p, B, O, c4, dC);
+                               NH, xs, eptr, cols, dense, ent, F.dense_a32.p, rsc, rsv, B, O, c4,
+                               dC);
         else
             hipLaunchKernelGGL((k_spmm_f32<TK, false, ACC, MAPPED>), grid, block, 0, st, U, rmap,
-                               NH, xs, eptr, cols, dense, ent, F.dense_a32.p, B, O, c4, dC);
+                               NH, xs, eptr, cols, dense, ent, F.dense_a32.p, rsc, rsv, B, O, c4,
+                               dC);
     } else if (b_f16) {
         const _Float16* B = static_cast<const _Float16*>(dB);
         if (aligned)
@@ -878,6 +955,8 @@ __global__ void k_b_to_half(const float* __restrict__ B, _Float16* __restrict__ 
 //     24.0 -> 22.8; 4 x 4 blocks, 20,000 block rows 46.3 -> 43.7; a band of 33 per row,
 //     50,000 rows 23.8 -> 22.6; an arrow matrix, 100,000 rows 45.6 -> 39.5 us; 2D 9-point
 //     300^2 32.7 -> 31.8; 5-point 500^2 (15,625 panels) and 7-point 60^3 (13,500) within 1%);
+//   * 64 for FP32 formats holding row steps (which only such formats take in the default mode):
+//     the kernels carry the row-step path only up to that width;
 //   * 64 for FP16 B above 4 MB with sparse tiles whose panels are alike (no panel more than three
 //     times the average tile count, as in uniform random matrices; power-law and R-MAT
 //     matrices have panels of hub rows 10x the average and keep 128): their B rows are used a
@@ -892,15 +971,15 @@ __global__ void k_b_to_half(const float* __restrict__ B, _Float16* __restrict__ 
 //   Otherwise fuller tiles keep 128, since every O tile repeats the A side of each tile
 //   (27-point stencil 100^3 and 32 x 32 blocks at 8192 block rows: 2-14% slower at 64), as do
 //   FP16 formats with a cache-resident FP16 B (power-law: 15.4 -> 17.4 us at 64).
-constexpr int kFewPanels32 = 8192;
-
 static int o_tile_width(const DeviceFormat& F, bool b_f16, int O, int tileK) {
     int tk = tileK;
     while (tk > 16 && tk / 2 >= O) tk /= 2;
     if (tk == 128 && F.num_chunks > 0) {
-        const bool sparse_tiles = F.nnz < 48LL * F.num_chunks;
+        const bool sparse_tiles = F.nnz < (long long)kSparseTileNnz * F.num_chunks;
         const long long b_bytes = (long long)F.N * O * (b_f16 ? 2 : 4);
-        if (F.fp32 && (sparse_tiles || F.num_panels < kFewPanels32)) tk = 64;
+        if (F.fp32 && (fp32_narrow_o_tiles(F.nnz, F.num_chunks, F.num_panels) ||
+                       F.num_row_step_batches > 0))
+            tk = 64;
         else if (!F.fp32 && !b_f16) tk = 64;
         else if (sparse_tiles && b_bytes > (32LL << 20)) tk = 64;
         else if (sparse_tiles && b_bytes > (4LL << 20) &&
@@ -937,7 +1016,7 @@ void spmm_launch(const DeviceFormat& F, const void* dB, bool b_f16, int O, int t
     const long long b32_bytes = (long long)F.N * O * 4;
     if (!F.fp32 && !b_f16 && ((uintptr_t)dB % 16) == 0 && F.num_chunks > 0 &&
         F.nnz >= 12LL * F.N &&
-        ((F.nnz < 48LL * F.num_chunks && b32_bytes > (12LL << 20)) ||
+        ((F.nnz < (long long)kSparseTileNnz * F.num_chunks && b32_bytes > (12LL << 20)) ||
          b32_bytes > (256LL << 20))) {
         const long long n = (long long)F.N * O;
         _Float16* half = ext.p;
