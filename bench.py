@@ -231,7 +231,8 @@ def run_config(cfg, args, stream, want_cpu, cpu_seconds, prec_override=None):
            "O": O, "precision": prec, "B": "fp32" if b32 else "fp16 in HBM",
            "format_build_ms": round(build_ms, 3), "bytes_alg": int(bytes_alg),
            "layout": {k: info[k] for k in ("num_panels", "num_chunks", "num_units", "num_heavy",
-                                           "num_split_panels", "num_dense", "row_grouped")}}
+                                           "num_split_panels", "num_dense", "row_grouped",
+                                           "num_row_step_batches")}}
     full = args.size == 0 and O == w["O"] and args.tileK == TILEK and not args.b_fp32
     oracle = None
     if want_cpu:

@@ -51,6 +51,7 @@ def test_bench_json_line():
     lay = p["layout"]
     assert 0 < lay["num_panels"] <= lay["num_units"] <= lay["num_chunks"]
     assert lay["num_heavy"] <= lay["num_units"] and lay["row_grouped"] in (0, 1)
+    assert lay["num_row_step_batches"] > 0  # uniform random FP32 panels take row steps
     for mode in ("accumulate", "overwrite"):
         m = p[mode]
         assert m["parity_row_sample"] is True

@@ -25,6 +25,11 @@
 //     of v_mfma_f32_16x16x4_f32, in two halves.
 //   The K order inside a tile is the same for A and B, so the contraction does not depend
 //   on how the instruction maps lanes to K.
+// FP32 panels whose rows rarely share a column run batches of 8 row steps instead of tiles
+// (units flagged kUnitRowSteps): v_mfma_f32_4x4x1_16b_f32 with its 16 blocks as 4 row groups x
+// 4 groups of output columns, each row group at its own column per step, a quarter of the
+// cycles of a 16x16x4 step.  Lane group g loads the 8 step columns of row group g exactly as it
+// loads 8 tile columns, and the accumulators end where the tile path leaves them.
 //
 // Epilogue: lane (n, g) holds rows 4g..4g+3 at output columns k0 + VEC n .. + VEC-1, so each
 // row is written as VEC contiguous floats per lane, 16 lanes per row: coalesced.  Rows that
