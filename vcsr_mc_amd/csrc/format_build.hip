@@ -419,10 +419,10 @@ __global__ void k_dense_fill(const uint32_t* __restrict__ entries,
 }
 
 // Row steps of FP32 panels (the layout is described with DeviceFormat).  rsmask[4c + g] = the
-// columns k of tile c that row group g (rows 4g .. 4g + 3) holds, as a 32-bit set; one thread per
-// tile.
+// columns k of tile c that row group g (rows 4g .. 4g + 3) holds, as a 32-bit set, and
+// rscnt[g * NC + c] = their number; one thread per tile.
 __global__ void k_row_step_masks(const int* __restrict__ eptr, const uint32_t* __restrict__ entries,
-                                 int NC, uint32_t* __restrict__ rsmask) {
+                                 int NC, uint32_t* __restrict__ rsmask, int* __restrict__ rscnt) {
     const long long c = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     if (c >= NC) return;
     uint32_t m[4] = {0u, 0u, 0u, 0u};
@@ -430,53 +430,63 @@ __global__ void k_row_step_masks(const int* __restrict__ eptr, const uint32_t* _
         const uint32_t w = entries[2 * (long long)e];
         m[(w & 15) >> 2] |= 1u << ((w >> 4) & 31);
     }
-    for (int g = 0; g < 4; ++g) rsmask[4 * c + g] = m[g];
+    for (int g = 0; g < 4; ++g) {
+        rsmask[4 * c + g] = m[g];
+        rscnt[g * (long long)NC + c] = __popc(m[g]);
+    }
 }
 
-// Per panel j (tiles cbase[j] .. cbase[j + 1]): rspre[4c + g] = row group g's columns in the
-// panel's tiles before c, and nbat[j] = the panel's batches of 8 row steps (its busiest row
-// group's columns / 8, rounded up) where it takes row steps, else 0: always (`all`), or when
-// they are at most num / den per tile.  One thread per panel.
-__global__ void k_row_step_counts(const int* __restrict__ cbase, const uint32_t* __restrict__ rsmask,
-                                  int NP, bool all, int num, int den, int* __restrict__ rspre,
-                                  int* __restrict__ nbat) {
+// nbat[j] = panel j's batches of 8 row steps (its busiest row group's columns, from the
+// exclusive sums rspre[g * (NC + 1) + c] of rscnt over the tiles, / 8 rounded up) where it takes
+// row steps, else 0: always (`all`), or when they are at most num / den per tile.  One thread
+// per panel.
+__global__ void k_row_step_batches(const int* __restrict__ cbase, const int* __restrict__ rspre,
+                                   int NP, int NC, bool all, int num, int den,
+                                   int* __restrict__ nbat) {
     const long long j = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     if (j >= NP) return;
     const int c0 = cbase[j], c1 = cbase[j + 1];
-    int cnt[4] = {0, 0, 0, 0};
-    for (int c = c0; c < c1; ++c)
-        for (int g = 0; g < 4; ++g) {
-            rspre[4LL * c + g] = cnt[g];
-            cnt[g] += __popc(rsmask[4LL * c + g]);
-        }
-    const int steps = max(max(cnt[0], cnt[1]), max(cnt[2], cnt[3]));
+    int steps = 0;
+    for (int g = 0; g < 4; ++g) {
+        const int* pre = rspre + g * ((long long)NC + 1);
+        steps = max(steps, pre[c1] - pre[c0]);
+    }
     const int nb = (steps + 7) / 8;
     nbat[j] = (all || (long long)nb * den <= (long long)num * (c1 - c0)) ? nb : 0;
 }
 
 // Writes the row steps of the panels that take them: entry (row 4g + x, tile column k of tile
-// c) becomes step s = (row group g's columns before it in the panel) of batch rbase[j] + s / 8.
-// The slots were set to column -1 and value 0 before.  One thread per panel.
+// c in panel j) becomes step s = (row group g's columns in the panel's tiles before it) of batch
+// rbase[j] + s / 8.  The slots were set to column -1 and value 0 before.  One thread per tile;
+// its panel is the last j with cbase[j] <= c.
 __global__ void k_row_step_fill(const int* __restrict__ cbase, const int* __restrict__ rbase,
                                 const int* __restrict__ nbat, const uint32_t* __restrict__ rsmask,
                                 const int* __restrict__ rspre, const int* __restrict__ eptr,
                                 const uint32_t* __restrict__ entries,
-                                const int* __restrict__ chunk_cols, int NP,
+                                const int* __restrict__ chunk_cols, int NP, int NC,
                                 int* __restrict__ rs_cols, float* __restrict__ rs_vals) {
-    const long long j = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (j >= NP || nbat[j] == 0) return;
+    const long long c = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= NC) return;
+    int lo = 0, hi = NP - 1;  // cbase[0] = 0 <= c
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (cbase[mid] <= c) lo = mid;
+        else hi = mid - 1;
+    }
+    const int j = lo;
+    if (nbat[j] == 0) return;
     const long long b0 = rbase[j];
-    for (int c = cbase[j]; c < cbase[j + 1]; ++c) {
-        for (int e = eptr[c]; e < eptr[c + 1]; ++e) {
-            const uint32_t w = entries[2 * (long long)e];
-            const int r = w & 15, k = (w >> 4) & 31, g = r >> 2, x = r & 3;
-            const int s = rspre[4LL * c + g] + __popc(rsmask[4LL * c + g] & ((1u << k) - 1u));
-            const long long b = b0 + s / 8;
-            const int t = s & 7;
-            // FP32 tiles keep their columns in K-step order: column k at slot (k & 3) * 8 + k / 4
-            rs_cols[32 * b + 8 * g + t] = chunk_cols[(long long)c * kChunkCols + (k & 3) * 8 + (k >> 2)];
-            rs_vals[256 * b + 64 * g + 8 * x + t] = __uint_as_float(entries[2 * (long long)e + 1]);
-        }
+    const int c0 = cbase[j];
+    for (int e = eptr[c]; e < eptr[c + 1]; ++e) {
+        const uint32_t w = entries[2 * (long long)e];
+        const int r = w & 15, k = (w >> 4) & 31, g = r >> 2, x = r & 3;
+        const int* pre = rspre + g * ((long long)NC + 1);
+        const int s = pre[c] - pre[c0] + __popc(rsmask[4 * c + g] & ((1u << k) - 1u));
+        const long long b = b0 + s / 8;
+        const int t = s & 7;
+        // FP32 tiles keep their columns in K-step order: column k at slot (k & 3) * 8 + k / 4
+        rs_cols[32 * b + 8 * g + t] = chunk_cols[c * kChunkCols + (k & 3) * 8 + (k >> 2)];
+        rs_vals[256 * b + 64 * g + 8 * x + t] = __uint_as_float(entries[2 * (long long)e + 1]);
     }
 }
 
@@ -715,12 +725,15 @@ static void build_exec_layout_k(DeviceFormat& F, const int* trow, const int* tco
     if (rs_mode == 1 && !fp32_narrow_o_tiles(n, NC, NP)) rs_mode = 0;
     if (rs_mode != 0) {
         DevBuf<uint32_t> rsmask((size_t)NC * 4);
-        DevBuf<int> rspre((size_t)NC * 4);
+        DevBuf<int> rscnt((size_t)NC * 4), rspre(((size_t)NC + 1) * 4);
         nbat.alloc(NP);
         rbase.alloc(NP + 1);
-        LAUNCH(k_row_step_masks, NC, F.chunk_eptr.p, F.entries.p, NC, rsmask.p);
-        LAUNCH(k_row_step_counts, NP, cbase.p, rsmask.p, NP, rs_mode == 2, kRowStepRatioNum,
-               kRowStepRatioDen, rspre.p, nbat.p);
+        LAUNCH(k_row_step_masks, NC, F.chunk_eptr.p, F.entries.p, NC, rsmask.p, rscnt.p);
+        for (int g = 0; g < 4; ++g)
+            exclusive_sum<int, int>(rscnt.p + (size_t)g * NC, rspre.p + (size_t)g * (NC + 1), NC,
+                                    st);
+        LAUNCH(k_row_step_batches, NP, cbase.p, rspre.p, NP, NC, rs_mode == 2, kRowStepRatioNum,
+               kRowStepRatioDen, nbat.p);
         exclusive_sum<int, int>(nbat.p, rbase.p, NP, st);
         NB = read_scalar(rbase.p + NP, st);
         if (NB > 0) {
@@ -728,8 +741,8 @@ static void build_exec_layout_k(DeviceFormat& F, const int* trow, const int* tco
             F.rs_vals.alloc((size_t)NB * 256);
             fill<int>(F.rs_cols.p, (long long)NB * kChunkCols, -1, st);
             fill<float>(F.rs_vals.p, (long long)NB * 256, 0.0f, st);
-            LAUNCH(k_row_step_fill, NP, cbase.p, rbase.p, nbat.p, rsmask.p, rspre.p,
-                   F.chunk_eptr.p, F.entries.p, F.chunk_cols.p, NP, F.rs_cols.p, F.rs_vals.p);
+            LAUNCH(k_row_step_fill, NC, cbase.p, rbase.p, nbat.p, rsmask.p, rspre.p,
+                   F.chunk_eptr.p, F.entries.p, F.chunk_cols.p, NP, NC, F.rs_cols.p, F.rs_vals.p);
             // a panel's work items: its batches where it takes row steps, else its tiles
             LAUNCH(k_pick_work, NP, nbat.p, NP, nch.p);
         }

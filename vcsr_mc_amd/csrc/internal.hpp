@@ -29,7 +29,7 @@ constexpr int kUnitSplit = 1 << 16;       // the panel has several units (merge 
 constexpr int kUnitSplitFirst = 1 << 17;  // ... and this is its first unit
 constexpr int kUnitRowSteps = 1 << 18;    // the unit runs row-step batches, not tiles (FP32)
 // Row steps of an FP32 panel, kept where a panel needs at most this many batches per tile
-// (as numerator / denominator), in the default mode (format_build.hip, k_row_step_counts).
+// (as numerator / denominator), in the default mode (format_build.hip, k_row_step_batches).
 constexpr int kRowStepRatioNum = 3, kRowStepRatioDen = 2;
 constexpr int kWaves = 4;
 
