@@ -110,7 +110,8 @@ int vcsrmc_download(vcsrmc_t h, int *group_ptr, int *group_depth, int *group_seg
  *   - never wider than O needs;
  *   - 64 instead of 128 for formats whose tiles hold few nonzeros (fewer than 48 on average)
  *     that are FP32 or whose B exceeds the GPU's 32 MB of L2;
- *   - 64 for FP32 formats of fewer than 8192 16-row panels;
+ *   - 64 for FP32 formats of fewer than 8192 16-row panels, and for FP32 formats holding row
+ *     steps (vcsrmc_set_fp32_row_steps);
  *   - 64 for FP16 B above 4 MB with sparse tiles and no panel of more than three times the
  *     average tile count (uniform random matrices);
  *   - 64 for an FP16 format reading FP32 B directly (at 128 that kernel holds too many
@@ -191,7 +192,9 @@ int vcsrmc_set_row_grouping(int mode);
  * groups of output columns, lets each group of 4 rows take its own next column, at a quarter of
  * the cycles, so a panel whose rows rarely share a column needs about as many row steps as tile
  * steps.  0: tile steps only; 1 (the default): row steps for every FP32 panel that needs at
- * most 3/2 as many batches of 8 row steps as it has tiles; 2: row steps for every FP32 panel.
+ * most 3/2 as many batches of 8 row steps as it has tiles, in formats whose tiles average fewer
+ * than 48 nonzeros or that have fewer than 8192 panels (those launch O tiles of 64 anyway);
+ * 2: row steps for every FP32 panel.
  * The product is the same up to rounding (each row's sum is formed in another order).
  * vcsrmc_info.num_row_step_batches counts a format's batches.  No counterpart in the
  * reference. */
