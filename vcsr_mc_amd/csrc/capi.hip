@@ -270,8 +270,11 @@ int vcsrmc_spmm_ex(vcsrmc_t h, const void* dB, int b_dtype, int O, int tileK, fl
         VCSRMC_HIP(hipEventCreate(&t0));
         VCSRMC_HIP(hipEventCreate(&t1));
         try {
+            // host decisions first: the events bracket the enqueued kernels only
+            const vcsrmc::SpmmPlan plan =
+                vcsrmc::plan_spmm(h->F, dB, b_dtype == VCSRMC_B_F16, O, tileK, dC, accumulate);
             VCSRMC_HIP(hipEventRecord(t0, st));
-            vcsrmc::spmm_launch(h->F, dB, b_dtype == VCSRMC_B_F16, O, tileK, dC, accumulate, st);
+            vcsrmc::run_spmm(plan, st);
             VCSRMC_HIP(hipEventRecord(t1, st));
             VCSRMC_HIP(hipEventSynchronize(t1));
             VCSRMC_HIP(hipEventElapsedTime(ms, t0, t1));

@@ -190,6 +190,22 @@ struct HalfScratch {
 // accumulate: C += A.B; otherwise C = A.B on the rows A touches (other rows untouched).
 void spmm_launch(const DeviceFormat& F, const void* dB, bool b_f16, int O, int tileK, float* dC,
                  bool accumulate, hipStream_t st, HalfScratch ext = HalfScratch());
+// spmm_launch in two steps: plan_spmm checks the arguments and makes every host decision (O tile
+// width, B conversion and its buffer, split-row clearing), run_spmm only enqueues the kernels,
+// so a caller timing the launch with events brackets GPU work only (as the reference's
+// run_vcsr_mc_spmm_gpu records its first event right before its launch, src/vcsr_mc.cu:381).
+struct SpmmPlan {
+    const DeviceFormat* F = nullptr;
+    const void* dB = nullptr;
+    float* dC = nullptr;
+    int O = 0, tk = 128;
+    bool b_f16 = false, accumulate = true, zero_split = false, launch = false;
+    _Float16* convert_to = nullptr;  // FP32 B converted into this binary16 buffer first
+    long long convert_n = 0;
+};
+SpmmPlan plan_spmm(const DeviceFormat& F, const void* dB, bool b_f16, int O, int tileK, float* dC,
+                   bool accumulate, HalfScratch ext = HalfScratch());
+void run_spmm(const SpmmPlan& p, hipStream_t st);
 
 // Reverse Cuthill-McKee order of the columns of a device CSR (include/reorder.hpp:17-77):
 // position[old column] = new column.  Synchronises `st`.

@@ -994,15 +994,22 @@ static int o_tile_width(const DeviceFormat& F, bool b_f16, int O, int tileK) {
     return tk;
 }
 
-void spmm_launch(const DeviceFormat& F, const void* dB, bool b_f16, int O, int tileK, float* dC,
-                 bool accumulate, hipStream_t st, HalfScratch ext) {
+SpmmPlan plan_spmm(const DeviceFormat& F, const void* dB, bool b_f16, int O, int tileK,
+                   float* dC, bool accumulate, HalfScratch ext) {
     if (tileK != 16 && tileK != 32 && tileK != 64 && tileK != 128)
         throw Error(VCSRMC_ERR_TILEK, "vcsr_mc supports tileK in {16, 32, 64, 128}");
     if (!F.ready) throw Error(VCSRMC_ERR_STATE, "no format in this handle");
     if (O < 0) throw Error(VCSRMC_ERR_ARG, "O must be >= 0");
     if (F.fp32 && b_f16) throw Error(VCSRMC_ERR_ARG, "an FP32 format takes an FP32 B");
-    if (F.num_units == 0 || O == 0) return;
+    SpmmPlan p;
+    p.F = &F;
+    if (F.num_units == 0 || O == 0) return p;  // nothing to launch
     if (!dB || !dC) throw Error(VCSRMC_ERR_ARG, "null B or C");
+    p.dB = dB;
+    p.b_f16 = b_f16;
+    p.O = O;
+    p.dC = dC;
+    p.accumulate = accumulate;
     // FP16 format, FP32 B: the kernel rounds each gathered FP32 B row to binary16 as it loads
     // it.  Converting B once instead costs 6 bytes per element and a pass before the multiply,
     // and saves 2 bytes per element on each gather from beyond the caches, so it pays only for
@@ -1035,23 +1042,42 @@ void spmm_launch(const DeviceFormat& F, const void* dB, bool b_f16, int O, int t
             if (!F.b_half.p || (long long)F.b_half.n < n) F.b_half.alloc((size_t)n);
             half = F.b_half.p;
         }
-        hipLaunchKernelGGL(k_b_to_half, dim3(grid_for((n + 3) / 4, 256)), dim3(256), 0, st,
-                           static_cast<const float*>(dB), half, n);
-        VCSRMC_HIP(hipGetLastError());
-        dB = half;
-        b_f16 = true;
+        p.convert_to = half;
+        p.convert_n = n;
+        p.b_f16 = true;
     }
-    if (!accumulate && F.num_split_panels > 0) {
+    p.zero_split = !accumulate && F.num_split_panels > 0;
+    p.tk = o_tile_width(F, p.b_f16, O, tileK);
+    p.launch = true;
+    return p;
+}
+
+void run_spmm(const SpmmPlan& p, hipStream_t st) {
+    if (!p.launch) return;
+    const DeviceFormat& F = *p.F;
+    const void* dB = p.dB;
+    if (p.convert_to) {
+        hipLaunchKernelGGL(k_b_to_half, dim3(grid_for((p.convert_n + 3) / 4, 256)), dim3(256), 0,
+                           st, static_cast<const float*>(p.dB), p.convert_to, p.convert_n);
+        VCSRMC_HIP(hipGetLastError());
+        dB = p.convert_to;
+    }
+    if (p.zero_split) {
         hipLaunchKernelGGL(k_zero_split_rows, dim3((unsigned)F.num_heavy), dim3(256), 0, st,
-                           F.units.p, F.row_map.n ? F.row_map.p : nullptr, F.num_heavy, O, dC);
+                           F.units.p, F.row_map.n ? F.row_map.p : nullptr, F.num_heavy, p.O, p.dC);
         VCSRMC_HIP(hipGetLastError());
     }
-    switch (o_tile_width(F, b_f16, O, tileK)) {
-        case 16: launch_tk<16>(F, dB, b_f16, O, dC, accumulate, st); break;
-        case 32: launch_tk<32>(F, dB, b_f16, O, dC, accumulate, st); break;
-        case 64: launch_tk<64>(F, dB, b_f16, O, dC, accumulate, st); break;
-        default: launch_tk<128>(F, dB, b_f16, O, dC, accumulate, st); break;
+    switch (p.tk) {
+        case 16: launch_tk<16>(F, dB, p.b_f16, p.O, p.dC, p.accumulate, st); break;
+        case 32: launch_tk<32>(F, dB, p.b_f16, p.O, p.dC, p.accumulate, st); break;
+        case 64: launch_tk<64>(F, dB, p.b_f16, p.O, p.dC, p.accumulate, st); break;
+        default: launch_tk<128>(F, dB, p.b_f16, p.O, p.dC, p.accumulate, st); break;
     }
+}
+
+void spmm_launch(const DeviceFormat& F, const void* dB, bool b_f16, int O, int tileK, float* dC,
+                 bool accumulate, hipStream_t st, HalfScratch ext) {
+    run_spmm(plan_spmm(F, dB, b_f16, O, tileK, dC, accumulate, ext), st);
 }
 
 }  // namespace vcsrmc
