@@ -373,7 +373,7 @@ std::vector<double> time_launches(Kernel& k, Operands& d, int warmup, int repeat
     return t;
 }
 
-struct Verdict {
+struct Outcome {
     double rel_l2 = 0;
     bool failed = false;
 };
@@ -382,9 +382,9 @@ struct Verdict {
 // (src/main.cpp:257-291): error <= tol_rel * ||ref|| + 1e-5 sqrt(|C|) and rel_l2 <= cap, with
 // (tol_rel, cap) = (3e-3, 1e-1) for FP16 inputs, (1e-4, 1e-2) otherwise.  A non-finite output,
 // or a result outside the bound, aborts unless lenient (then FAIL).
-Verdict validate(const Kernel& k, const std::vector<float>& got, const std::vector<double>& ref,
+Outcome validate(const Kernel& k, const std::vector<float>& got, const std::vector<double>& ref,
                  bool lenient) {
-    Verdict v;
+    Outcome v;
     double err2 = 0, ref2 = 0;
     for (size_t i = 0; i < got.size(); ++i) {
         if (!std::isfinite(got[i])) {
@@ -435,7 +435,7 @@ struct Report {
         std::printf("Kernel                Time (ms)      GFLOP/s   Validation\n");
     }
 
-    void row(const Kernel& k, std::vector<double> t, const Verdict& v) const {
+    void row(const Kernel& k, std::vector<double> t, const Outcome& v) const {
         double sum = 0;
         for (double x : t) sum += x;
         const double mean = sum / (double)t.size();
@@ -444,15 +444,15 @@ struct Report {
         const double median = t.size() % 2 ? t[h] : 0.5 * (t[h - 1] + t[h]);
         const double ms = o.stat == "median" ? median : mean;
         const double gflops = ms > 0 ? 2.0 * (double)a.nnz * o.O / (ms * 1e6) : 0.0;
-        const char* verdict = o.check == "none" ? "unchecked" : v.failed ? "FAIL" : "pass";
+        const char* outcome = o.check == "none" ? "unchecked" : v.failed ? "FAIL" : "pass";
         if (o.csv)
             std::printf("%s,%d,%s,%d,%d,%d,%d,%d,%s,%.9g,%.9g,%s,%.9g,%.6g,%.9g,%.9g,%.6g,%.6g\n",
                         csv_field(device).c_str(), sm, csv_field(source).c_str(), o.O, o.segw, 16,
-                        o.tileK, o.repeat, k.name, ms, gflops, verdict, v.rel_l2, k.setup_ms, mean,
+                        o.tileK, o.repeat, k.name, ms, gflops, outcome, v.rel_l2, k.setup_ms, mean,
                         median, k.convert_ms, k.upload_ms);
         else
             std::printf("%-20s %10.6f %12.2f   %s (rel_l2=%.3g, setup %.3f ms)\n", k.name, ms,
-                        gflops, verdict, v.rel_l2, k.setup_ms);
+                        gflops, outcome, v.rel_l2, k.setup_ms);
         std::fflush(stdout);
     }
 };
@@ -526,7 +526,7 @@ int run(int argc, char** argv) {
     rep.header();
     auto measure = [&](Kernel& k) {
         const std::vector<double> t = time_launches(k, d, o.warmup, o.repeat);
-        const Verdict v = o.check == "none" ? Verdict{} : validate(k, d.C.download(), ref, o.lenient);
+        const Outcome v = o.check == "none" ? Outcome{} : validate(k, d.C.download(), ref, o.lenient);
         rep.row(k, t, v);
     };
     if (wants(o, "rocsparse")) {
