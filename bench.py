@@ -272,6 +272,11 @@ def run_config(cfg, args, stream, want_cpu, cpu_seconds, prec_override=None):
         achieved = bytes_alg / (kernel_ms * 1e-3) / 1e9
         traffic, stamp = measured_traffic(f"config{cfg}-{prec}-{mode}") if full else \
             (None, "measured at the full workload only")
+        # what this launch's schedule cannot avoid moving, if each XCD's L2 kept everything
+        # its work-groups touched: B per XCD row part, the layout per O tile, C once (twice
+        # accumulating)
+        floor = fmt.traffic_floor(O, tileK=args.tileK, b_f16=not b32, overwrite=ow)
+        floor_rate = floor["total"] / (kernel_ms * 1e-3) / 1e9
         mfma_tf = f_exec / (kernel_ms * 1e-3) / 1e12
         ref_tf = f_pad / (kernel_ms * 1e-3) / 1e12
         out[mode] = {
@@ -283,7 +288,13 @@ def run_config(cfg, args, stream, want_cpu, cpu_seconds, prec_override=None):
             "single_launch_gflops": round(flops / (ms_single * 1e-3) / 1e9, 2),
             "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                          "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                         "traffic": traffic, "traffic_source": stamp},
+                         "traffic": traffic, "traffic_source": stamp,
+                         "floor_bytes": int(floor["total"]),
+                         "floor_frac": round(floor_rate / HBM_PEAK_GBS, 4),
+                         "frac_ceiling": round(bytes_alg / floor["total"], 4),
+                         "floor": {k: floor[k] for k in ("b_bytes", "b_once_bytes", "a_bytes",
+                                                         "c_bytes", "convert_bytes",
+                                                         "o_tile_width", "row_parts")}},
             "mfma": {"executed_tflops": round(mfma_tf, 2), "peak": MFMA_PEAK_TFLOPS[prec],
                      "frac": round(mfma_tf / MFMA_PEAK_TFLOPS[prec], 5),
                      "ref_padded_tflops": round(ref_tf, 2),
@@ -291,7 +302,8 @@ def run_config(cfg, args, stream, want_cpu, cpu_seconds, prec_override=None):
             "parity_row_sample": parity,
         }
         log(f"[config {cfg}] {mode}: {kernel_ms * 1e3:.2f} us/launch back to back, single "
-            f"{ms_single * 1e3:.2f} us, {achieved / HBM_PEAK_GBS:.3f} of HBM peak, "
+            f"{ms_single * 1e3:.2f} us, {achieved / HBM_PEAK_GBS:.3f} of HBM peak "
+            f"(floor {floor['total'] / 1e6:.1f} MB: {floor_rate / HBM_PEAK_GBS:.3f}), "
             f"parity {parity}")
 
     if not args.no_rocsparse:
@@ -417,6 +429,39 @@ def main():
             if len(sp) == 4:
                 out[f"speedup_vs_rocsparse_fp32_geomean_1_4_{mode}"] = round(geomean(sp), 3)
     out["per_config"] = per
+    # The target in a few lines, last in the JSON line and in stderr (a reader of either tail
+    # finds it): per workload and mode, our single-launch median, rocSPARSE FP32's, the ratio,
+    # the HBM fraction, measured traffic and the schedule's floor over the algorithmic bytes.
+    summary = []
+    for p in per:
+        for mode in modes:
+            m = p[mode]
+            rf = m["roofline"]
+            row = {"w": f"{p['config']}:{p['precision']}", "mode": mode[:3],
+                   "us": round(m["single_launch_median_ms"] * 1e3, 2),
+                   "frac": rf["frac"], "floor/alg": round(rf["floor_bytes"] / p["bytes_alg"], 2),
+                   "traffic/alg": (round(rf["traffic"] / p["bytes_alg"], 2)
+                                   if rf["traffic"] else None)}
+            if "rocsparse" in p:
+                row["rs32_us"] = round(p["rocsparse"]["fp32"]["ms_median"] * 1e3, 2)
+                row["x"] = m["speedup_vs_rocsparse_fp32"]
+            summary.append(row)
+    out["summary"] = summary
+    for mode in modes:
+        k = f"speedup_vs_rocsparse_fp32_geomean_1_4_{mode}"
+        if k in out:
+            out[k] = out.pop(k)  # moved after per_config
+    log("[summary] workload:precision mode | ours us | rocSPARSE FP32 us | speedup | HBM frac "
+        "| traffic/alg | floor/alg  (single-launch medians)")
+    for row in summary:
+        log("[summary] {w} {mode} | {us} | {rs} | {x} | {frac} | {t} | {f}".format(
+            rs=row.get("rs32_us"), x=row.get("x"), t=row["traffic/alg"], f=row["floor/alg"],
+            **{k: row[k] for k in ("w", "mode", "us", "frac")}))
+    for mode in modes:
+        k = f"speedup_vs_rocsparse_fp32_geomean_1_4_{mode}"
+        if k in out:
+            log(f"[summary] geomean speedup vs rocSPARSE FP32, workloads 1-4 at their "
+                f"configured precision, {mode}: {out[k]}")
 
     if args.copy_probe_mib:
         # a plain copy of known size: reads and writes copy_probe_mib MiB once

@@ -207,6 +207,39 @@ int vcsrmc_set_fp32_row_steps(int mode);
  * only *length is set).  No counterpart in the reference. */
 int vcsrmc_get_row_map(vcsrmc_t h, int *row_of_position, long long capacity, long long *length);
 
+/* The work units of h's execution layout, for inspection: *num_units = their number and, when
+ * units is not NULL, units[4u .. 4u+3] = {p0, first, end, mask | flags} of unit u (host buffer
+ * of `capacity` ints, at least 4 * *num_units): the unit multiplies tiles (or, with flag bit 18,
+ * batches of FP32 row steps) first .. end - 1 of the 16-row panel at row-order positions
+ * p0 .. p0 + 15 (rows p0 + i, or row_of_position[p0 + i] of vcsrmc_get_row_map), bit i of the
+ * low 16 bits set when position p0 + i holds a row with nonzeros; flag bit 16: the panel is
+ * split into several units, which add into C through atomics; bit 17: this is its first unit.
+ * The first vcsrmc_info.num_heavy units are shared by the four waves of a work-group; light
+ * unit num_heavy + j runs on the XCD range x with xcd_start[x] <= j < xcd_start[x + 1]
+ * (xcd_start: 9 ints, may be NULL).  No counterpart in the reference. */
+int vcsrmc_get_units(vcsrmc_t h, int *units, long long capacity, long long *num_units,
+                     int *xcd_start);
+
+/* HBM bytes a launch of vcsrmc_spmm_ex with these arguments cannot avoid under its schedule,
+ * if each XCD's L2 kept everything its work-groups touched for the whole launch (a floor for
+ * measured traffic, not a prediction).  The launch deals row parts of the units to the XCDs of
+ * each O group; B counts, per part, every distinct column of its units once, at O values of
+ * the element type the kernel reads (binary16 where B is FP16 or converted first).  No
+ * counterpart in the reference. */
+typedef struct vcsrmc_traffic {
+    long long b_bytes;       /* B: sum over row parts of (distinct columns) x O x element size */
+    long long b_once_bytes;  /* B: every distinct column once for the whole GPU               */
+    long long a_bytes;       /* execution layout a launch reads, once per O tile              */
+    long long c_bytes;       /* C: non-empty rows x O x 4, x 2 when accumulating (read+write) */
+    long long convert_bytes; /* FP32 B rounded to binary16 in a pass first: 6 B per element   */
+    long long total;         /* b_bytes + a_bytes + c_bytes + convert_bytes                   */
+    int o_tile_width;        /* output columns per work-group the launch takes                */
+    int o_tiles;             /* ceil(O / o_tile_width)                                        */
+    int row_parts;           /* row parts per O group (8 XCDs / O groups)                     */
+} vcsrmc_traffic;
+int vcsrmc_traffic_floor(vcsrmc_t h, int b_dtype, int O, int tileK, int flags,
+                         vcsrmc_traffic *out, void *stream);
+
 /* Relabels the columns of a device CSR in place, col[p] = position[col[p]], with every row
  * re-sorted by its new columns (values follow), and, when d_B is non-NULL, writes
  * d_B_out[position[r], :] = d_B[r, :] (N x O floats, d_B_out distinct from d_B), so that

@@ -376,37 +376,100 @@ int orc_canonicalize(orc_format *f) {
  * ------------------------------------------------------------------------------------- */
 static inline double q16(float x) { return (double)orc_f16_to_f32(orc_f32_to_f16(x)); }
 
+/* One row of orc_spmm_csr: out[0..O) and the row's L1 norm of |a||b|.  Bq (mode 1) is B
+ * already rounded to binary16 elementwise, or NULL to round each b as it is read; both give
+ * the same doubles, q16 being a function of its argument. */
+static void spmm_row(const int *row_ptr, const int *col, const float *val, int r, const float *B,
+                     const float *Bq, int O, int mode, float inv, float scale, double *out,
+                     double *rowL1) {
+    for (int k = 0; k < O; ++k) out[k] = 0.0;
+    double l1 = 0.0;
+    for (int p = row_ptr[r]; p < row_ptr[r + 1]; ++p) {
+        if (mode == 0) {
+            const float *b = B + (size_t)col[p] * O;
+            const double a = (double)val[p];
+            for (int k = 0; k < O; ++k) {
+                const double t = a * (double)b[k];
+                out[k] += t;
+                l1 += fabs(t);
+            }
+        } else if (Bq) {
+            const float *b = Bq + (size_t)col[p] * O;
+            const double a = q16(val[p] * inv);
+            for (int k = 0; k < O; ++k) {
+                const double t = a * (double)b[k];
+                out[k] += t;
+                l1 += fabs(t);
+            }
+        } else {
+            const float *b = B + (size_t)col[p] * O;
+            const double a = q16(val[p] * inv);
+            for (int k = 0; k < O; ++k) {
+                const double t = a * q16(b[k]);
+                out[k] += t;
+                l1 += fabs(t);
+            }
+        }
+    }
+    if (mode != 0) {
+        for (int k = 0; k < O; ++k) out[k] *= (double)scale;
+        l1 *= (double)scale;
+    }
+    *rowL1 = l1;
+}
+
 void orc_spmm_csr(const int *row_ptr, const int *col, const float *val, int M, const float *B,
                   int O, int mode, float scale, double *R, double *rowL1) {
     const float inv = 1.0f / scale;
     for (int r = 0; r < M; ++r) {
-        double *out = R + (size_t)r * O;
-        for (int k = 0; k < O; ++k) out[k] = 0.0;
-        double l1 = 0.0;
-        for (int p = row_ptr[r]; p < row_ptr[r + 1]; ++p) {
-            const float *b = B + (size_t)col[p] * O;
-            if (mode == 0) {
-                const double a = (double)val[p];
-                for (int k = 0; k < O; ++k) {
-                    const double t = a * (double)b[k];
-                    out[k] += t;
-                    l1 += fabs(t);
-                }
-            } else {
-                const double a = q16(val[p] * inv);
-                for (int k = 0; k < O; ++k) {
-                    const double t = a * q16(b[k]);
-                    out[k] += t;
-                    l1 += fabs(t);
-                }
-            }
-        }
-        if (mode != 0) {
-            for (int k = 0; k < O; ++k) out[k] *= (double)scale;
-            l1 *= (double)scale;
-        }
+        double l1;
+        spmm_row(row_ptr, col, val, r, B, NULL, O, mode, inv, scale, R + (size_t)r * O, &l1);
         if (rowL1) rowL1[r] = l1;
     }
+}
+
+int orc_spmm_check(const int *row_ptr, const int *col, const float *val, int M, const float *B,
+                   long long nb, int O, int mode, float scale, const float *C, const float *C0,
+                   int threads, double *err, double *bound) {
+    const float inv = 1.0f / scale;
+    float *Bq = NULL;
+    if (mode != 0) {
+        Bq = (float *)malloc(sizeof(float) * (size_t)(nb > 0 ? nb : 1));
+        if (!Bq) return ORC_NOMEM;
+#pragma omp parallel for schedule(static) num_threads(threads)
+        for (long long i = 0; i < nb; ++i) Bq[i] = (float)q16(B[i]);
+    }
+    int status = ORC_OK;
+#pragma omp parallel num_threads(threads)
+    {
+        double *out = (double *)malloc(sizeof(double) * (size_t)(O > 0 ? O : 1));
+        if (!out) {
+#pragma omp atomic write
+            status = ORC_NOMEM;
+        }
+#pragma omp for schedule(dynamic, 256)
+        for (int r = 0; r < M; ++r) {
+            if (!out) continue;
+            double l1;
+            spmm_row(row_ptr, col, val, r, B, Bq, O, mode, inv, scale, out, &l1);
+            const float *c = C + (size_t)r * O;
+            const float *c0 = C0 ? C0 + (size_t)r * O : NULL;
+            double e = 0.0, n0 = 0.0;
+            for (int k = 0; k < O; ++k) {
+                double want = out[k];
+                if (c0) {
+                    want += (double)c0[k];
+                    n0 += fabs((double)c0[k]);
+                }
+                e += fabs((double)c[k] - want);
+            }
+            err[r] = e;
+            bound[r] = l1 + n0;
+        }
+        free(out);
+    }
+    free(Bq);
+    return status;
 }
 
 void orc_spmm_format(const orc_format *f, const float *B, int O, double *R) {

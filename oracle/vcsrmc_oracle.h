@@ -19,6 +19,8 @@
  *                         canonical tie order
  *   orc_spmm_csr          src/main.cpp:202-207 (r -> p -> k, double accumulation),
  *                         with the FP16 input model of src/vcsr_mc.cu:195-196, 213, 234
+ *   orc_spmm_check        orc_spmm_csr row by row against a given C (the parity norm's
+ *                         terms for every row, OpenMP over rows)
  *   orc_spmm_format       C = A.B read back from the format arrays
  *                         (the semantics of the kernels src/vcsr_mc.cu:144-329)
  *
@@ -33,6 +35,9 @@
  *     seg_base + lcol = col, depth = max count, items partition the groups).
  *   - orc_spmm_csr: a dense numpy matmul in float64 of the same quantised inputs.
  *   - orc_spmm_format: equals orc_spmm_csr on the same matrix.
+ *   - orc_spmm_check: its err and bound equal |C - R| and rowL1 of orc_spmm_csr, bit for bit,
+ *     in both modes, with and without C0, at 1 and several threads; a planted error in one
+ *     element of C shows up in that row only.
  */
 #ifndef VCSRMC_ORACLE_H
 #define VCSRMC_ORACLE_H
@@ -76,6 +81,15 @@ int orc_canonicalize(orc_format *f);
 void orc_spmm_csr(const int *row_ptr, const int *col, const float *val, int M, const float *B,
                   int O, int mode, float scale, double *R, double *rowL1);
 void orc_spmm_format(const orc_format *f, const float *B, int O, double *R);
+/* The parity check of a whole product, rows split over `threads` OpenMP threads, without an
+ * M x O result buffer: for every row r, the row of orc_spmm_csr (same arithmetic, so the same
+ * doubles), then err[r] = sum_k |C[r,k] - (R[r,k] + C0[r,k])| and bound[r] = rowL1[r] +
+ * sum_k |C0[r,k]| (C0 = C's values before a C += A.B launch; NULL = zero).  nb = the number of
+ * B elements (mode 1 rounds B to binary16 once, in a buffer of that size).  Returns ORC_OK or
+ * ORC_NOMEM. */
+int orc_spmm_check(const int *row_ptr, const int *col, const float *val, int M, const float *B,
+                   long long nb, int O, int mode, float scale, const float *C, const float *C0,
+                   int threads, double *err, double *bound);
 
 /* The reference's CPU SpMM exactly as the driver runs it (main.cpp:202-207): plain FP32
  * inputs, double accumulation, r -> p -> k.  R must be zeroed by the caller (+=). */

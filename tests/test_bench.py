@@ -59,7 +59,16 @@ def test_bench_json_line():
         assert abs(m["roofline"]["achieved"] - p["bytes_alg"] / m["kernel_ms"] / 1e6) < \
             1e-3 * m["roofline"]["achieved"] + 0.1
         assert m["speedup_vs_rocsparse_fp32"] > 0
+        rf = m["roofline"]
+        # the schedule's floor holds at least C and every distinct B row once
+        assert rf["floor_bytes"] >= rf["floor"]["c_bytes"] + rf["floor"]["b_once_bytes"] > 0
+        assert rf["frac_ceiling"] == round(p["bytes_alg"] / rf["floor_bytes"], 4)
     assert d["value"] == p["accumulate"]["gflops"]
+    # the summary closes both the JSON line and stderr, where a kept tail of either holds it
+    keys = list(d)
+    assert keys.index("summary") > keys.index("per_config")
+    assert [r["mode"] for r in d["summary"]] == ["acc", "ove"]
+    assert r.stderr.rstrip().splitlines()[-1].startswith("[summary]")
 
 
 def test_traffic_stamp_matches_sources():

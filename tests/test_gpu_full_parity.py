@@ -1,0 +1,103 @@
+"""Every row of C against the oracle at the five workloads' full benchmark sizes.
+
+For each workload (uniform 4096^2, power-law 36,692^2, 27-point stencil 100^3, 32 x 32 blocks
+262,144^2 at O = 256, R-MAT scale 22), in the precision it is configured for and in the other
+one (the reference's driver runs both kernels on every matrix, src/main.cpp:345), in both launch
+modes (C += A.B from C = 0, and C = A.B over a C holding 9.0), every row of C is checked with the
+parity norm, per row r:
+    ||C[r,:] - C_ref[r,:]||_1 <= tau * sum_k sum_p |a_rp b_{c_p,k}|,
+tau = 1e-5 for FP32 inputs and 2e-3 for FP16 inputs, C_ref the oracle's double-precision product
+of the same operands (FP16-quantised for vcsr_mc) -- the reference's own check covers every
+element of C (src/main.cpp:257-291).  Rows without nonzeros must keep C's value.  The checked
+set is asserted to hold every row of a split panel (merged through float atomics) and the 100
+rows of highest degree, where the sums are longest."""
+import numpy as np
+import pytest
+
+import vcsr_mc_amd as vm
+from gpu_util import dev, say
+
+pytestmark = pytest.mark.gpu
+
+TAU = {True: 1e-5, False: 2e-3}
+SPLIT = 1 << 16
+
+_cache = {}
+
+
+def workload(config):
+    """The full-size workload, generated once and kept while the next test uses it."""
+    if config not in _cache:
+        _cache.clear()
+        _cache[config] = vm.generate(config, 0)
+    return _cache[config]
+
+
+def split_rows(f):
+    units, _ = f.units()
+    sel = units[(units[:, 3] & SPLIT) != 0]
+    rows = f.rows_of_units(sel)
+    return np.unique(np.concatenate(rows)) if rows else np.zeros(0, np.int64)
+
+
+@pytest.mark.parametrize("config", [1, 2, 3, 4, 5])
+@pytest.mark.parametrize("second", [False, True])
+def test_every_row_full_size(orc, config, second):
+    import torch
+    w = vm.WORKLOADS[config]
+    configured_fp32 = w["precision"] == "fp32"
+    fp32 = configured_fp32 != second
+    A = workload(config)
+    O = w["O"]
+    if second:
+        # the other kernel of the reference's driver, fed FP32 B as run_vcsr_mc_spmm_gpu is
+        B = vm.dense(A.N, O, seed=vm.SEED_BASE + 200 + config)
+        b16 = False
+    else:
+        B = vm.dense(A.N, O, seed=vm.SEED_BASE + 100 + config, fp16_exact=not fp32)
+        b16 = not fp32
+    deg = np.diff(A.row_ptr)
+    nonempty = deg > 0
+    say("full-C parity", config, "fp32" if fp32 else "fp16", "second" if second else "configured",
+        A.M, A.nnz, O)
+    mode = 0 if fp32 else 1
+    with vm.DeviceFormat.from_device_csr(dev(A.row_ptr), dev(A.col), dev(A.val), A.M, A.N,
+                                         fp32, 32) as f:
+        info = f.info()
+        scale = info["scale"]
+        srows = split_rows(f)
+        assert srows.size == 0 or info["num_split_panels"] > 0
+        dB = dev(B).half() if b16 else dev(B)
+        results = {}
+        for overwrite in (False, True):
+            fill = 9.0 if overwrite else 0.0
+            C = torch.full((A.M, O), fill, dtype=torch.float32, device="cuda")
+            f.spmm(dB, C, tileK=128, overwrite=overwrite)
+            torch.cuda.synchronize()
+            Ch = C.cpu().numpy()
+            del C
+            assert np.all(Ch[~nonempty] == fill)
+            err, bound = orc.spmm_check(A.row_ptr, A.col, A.val, A.M, B, Ch, mode=mode,
+                                        scale=scale)
+            del Ch
+            ratio = err[nonempty] / (TAU[fp32] * bound[nonempty] + 1e-30)
+            results[overwrite] = (err, bound)
+            worst = int(np.argmax(ratio)) if ratio.size else -1
+            bad = int(np.count_nonzero(ratio > 1.0))
+            assert bad == 0, (f"overwrite={overwrite}: {bad} rows over the bound, worst row "
+                              f"{np.nonzero(nonempty)[0][worst]} at {ratio[worst]:.3g}")
+    # the compared set: every non-empty row, which holds the split panels' rows and the hubs
+    checked = np.zeros(A.M, bool)
+    checked[nonempty] = True
+    hubs = np.argsort(deg, kind="stable")[-100:]
+    assert checked[hubs].all()
+    assert srows.size == 0 or checked[srows].all()
+    if config == 5:
+        # R-MAT's hub rows span several work-groups: the atomic merge is exercised here
+        assert info["num_split_panels"] > 0 and srows.size > 0
+    for overwrite, (err, bound) in results.items():
+        for name, rows in (("hub", hubs), ("split", srows)):
+            if rows.size:
+                r = err[rows] / (TAU[fp32] * bound[rows] + 1e-30)
+                print(f"  overwrite={overwrite} {name} rows: {rows.size}, worst error / bound "
+                      f"{r.max():.3g}", flush=True)

@@ -255,3 +255,32 @@ def test_cpu_baseline_loop_matches_dense(orc, rng):
     np.testing.assert_allclose(R, _dense(rp, c, v, 40, 30) @ B.astype(np.float64), atol=1e-12)
     R2 = orc.cpu_spmm_f64(rp, c, v, B, threads=4)
     assert R2.tobytes() == R.tobytes()
+
+
+@pytest.mark.parametrize("mode", [0, 1])
+@pytest.mark.parametrize("with_c0", [False, True])
+def test_spmm_check_equals_spmm_csr(orc, rng, mode, with_c0):
+    """The whole-matrix check gives, per row, exactly |C - (R + C0)|_1 and rowL1 + |C0|_1 of
+    spmm_csr (the same arithmetic, row by row), at one and at several threads; a planted error
+    in one element of C moves that row's error and no other."""
+    rp, c, v = random_csr(rng, 300, 200, density=0.05, empty_frac=0.2, mag=1e5 if mode else 1)
+    B = rng.uniform(-2, 2, (200, 19)).astype(np.float32)  # not binary16-exact: mode 1 rounds it
+    s = float(orc.half_scale(v)) if mode else 1.0
+    R, L1 = orc.spmm_csr(rp, c, v, 300, B, mode=mode, scale=s)
+    C0 = rng.uniform(-1, 1, R.shape).astype(np.float32) if with_c0 else None
+    want = R + (C0.astype(np.float64) if with_c0 else 0.0)
+    C = (want + rng.normal(0, 1e-3, R.shape)).astype(np.float32)
+    # sums in index order, as the check forms them (numpy's sum is pairwise)
+    err_want = np.cumsum(np.abs(C.astype(np.float64) - want), axis=1)[:, -1]
+    bound_want = L1 + (np.cumsum(np.abs(C0.astype(np.float64)), axis=1)[:, -1] if with_c0
+                       else 0.0)
+    for threads in (1, 5):
+        err, bound = orc.spmm_check(rp, c, v, 300, B, C, mode=mode, scale=s, C0=C0,
+                                    threads=threads)
+        assert err.tobytes() == err_want.tobytes()
+        assert bound.tobytes() == bound_want.tobytes()
+    C2 = C.copy()
+    C2[17, 3] += 0.5
+    err2, _ = orc.spmm_check(rp, c, v, 300, B, C2, mode=mode, scale=s, C0=C0, threads=3)
+    moved = np.nonzero(err2 != err)[0]
+    assert moved.tolist() == [17] and err2[17] > err[17] + 0.49

@@ -53,6 +53,14 @@ class _Info(C.Structure):
     ]
 
 
+class _Traffic(C.Structure):
+    _fields_ = [
+        ("b_bytes", C.c_longlong), ("b_once_bytes", C.c_longlong), ("a_bytes", C.c_longlong),
+        ("c_bytes", C.c_longlong), ("convert_bytes", C.c_longlong), ("total", C.c_longlong),
+        ("o_tile_width", C.c_int), ("o_tiles", C.c_int), ("row_parts", C.c_int),
+    ]
+
+
 _lib_handle = None
 _bench_handle = None
 
@@ -94,6 +102,9 @@ def lib():
         L.vcsrmc_get_row_map.argtypes = [vp, vp, C.c_longlong, C.POINTER(C.c_longlong)]
         L.vcsrmc_apply_column_permutation.argtypes = [vp, vp, vp, C.c_int, C.c_int, C.c_int, vp,
                                                       vp, C.c_int, vp, vp]
+        L.vcsrmc_get_units.argtypes = [vp, vp, C.c_longlong, C.POINTER(C.c_longlong), vp]
+        L.vcsrmc_traffic_floor.argtypes = [vp, C.c_int, C.c_int, C.c_int, C.c_int,
+                                           C.POINTER(_Traffic), vp]
         L.vcsrmc_status_string.restype = C.c_char_p
         L.vcsrmc_status_string.argtypes = [C.c_int]
         L.vcsrmc_last_error.restype = C.c_char_p
@@ -101,7 +112,8 @@ def lib():
                   "vcsrmc_upload", "vcsrmc_get_info", "vcsrmc_download", "vcsrmc_spmm",
                   "vcsrmc_spmm_ex", "vcsrmc_spmm_noalloc", "vcsrmc_rcm_order",
                   "vcsrmc_set_rcm_limits", "vcsrmc_set_row_grouping", "vcsrmc_get_row_map",
-                  "vcsrmc_apply_column_permutation", "vcsrmc_set_fp32_row_steps"):
+                  "vcsrmc_apply_column_permutation", "vcsrmc_set_fp32_row_steps",
+                  "vcsrmc_get_units", "vcsrmc_traffic_floor"):
             getattr(L, f).restype = C.c_int
         _lib_handle = L
     return _lib_handle
@@ -299,6 +311,40 @@ class DeviceFormat:
         _check(lib().vcsrmc_get_row_map(self.handle, out.ctypes.data, out.size, C.byref(n)),
                "vcsrmc_get_row_map")
         return out
+
+    def units(self):
+        """The execution layout's work units: (units, xcd_start), units an int32 array of shape
+        (num_units, 4) = {first row-order position, first tile, end tile, row mask | flags}
+        (flags: 1 << 16 split panel, 1 << 17 its first unit, 1 << 18 FP32 row steps), and
+        xcd_start (9 ints) the light units' XCD ranges."""
+        n = C.c_longlong(0)
+        xs = np.zeros(9, np.int32)
+        _check(lib().vcsrmc_get_units(self.handle, None, 0, C.byref(n), xs.ctypes.data),
+               "vcsrmc_get_units")
+        out = np.zeros((n.value, 4), np.int32)
+        if n.value:
+            _check(lib().vcsrmc_get_units(self.handle, out.ctypes.data, out.size, C.byref(n),
+                                          None), "vcsrmc_get_units")
+        return out, xs
+
+    def rows_of_units(self, units):
+        """The C rows each unit writes, as a list of int arrays (row map applied)."""
+        rmap = self.row_map()
+        out = []
+        for p0, _, _, w in units:
+            pos = p0 + np.nonzero((int(w) >> np.arange(16)) & 1)[0]
+            out.append(rmap[pos] if rmap is not None else pos)
+        return out
+
+    def traffic_floor(self, O, tileK=128, b_f16=False, overwrite=False, stream=None) -> dict:
+        """HBM bytes a launch with these arguments cannot avoid under its schedule (see
+        vcsrmc_traffic_floor in include/vcsrmc.h)."""
+        t = _Traffic()
+        _check(lib().vcsrmc_traffic_floor(self.handle, B_F16 if b_f16 else B_F32, int(O),
+                                          int(tileK), SPMM_OVERWRITE if overwrite else 0,
+                                          C.byref(t), _stream_ptr(stream)),
+               "vcsrmc_traffic_floor")
+        return {k: getattr(t, k) for k, _ in _Traffic._fields_}
 
     def download(self) -> VCSRMC:
         i = self.info()

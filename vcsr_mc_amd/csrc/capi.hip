@@ -227,6 +227,45 @@ int vcsrmc_get_row_map(vcsrmc_t h, int* row_of_position, long long capacity, lon
     });
 }
 
+int vcsrmc_get_units(vcsrmc_t h, int* units, long long capacity, long long* num_units,
+                     int* xcd_start) {
+    return guarded([&] {
+        need(h != nullptr && num_units != nullptr, "null argument");
+        if (!h->F.ready) throw vcsrmc::Error(VCSRMC_ERR_STATE, "no format in this handle");
+        const auto& F = h->F;
+        *num_units = F.num_units;
+        if (xcd_start)
+            for (int x = 0; x < 9; ++x) xcd_start[x] = F.xcd_start[x];
+        if (units == nullptr || F.num_units == 0) return;
+        need(capacity >= 4LL * F.num_units, "units buffer smaller than 4 ints per unit");
+        DeviceScope ds(h->device);
+        VCSRMC_HIP(hipMemcpy(units, F.units.p, sizeof(int4) * (size_t)F.num_units,
+                             hipMemcpyDeviceToHost));
+    });
+}
+
+int vcsrmc_traffic_floor(vcsrmc_t h, int b_dtype, int O, int tileK, int flags,
+                         vcsrmc_traffic* out, void* stream) {
+    return guarded([&] {
+        need(h != nullptr && out != nullptr, "null argument");
+        need(b_dtype == VCSRMC_B_F32 || b_dtype == VCSRMC_B_F16, "unknown B dtype");
+        need((flags & ~VCSRMC_SPMM_OVERWRITE) == 0, "unknown flag");
+        DeviceScope ds(h->device);
+        const vcsrmc::TrafficFloor t =
+            vcsrmc::traffic_floor(h->F, b_dtype == VCSRMC_B_F16, O, tileK,
+                                  !(flags & VCSRMC_SPMM_OVERWRITE), (hipStream_t)stream);
+        out->b_bytes = t.b_bytes;
+        out->b_once_bytes = t.b_once_bytes;
+        out->a_bytes = t.a_bytes;
+        out->c_bytes = t.c_bytes;
+        out->convert_bytes = t.convert_bytes;
+        out->total = t.total;
+        out->o_tile_width = t.o_tile_width;
+        out->o_tiles = t.o_tiles;
+        out->row_parts = t.row_parts;
+    });
+}
+
 int vcsrmc_download(vcsrmc_t h, int* group_ptr, int* group_depth, int* group_seg_base,
                     int* group_rows, int* lcol, float* val, int* item_gbeg, int* item_gend) {
     return guarded([&] {

@@ -155,6 +155,12 @@ void gen_uniform(vcsrmc_matrix_s& A, int n, uint64_t seed) {
     fill_values(A, seed, 0, false);
 }
 
+// Power-law graph: degrees Zipf(2.1) on [1, 1383], paired by the configuration model
+// (shuffled stubs), self-loops and repeated pairs dropped, pattern symmetric.  The degree scale
+// is calibrated so that the matrix holds about 368,000 * n / 36,692 nonzeros after the drops:
+// the stub total aimed at is corrected by the ratio of the nonzeros it gave, a few times, and
+// the closest matrix is kept (every attempt pairs with the same shuffle stream, so the result
+// depends on the seed only).
 void gen_powerlaw(vcsrmc_matrix_s& A, int n, uint64_t seed) {
     Engine e = block_engine(seed, 2, 0);
     const int dmax = 1383;
@@ -168,33 +174,51 @@ void gen_powerlaw(vcsrmc_matrix_s& A, int n, uint64_t seed) {
         z[i] = (int)(std::upper_bound(cdf.begin(), cdf.end(), u) - cdf.begin()) + 1;
         if (z[i] > dmax) z[i] = dmax;
     }
-    const double target = 368000.0 * (double)n / 36692.0;
-    auto total = [&](double s) {
-        long long t = 0;
-        for (int i = 0; i < n; ++i)
-            t += std::min<long long>(std::max<long long>(std::llround(s * z[i]), 1), dmax);
-        return t;
+    const Engine pairing = e;  // shuffle stream shared by every attempt
+    const double goal = 368000.0 * (double)n / 36692.0;
+    auto degree = [&](double s, int i) {
+        return std::min<long long>(std::max<long long>(std::llround(s * z[i]), 1), dmax);
     };
-    double lo = 0.0, hi = 1000.0;
-    for (int it = 0; it < 100; ++it) {
-        const double mid = 0.5 * (lo + hi);
-        if (total(mid) < target) lo = mid; else hi = mid;
+    // Degree scale whose stub total first reaches `target` (bisection on a monotone sum).
+    auto scale_for = [&](double target) {
+        double lo = 0.0, hi = 1000.0;
+        for (int it = 0; it < 100; ++it) {
+            const double mid = 0.5 * (lo + hi);
+            long long t = 0;
+            for (int i = 0; i < n; ++i) t += degree(mid, i);
+            if (t < target) lo = mid; else hi = mid;
+        }
+        return hi;
+    };
+    auto attempt = [&](double s, vcsrmc_matrix_s& out) {
+        Engine sh = pairing;
+        std::vector<int> stubs;
+        for (int i = 0; i < n; ++i)
+            for (long long j = degree(s, i); j > 0; --j) stubs.push_back(i);
+        if (stubs.size() & 1) stubs.pop_back();
+        for (size_t i = stubs.size(); i > 1; --i) std::swap(stubs[i - 1], stubs[uniform_int(sh, i)]);
+        std::vector<int> r, c;
+        for (size_t i = 0; i + 1 < stubs.size(); i += 2) {
+            const int u = stubs[i], v = stubs[i + 1];
+            if (u == v) continue;
+            r.push_back(u); c.push_back(v);
+            r.push_back(v); c.push_back(u);
+        }
+        csr_from_pairs(out, n, n, r, c);
+        return (double)out.col.size();
+    };
+    double target = goal, best_gap = -1.0;
+    for (int it = 0; it < 4; ++it) {
+        vcsrmc_matrix_s T;
+        const double got = attempt(scale_for(target), T);
+        const double gap = std::fabs(got - goal);
+        if (best_gap < 0.0 || gap < best_gap) {
+            best_gap = gap;
+            A = std::move(T);
+        }
+        if (got <= 0.0 || gap <= 1e-3 * goal) break;
+        target *= goal / got;
     }
-    std::vector<int> stubs;
-    for (int i = 0; i < n; ++i) {
-        const long long d = std::min<long long>(std::max<long long>(std::llround(hi * z[i]), 1), dmax);
-        for (long long j = 0; j < d; ++j) stubs.push_back(i);
-    }
-    if (stubs.size() & 1) stubs.pop_back();
-    for (size_t i = stubs.size(); i > 1; --i) std::swap(stubs[i - 1], stubs[uniform_int(e, i)]);
-    std::vector<int> r, c;
-    for (size_t i = 0; i + 1 < stubs.size(); i += 2) {
-        const int u = stubs[i], v = stubs[i + 1];
-        if (u == v) continue;
-        r.push_back(u); c.push_back(v);
-        r.push_back(v); c.push_back(u);
-    }
-    csr_from_pairs(A, n, n, r, c);
     fill_values(A, seed, 0, true);
 }
 

@@ -207,6 +207,19 @@ SpmmPlan plan_spmm(const DeviceFormat& F, const void* dB, bool b_f16, int O, int
                    bool accumulate, HalfScratch ext = HalfScratch());
 void run_spmm(const SpmmPlan& p, hipStream_t st);
 
+// The HBM bytes a launch cannot avoid under its schedule, if every XCD's L2 kept everything its
+// work-groups touched for the whole launch: B, the distinct columns of each XCD row part's
+// units, once per part; the execution layout each O tile reads; C written once per non-empty
+// row (and read first when accumulating); the FP32-to-binary16 pass over B where the launch
+// makes one (6 bytes per element).  The launch's own decisions for a 16-byte aligned B.
+struct TrafficFloor {
+    long long b_bytes = 0, b_once_bytes = 0, a_bytes = 0, c_bytes = 0, convert_bytes = 0,
+              total = 0;
+    int o_tile_width = 0, o_tiles = 0, row_parts = 0;
+};
+TrafficFloor traffic_floor(const DeviceFormat& F, bool b_f16, int O, int tileK, bool accumulate,
+                           hipStream_t st);
+
 // Reverse Cuthill-McKee order of the columns of a device CSR (include/reorder.hpp:17-77):
 // position[old column] = new column.  Synchronises `st`.
 void rcm_order_device(const int* rp, const int* col, int M, int N, int nnz, int* position,

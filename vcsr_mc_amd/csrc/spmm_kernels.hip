@@ -34,6 +34,8 @@
 // Epilogue: lane (n, g) holds rows 4g..4g+3 at output columns k0 + VEC n .. + VEC-1, so each
 // row is written as VEC contiguous floats per lane, 16 lanes per row: coalesced.  Rows that
 // A does not touch are not written (the reference never touches them either).
+#include <vector>
+
 #include "../../include/vcsrmc.h"
 #include "internal.hpp"
 
@@ -994,6 +996,28 @@ static int o_tile_width(const DeviceFormat& F, bool b_f16, int O, int tileK) {
     return tk;
 }
 
+// FP16 format, FP32 B: the kernel rounds each gathered FP32 B row to binary16 as it loads it.
+// Converting B once instead costs 6 bytes per element and a pass before the multiply, and saves
+// 2 bytes per element on each gather from beyond the caches, so it pays only for B rows used
+// many times (12 or more on average) that come from beyond the caches: B above 12 MB (three
+// times one XCD's 4 MB L2, which each XCD fills with its own copies) with tiles of few nonzeros
+// (< 48 on average: about one gathered row per nonzero), or B above the 256 MB last-level cache.
+// Measured on gfx950 (reference protocol, 24 synthetic matrices and the benchmark workloads),
+// direct -> converted: uniform random 100,000^2 with 16 per row 118 -> 83 us, 50,000^2 with 32
+// per row 107 -> 62, power-law 30,000^2 with 20 per row 37 -> 31, 27-point stencil 100^3
+// 572 -> 534; kept direct, where converting measured slower: 5-point grids 500^2 / 700^2
+// 75 / 171 us (105 / 208 converted), 7-point 60^3 61 (88), 27-point 60^3 94 (117), uniform
+// 300,000^2 with 3 per row 113 (129), uniform 4096^2 8.0 (11.9), power-law 36,692^2 24.9
+// (25.7), R-MAT scale 17 51 (55).  Missed by the rule: R-MAT scale 15 (converted, 23 -> 26 us)
+// and power-law 200,000^2 with 6 per row (direct, 98 against 92).  Same values either way:
+// both round to nearest even.
+static bool converts_b(const DeviceFormat& F, bool b_f16, bool b_aligned, int O) {
+    const long long b32_bytes = (long long)F.N * O * 4;
+    return !F.fp32 && !b_f16 && b_aligned && F.num_chunks > 0 && F.nnz >= 12LL * F.N &&
+           ((F.nnz < (long long)kSparseTileNnz * F.num_chunks && b32_bytes > (12LL << 20)) ||
+            b32_bytes > (256LL << 20));
+}
+
 SpmmPlan plan_spmm(const DeviceFormat& F, const void* dB, bool b_f16, int O, int tileK,
                    float* dC, bool accumulate, HalfScratch ext) {
     if (tileK != 16 && tileK != 32 && tileK != 64 && tileK != 128)
@@ -1010,26 +1034,7 @@ SpmmPlan plan_spmm(const DeviceFormat& F, const void* dB, bool b_f16, int O, int
     p.O = O;
     p.dC = dC;
     p.accumulate = accumulate;
-    // FP16 format, FP32 B: the kernel rounds each gathered FP32 B row to binary16 as it loads
-    // it.  Converting B once instead costs 6 bytes per element and a pass before the multiply,
-    // and saves 2 bytes per element on each gather from beyond the caches, so it pays only for
-    // B rows used many times (12 or more on average) that come from beyond the caches: B above
-    // 12 MB (three times one XCD's 4 MB L2, which each XCD fills with its own copies) with
-    // tiles of few nonzeros (< 48 on average: about one gathered row per nonzero), or B above
-    // the 256 MB last-level cache.  Measured on gfx950 (reference protocol, 24 synthetic
-    // matrices and the benchmark workloads), direct -> converted: uniform random 100,000^2 with
-    // 16 per row 118 -> 83 us, 50,000^2 with 32 per row 107 -> 62, power-law 30,000^2 with 20
-    // per row 37 -> 31, 27-point stencil 100^3 572 -> 534; kept direct, where converting measured
-    // slower: 5-point grids 500^2 / 700^2 75 / 171 us (105 / 208 converted), 7-point 60^3 61
-    // (88), 27-point 60^3 94 (117), uniform 300,000^2 with 3 per row 113 (129), uniform 4096^2
-    // 8.0 (11.9), power-law 36,692^2 24.9 (25.7), R-MAT scale 17 51 (55).  Missed by the rule:
-    // R-MAT scale 15 (converted, 23 -> 26 us) and power-law 200,000^2 with 6 per row (direct,
-    // 98 against 92).  Same values either way: both round to nearest even.
-    const long long b32_bytes = (long long)F.N * O * 4;
-    if (!F.fp32 && !b_f16 && ((uintptr_t)dB % 16) == 0 && F.num_chunks > 0 &&
-        F.nnz >= 12LL * F.N &&
-        ((F.nnz < (long long)kSparseTileNnz * F.num_chunks && b32_bytes > (12LL << 20)) ||
-         b32_bytes > (256LL << 20))) {
+    if (converts_b(F, b_f16, ((uintptr_t)dB % 16) == 0, O)) {
         const long long n = (long long)F.N * O;
         _Float16* half = ext.p;
         if (half) {
@@ -1078,6 +1083,123 @@ void run_spmm(const SpmmPlan& p, hipStream_t st) {
 void spmm_launch(const DeviceFormat& F, const void* dB, bool b_f16, int O, int tileK, float* dC,
                  bool accumulate, hipStream_t st, HalfScratch ext) {
     run_spmm(plan_spmm(F, dB, b_f16, O, tileK, dC, accumulate, ext), st);
+}
+
+// ---- traffic floor of a launch ------------------------------------------------------------
+// The row part (of the XCDs of one O group) that runs unit u, as `schedule` deals the units:
+// heavy unit u to part u mod parts, light units by the ranges of xcd_start.
+__device__ __forceinline__ int unit_part(int u, int num_heavy, const XcdSplit& xs) {
+    const int parts = 1 << xs.lgp;
+    if (u < num_heavy) return u & (parts - 1);
+    const int j = u - num_heavy, G = 8 >> xs.lgp;
+    int r = 0;
+    while (r + 1 < parts && j >= xs.start[(r + 1) * G]) ++r;
+    return r;
+}
+
+// One wave per unit: marks mark[part * N + column] for every column of the unit's tiles (or
+// row-step batches) -- plain byte stores, every writer stores 1 -- and writes the bytes of the
+// execution layout the unit reads once per O tile (unit 16 B, its row map 64 B; per tile the
+// two entry offsets and the dense index 8 B, the column list 128 B, and the dense copy or the
+// entries; per row-step batch its columns 128 B and the 512 B of values its lanes read) and the
+// rows it writes (a split panel counted at its first unit).
+__global__ __launch_bounds__(256) void k_floor_units(
+    const int4* __restrict__ units, int num_units, int num_heavy, XcdSplit xs,
+    const int* __restrict__ chunk_eptr, const int* __restrict__ chunk_cols,
+    const int* __restrict__ chunk_dense, const int* __restrict__ rs_cols, int N, int fp32,
+    int mapped, unsigned char* __restrict__ mark, long long* __restrict__ a_bytes,
+    int* __restrict__ rows) {
+    const int u = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (u >= num_units) return;
+    const int lane = threadIdx.x & 63;
+    const int4 U = units[u];
+    unsigned char* m = mark + (long long)unit_part(u, num_heavy, xs) * N;
+    const bool rs = U.w & kUnitRowSteps;
+    const int* cols = rs ? rs_cols : chunk_cols;
+    long long bytes = 16 + (mapped ? 64 : 0);
+    for (int t = U.y; t < U.z; ++t) {
+        if (lane < kChunkCols) {
+            const int c = cols[(long long)kChunkCols * t + lane];
+            if (c >= 0) m[c] = 1;
+        }
+        if (rs) {
+            bytes += 128 + 512;
+        } else {
+            const int d = chunk_dense[t];
+            bytes += 8 + 128 +
+                     (d >= 0 ? 512LL * (fp32 ? 4 : 2)
+                             : (long long)(chunk_eptr[t + 1] - chunk_eptr[t]) * (fp32 ? 8 : 4));
+        }
+    }
+    if (lane == 0) {
+        a_bytes[u] = bytes;
+        const bool first = !(U.w & kUnitSplit) || (U.w & kUnitSplitFirst);
+        rows[u] = first ? __popc(U.w & 0xffff) : 0;
+    }
+}
+
+TrafficFloor traffic_floor(const DeviceFormat& F, bool b_f16, int O, int tileK, bool accumulate,
+                           hipStream_t st) {
+    if (tileK != 16 && tileK != 32 && tileK != 64 && tileK != 128)
+        throw Error(VCSRMC_ERR_TILEK, "vcsr_mc supports tileK in {16, 32, 64, 128}");
+    if (!F.ready) throw Error(VCSRMC_ERR_STATE, "no format in this handle");
+    if (O < 0) throw Error(VCSRMC_ERR_ARG, "O must be >= 0");
+    if (F.fp32 && b_f16) throw Error(VCSRMC_ERR_ARG, "an FP32 format takes an FP32 B");
+    TrafficFloor t;
+    if (F.num_units == 0 || O == 0) return t;
+    // the launch's decisions for a 16-byte aligned B (plan_spmm)
+    const bool convert = converts_b(F, b_f16, true, O);
+    const bool bh = b_f16 || convert;
+    t.o_tile_width = o_tile_width(F, bh, O, tileK);
+    t.o_tiles = (O + t.o_tile_width - 1) / t.o_tile_width;
+    int G = 8;
+    while (t.o_tiles % G) G >>= 1;
+    XcdSplit xs;
+    xs.lgp = G == 8 ? 0 : G == 4 ? 1 : G == 2 ? 2 : 3;
+    for (int x = 0; x < 9; ++x) xs.start[x] = F.xcd_start[x];
+    t.row_parts = 1 << xs.lgp;
+    const int parts = t.row_parts;
+    DevBuf<unsigned char> mark((size_t)parts * F.N);
+    DevBuf<long long> a_bytes((size_t)F.num_units);
+    DevBuf<int> rows((size_t)F.num_units);
+    VCSRMC_HIP(hipMemsetAsync(mark.p, 0, mark.n, st));
+    hipLaunchKernelGGL(k_floor_units, dim3(grid_for(F.num_units, 4)), dim3(256), 0, st, F.units.p,
+                       F.num_units, F.num_heavy, xs, F.chunk_eptr.p, F.chunk_cols.p,
+                       F.chunk_dense.p, F.rs_cols.p, F.N, F.fp32, F.row_map.n > 0 ? 1 : 0,
+                       mark.p, a_bytes.p, rows.p);
+    VCSRMC_HIP(hipGetLastError());
+    std::vector<unsigned char> hm(mark.n);
+    std::vector<long long> ha((size_t)F.num_units);
+    std::vector<int> hr((size_t)F.num_units);
+    VCSRMC_HIP(hipMemcpyAsync(hm.data(), mark.p, mark.n, hipMemcpyDeviceToHost, st));
+    VCSRMC_HIP(hipMemcpyAsync(ha.data(), a_bytes.p, sizeof(long long) * ha.size(),
+                              hipMemcpyDeviceToHost, st));
+    VCSRMC_HIP(hipMemcpyAsync(hr.data(), rows.p, sizeof(int) * hr.size(), hipMemcpyDeviceToHost,
+                              st));
+    VCSRMC_HIP(hipStreamSynchronize(st));
+    const long long sb = bh ? 2 : 4;
+    long long per_part = 0, once = 0;
+    for (int c = 0; c < F.N; ++c) {
+        bool any = false;
+        for (int r = 0; r < parts; ++r) {
+            const bool hit = hm[(size_t)r * F.N + c] != 0;
+            per_part += hit;
+            any = any || hit;
+        }
+        once += any;
+    }
+    long long a = 0, nrows = 0;
+    for (size_t u = 0; u < ha.size(); ++u) {
+        a += ha[u];
+        nrows += hr[u];
+    }
+    t.b_bytes = per_part * O * sb;
+    t.b_once_bytes = once * O * sb;
+    t.a_bytes = a * t.o_tiles;
+    t.c_bytes = nrows * O * 4LL * (accumulate ? 2 : 1);
+    t.convert_bytes = convert ? (long long)F.N * O * 6 : 0;
+    t.total = t.b_bytes + t.a_bytes + t.c_bytes + t.convert_bytes;
+    return t;
 }
 
 }  // namespace vcsrmc
