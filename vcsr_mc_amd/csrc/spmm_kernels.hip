@@ -214,6 +214,37 @@ __device__ __forceinline__ void store_c4(float* p, const floatx4& v) {
     else __builtin_nontemporal_store(v, reinterpret_cast<floatx4*>(p));
 }
 
+// Parks a wave's 16 x TK tile row-major in P (row pitch TK floats): lane (n, g) holds rows
+// 4g..4g+3 at columns VEC n .. VEC n + VEC - 1, written as 16-byte pieces.  The LDS serves 128
+// bytes per cycle over 32 four-byte banks, so a ds_write_b128 runs 8 lanes at a time (measured
+// on gfx950 with rocprofv3's SQ_LDS_BANK_CONFLICT: contiguous 16-byte pieces count no conflict,
+// pieces 32 bytes apart one conflict cycle per cycle, a 32-bit access of 64 lanes on one bank 31
+// per cycle).  At VEC = 8 the 8 lanes n = 0..7 of a row would write dword offsets 8n + 4h:
+// lanes n and n + 4 on the same four banks.  Lanes with n & 4 therefore write their two pieces
+// in the other order, and each 8-lane pass covers all 32 banks once; the layout, and so the
+// contiguous reads of the merge, are unchanged.  (At VEC = 4 a pass is already conflict-free.)
+template <int TK>
+__device__ __forceinline__ void park_tile(float* Pw, const floatx4 (&acc)[TK / 16], float scale,
+                                          int n, int g) {
+    constexpr int VEC = TK / 16;
+    if constexpr (VEC == 8) {
+        const bool sw = (n & 4) != 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const floatx4 lo = floatx4{acc[0][i], acc[1][i], acc[2][i], acc[3][i]} * scale;
+            const floatx4 hi = floatx4{acc[4][i], acc[5][i], acc[6][i], acc[7][i]} * scale;
+            float* row = Pw + (4 * g + i) * TK + VEC * n;
+            *reinterpret_cast<floatx4*>(row + (sw ? 4 : 0)) = sw ? hi : lo;
+            *reinterpret_cast<floatx4*>(row + (sw ? 0 : 4)) = sw ? lo : hi;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int q = 0; q < VEC; ++q) Pw[(4 * g + i) * TK + VEC * n + q] = acc[q][i] * scale;
+    }
+}
+
 // Adds the unit's 16 x TK result into C (ACC) or writes it (overwrite).  W == 1, staged merge
 // (a whole, aligned tile of an unsplit panel): the wave parks its tile in its slice of P (lane
 // (n, g) owns rows 4g..4g+3, columns k0 + VEC n .. + VEC - 1), reads it back with consecutive
@@ -239,13 +270,9 @@ __device__ __forceinline__ void merge_into_c(const floatx4 (&acc)[TK / 16], floa
     const long long OL = O;
     if constexpr (W == 1) {
         if (!split && c4 && k0 + TK <= O) {  // staged merge
-            float* Pw = P + wave * 16 * TK;
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int q = 0; q < VEC; ++q)
-                    Pw[(4 * g + i) * TK + VEC * n + q] = acc[q][i] * scale;
+            park_tile<TK>(P + wave * 16 * TK, acc, scale, n, g);
             wave_lds_sync();
+            const float* Pw = P + wave * 16 * TK;
 #pragma unroll
             for (int j = 0; j < 16 * TK / 256; ++j) {
                 const int e = lane * 4 + 256 * j;
@@ -283,11 +310,7 @@ __device__ __forceinline__ void merge_into_c(const floatx4 (&acc)[TK / 16], floa
             }
         }
     } else {
-        float* Pw = P + wave * 16 * TK;
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int q = 0; q < VEC; ++q) Pw[(4 * g + i) * TK + VEC * n + q] = acc[q][i];
+        park_tile<TK>(P + wave * 16 * TK, acc, 1.0f, n, g);
         __syncthreads();
 #pragma unroll
         for (int j = 0; j < CAhead<TK, W>::N; ++j) {
