@@ -1,6 +1,6 @@
 """The corpus sweep protocol (vcsr_mc_amd/sweep.py; the reference's bench200/run200.py,
 rerun_noisy.py, analyze.py, orig_table.py): statistics against closed forms, and the run /
-rerun / table logic against a stub driver whose timings are known, so no GPU is needed.  The
+rerun / report logic against a stub driver whose timings are known, so no GPU is needed.  The
 GPU test runs the real spmm_vcsr over a small corpus."""
 import csv
 import io
@@ -76,7 +76,7 @@ RESULT_FIELDS = ["gpu", "sm", "mtx", "O", "segw", "bundle", "tileK", "repeat", "
 
 
 def test_result_columns_match_reference():
-    assert sweep.FIELDS == RESULT_FIELDS
+    assert sweep.RESULT_COLUMNS == RESULT_FIELDS
 
 
 def test_synth_corpus_files(tmp_path):
@@ -106,7 +106,9 @@ def test_statistics_closed_forms():
     gm, gs = sweep.geo_gstd([5.0] * 7)
     assert math.isclose(gm, 5.0) and math.isclose(gs, 1.0)
     assert all(math.isnan(x) for x in sweep.geo_gstd([]))
-    assert sweep.matrix_name("/x/y/cop20k_A.mtx") == "cop20k_A"
+    assert sweep.matrix_of("/x/y/cop20k_A.mtx") == "cop20k_A"
+    assert sweep.with_width(["--repeat", "10", "--O", "7", "--tileK", "16"], 128, 64) == \
+        ["--O", "128", "--tileK", "64", "--repeat", "10"]
 
 
 def test_run_writes_reference_columns(stub, corpus, tmp_path):
@@ -117,29 +119,31 @@ def test_run_writes_reference_columns(stub, corpus, tmp_path):
                   extra=["--O", "64", "--tileK", "64"], log=log)
     rows = rows_of(out)
     assert n == len(rows) == 3 * 2 * 2  # 3 present matrices x 2 reps x 2 working algos
-    assert list(rows[0].keys()) == sweep.FIELDS
+    assert list(rows[0].keys()) == sweep.RESULT_COLUMNS
     assert {r["rep"] for r in rows} == {"0", "1"}
-    assert {r["nnz"] for r in rows if sweep.matrix_name(r["mtx"]) == "b"} == {"20"}
+    assert {r["nnz"] for r in rows if sweep.matrix_of(r["mtx"]) == "b"} == {"20"}
     assert all(r["O"] == "64" for r in rows)
     text = log.getvalue()
-    assert "missing" in text and "absent.mtx" in text
-    assert "fail a bad rep0: Unknown algorithm: bad" in text
+    assert "absent: no Matrix Market file at" in text and "absent.mtx, skipped" in text
+    assert "a / bad / repetition 0: Unknown algorithm: bad" in text
+    assert "b: 4 rows" in text  # 2 repetitions x 2 working kernels
 
 
 def test_load_medians_and_gflops(stub, corpus, tmp_path):
     c, d = corpus
     out = tmp_path / "r.csv"
     sweep.run(stub, c, d, out, algos=["rocsparse", "vcsr_mc"], reps=3, log=io.StringIO())
-    g, t, e, nnz = sweep.load(out, "ms")
-    assert t["a"]["vcsr_mc"] == 0.25 and t["b"]["rocsparse"] == 2.0
+    res = sweep.Results.read(out, "ms")
+    assert res.time("a", "vcsr_mc") == 0.25 and res.time("b", "rocsparse") == 2.0
     # noisy: first call 10x slower, median of three is the normal time
-    assert t["noisy"]["vcsr_mc"] == 1.0
-    assert math.isclose(g["b"]["vcsr_mc"], 200.0 / 0.5)
-    _, tm, _, _ = sweep.load(out, "ms_mean")
-    assert math.isclose(tm["a"]["rocsparse"], 1.1)
-    g2, _, _, _ = sweep.load(out, "ms_mean")
-    assert math.isclose(g2["a"]["rocsparse"], 100.0 / 1.1)
-    assert math.isclose(e["a"]["vcsr_mc"], 0.25e-7) and nnz["noisy"] == 30
+    assert res.time("noisy", "vcsr_mc") == 1.0
+    assert math.isclose(res.gflops("b", "vcsr_mc"), 200.0 / 0.5)
+    mean = sweep.Results.read(out, "ms_mean")
+    assert math.isclose(mean.time("a", "rocsparse"), 1.1)
+    assert math.isclose(mean.gflops("a", "rocsparse"), 100.0 / 1.1)
+    assert math.isclose(res.error("a", "vcsr_mc"), 0.25e-7) and res.nnz["noisy"] == 30
+    assert res.width == 128
+    assert res.speedups("vcsr_mc") == {"a": 4.0, "b": 4.0, "noisy": 4.0}
 
 
 def test_rerun_replaces_noisy_rows(stub, corpus, tmp_path):
@@ -154,31 +158,34 @@ def test_rerun_replaces_noisy_rows(stub, corpus, tmp_path):
     after = rows_of(out)
     raw = rows_of(tmp_path / "results_O128_raw.csv")
     assert raw == before
-    noisy_rows = [r for r in after if sweep.matrix_name(r["mtx"]) == "noisy"]
-    assert len(noisy_rows) == sweep.RERUN_REPS * 2
+    noisy_rows = [r for r in after if sweep.matrix_of(r["mtx"]) == "noisy"]
+    assert len(noisy_rows) == sweep.NOISY_REPS * 2
     assert all(float(r["ms"]) < 10 for r in noisy_rows)  # later calls are not slow
     assert all(r["O"] == "128" for r in noisy_rows)  # --O comes from the results file
-    assert [r for r in after if sweep.matrix_name(r["mtx"]) != "noisy"] == \
-        [r for r in before if sweep.matrix_name(r["mtx"]) != "noisy"]
+    assert [r for r in after if sweep.matrix_of(r["mtx"]) != "noisy"] == \
+        [r for r in before if sweep.matrix_of(r["mtx"]) != "noisy"]
     assert not (tmp_path / "results_O128_rerun_corpus.csv").exists()
 
 
-def test_table_speedups(stub, corpus, tmp_path):
+def test_report_speedups(stub, corpus, tmp_path):
     c, d = corpus
     paths = []
     for O in (64, 128):
         p = tmp_path / f"res_O{O}.csv"
-        sweep.run(stub, c, d, p, algos=sweep.DEFAULT_ALGOS, reps=3,
+        sweep.run(stub, c, d, p, algos=sweep.ALL_KERNELS, reps=3,
                   extra=["--O", str(O)], log=io.StringIO())
         paths.append(str(p))
     buf = io.StringIO()
-    res = sweep.table(paths, out=buf)
+    res = sweep.report(paths, out=buf)
     s = res[("ms_median", 64, "vcsr_mc")]
-    assert s["n"] == 3 and math.isclose(s["geomean"], 4.0) and math.isclose(s["gstd"], 1.0)
-    assert s["wins"] == 3 and math.isclose(s["max_rel_l2"], 0.25e-7)
-    assert math.isclose(res[("ms_median", "all", "vcsr_mc_fp32")]["geomean"], 2.0)
-    assert res[("ms_median", "all", "vcsr_mc_fp32")]["n"] == 6
-    assert "Speedup over rocSPARSE default" in buf.getvalue()
+    assert s.n == 3 and math.isclose(s.geomean, 4.0) and math.isclose(s.gstd, 1.0)
+    assert s.wins == 3 and math.isclose(s.max_rel_l2, 0.25e-7)
+    assert s.min == s.max == s.median == 4.0
+    assert math.isclose(res[("ms_median", "all", "vcsr_mc_fp32")].geomean, 2.0)
+    assert res[("ms_median", "all", "vcsr_mc_fp32")].n == 6
+    assert math.isclose(res[("ms_mean", 128, "vcsr_mc")].geomean, 4.0)
+    text = buf.getvalue()
+    assert "Speedup over rocsparse" in text and "| 64 | vcsr_mc | 3 | 4.00x |" in text
 
 
 @pytest.mark.gpu
@@ -203,8 +210,8 @@ def test_sweep_real_driver(tmp_path):
     csvs, res = sweep.sweep(c, d, tag="t", widths=(32,), tileK=128, reps=2,
                             logdir=tmp_path / "logs", outdir=tmp_path)
     rows = rows_of(csvs[0])
-    assert len(rows) == 3 * 2 * len(sweep.DEFAULT_ALGOS)
+    assert len(rows) == 3 * 2 * len(sweep.ALL_KERNELS)
     assert all(r["validation"] == "pass" for r in rows)
     assert all(r["tileK"] == "32" for r in rows)
-    for k in sweep.KERNELS:
-        assert res[("ms_median", 32, k)]["n"] == 3
+    for k in sweep.REPORTED:
+        assert res[("ms_median", 32, k)].n == 3

@@ -1,324 +1,434 @@
-"""Corpus sweep protocol for the spmm_vcsr driver: run, rerun noisy matrices, tabulate.
+"""Corpus sweep for the spmm_vcsr driver: measure, re-measure noisy matrices, report speedups.
 
-The same protocol as the reference's harness (bench200/run200.py, rerun_noisy.py, analyze.py,
-orig_table.py, run.sh of MuuSeoTia/VCSR_MC), for a corpus of Matrix Market files supplied
-locally (nothing is downloaded):
+The protocol of the reference's corpus harness (bench200/run200.py, rerun_noisy.py, analyze.py,
+orig_table.py, run.sh of MuuSeoTia/VCSR_MC), over Matrix Market files supplied locally (nothing
+is downloaded).  What is kept from it is the interface: the results CSV columns and file names,
+the environment variables ALGOS / REPS / EXTRA, the noise rule and the statistics.  The code is
+organised differently:
 
-* run: one fresh driver process per (matrix, algorithm, repetition), each with
-  ``--mtx --algo --csv`` plus the extra arguments; rows are tagged with the corpus nnz and the
-  repetition and written to one CSV with the reference's columns (run200.py:24-27).  A failing or
-  timed-out process is reported and skipped (run200.py:42-56).
-* rerun: a matrix is noisy when, for some algorithm, its slowest repetition is more than 2x its
-  fastest; noisy matrices are run again with 5 repetitions and their rows replaced, the original
-  CSV kept as ``<name>_raw.csv`` (rerun_noisy.py:2-8, 24-59).
-* table: per (matrix, algorithm) the median over repetitions (analyze.py:7-10, 32), speedup =
-  t_rocsparse / t_kernel, and per kernel the geometric mean, geometric standard deviation
-  exp(sigma of log speedup), median, min, max, wins and the largest rel_l2, for the mean and the
-  median launch time columns, pooled over widths O when several CSVs are given
-  (orig_table.py:17-40, analyze.py:38-45).
+* a sweep is a plan of jobs (matrix, repetition, kernel), each run by a `Driver` -- one fresh
+  process of the binary with ``--mtx --algo --csv`` and the sweep's extra arguments -- whose rows
+  are tagged with the corpus nnz and the repetition and streamed to the CSV;
+* `Results` holds a CSV's rows per (matrix, kernel) cell: the median time over repetitions, the
+  GFLOP/s at that time (from the FLOP count every row of a matrix shares) and the largest
+  rel_l2;
+* a matrix is noisy when some kernel's slowest repetition took more than twice its fastest;
+  `rerun_noisy` measures those matrices again with five fresh repetitions, in memory, and
+  replaces their rows, keeping the first CSV as ``<name>_raw.csv``;
+* `report` prints, per timing column (mean and median of a process's timed launches) and width
+  O, each kernel's speedup over rocSPARSE (t_rocsparse / t_kernel per matrix) as geometric mean,
+  geometric standard deviation exp(sigma of ln speedup), median, min, max, wins and the largest
+  rel_l2, pooled over widths when several CSVs are given.
 
 Usage::
 
-    python -m vcsr_mc_amd.sweep run   BINARY CORPUS.csv MTXDIR OUT.csv
-    python -m vcsr_mc_amd.sweep rerun BINARY CORPUS.csv MTXDIR RESULTS.csv [...]
-    python -m vcsr_mc_amd.sweep table RESULTS.csv [...]
-    python -m vcsr_mc_amd.sweep all   --corpus CORPUS.csv --mtx-dir MTXDIR [--tag T] [--O 128 ...]
-
-``ALGOS``, ``REPS`` and ``EXTRA`` are read from the environment when the options are not given,
-like the reference's scripts.
+    python -m vcsr_mc_amd.sweep run    BINARY CORPUS.csv MTXDIR OUT.csv
+    python -m vcsr_mc_amd.sweep rerun  BINARY CORPUS.csv MTXDIR RESULTS.csv [...]
+    python -m vcsr_mc_amd.sweep report RESULTS.csv [...]
+    python -m vcsr_mc_amd.sweep all    --corpus CORPUS.csv --mtx-dir MTXDIR [--tag T] [--O 128 ...]
 """
 from __future__ import annotations
 
 import argparse
-import collections
 import csv
 import io
 import math
 import os
+import platform
 import shlex
 import shutil
-import socket
+import statistics
 import subprocess
 import sys
 import time
+from dataclasses import dataclass, field
 from pathlib import Path
+from typing import Callable, Iterable
 
-FIELDS = ["gpu", "sm", "mtx", "O", "segw", "bundle", "tileK", "repeat", "algo", "ms", "gflops",
-          "validation", "rel_l2", "setup_ms", "nnz", "rep", "ms_mean", "ms_median", "convert_ms",
-          "upload_ms"]
-DEFAULT_ALGOS = ["rocsparse", "rocsparse_fp16", "vcsr_mc", "vcsr_mc_fp32"]
-BASE = "rocsparse"
-KERNELS = ["vcsr_mc", "vcsr_mc_fp32"]
-SPREAD, RERUN_REPS = 2.0, 5
+# Columns of a results CSV (the reference harness's, bench200/run200.py:22-24): the driver's CSV
+# columns plus the corpus nnz and the repetition.
+RESULT_COLUMNS = ["gpu", "sm", "mtx", "O", "segw", "bundle", "tileK", "repeat", "algo", "ms",
+                  "gflops", "validation", "rel_l2", "setup_ms", "nnz", "rep", "ms_mean",
+                  "ms_median", "convert_ms", "upload_ms"]
+ALL_KERNELS = ("rocsparse", "rocsparse_fp16", "vcsr_mc", "vcsr_mc_fp32")
+BASELINE = "rocsparse"
+REPORTED = ("vcsr_mc", "vcsr_mc_fp32")
+NOISE_SPREAD = 2.0   # slowest / fastest repetition above this: the matrix is measured again
+NOISY_REPS = 5       # repetitions of a noisy matrix's second measurement
+RERUN_KERNELS = ("rocsparse", "vcsr_mc")
+RERUN_EXTRA = "--repeat 10 --warmup 0 --stat median"
 DRIVER = Path(__file__).resolve().parent / "spmm_vcsr"
 
 
-def _env_list(name: str, default: list[str]) -> list[str]:
-    v = os.environ.get(name)
-    return v.replace(",", " ").split() if v else list(default)
+def _from_env(name: str, fallback: Iterable[str]) -> list[str]:
+    """A list option from the environment (spaces or commas), else the fallback."""
+    text = os.environ.get(name, "")
+    return text.replace(",", " ").split() if text.strip() else list(fallback)
 
 
-def matrix_name(mtx: str) -> str:
-    base = mtx.replace("\\", "/").split("/")[-1]
-    return base[:-4] if base.endswith(".mtx") else base
+def matrix_of(mtx_path: str) -> str:
+    """Corpus name of a row's Matrix Market path: its file name without .mtx."""
+    stem = Path(mtx_path.replace("\\", "/")).name
+    return stem[: -len(".mtx")] if stem.endswith(".mtx") else stem
 
 
-# ---- statistics (analyze.py:7-10, 38-45) ------------------------------------------------
-def median(v):
-    v = sorted(v)
-    n = len(v)
-    if n == 0:
-        raise ValueError("median of nothing")
-    return v[n // 2] if n % 2 else 0.5 * (v[n // 2 - 1] + v[n // 2])
+# ---- statistics -------------------------------------------------------------------------------
+def median(values: Iterable[float]) -> float:
+    return statistics.median(list(values))
 
 
-def geo_gstd(vals):
-    """Geometric mean and geometric standard deviation exp(sigma of log x), sigma over n."""
-    if not vals:
-        return float("nan"), float("nan")
-    lg = [math.log(x) for x in vals]
-    mu = sum(lg) / len(lg)
-    sd = math.sqrt(sum((x - mu) ** 2 for x in lg) / len(lg))
-    return math.exp(mu), math.exp(sd)
+def geo_gstd(values: Iterable[float]) -> tuple[float, float]:
+    """Geometric mean and geometric standard deviation, exp(population sigma of ln x)."""
+    logs = [math.log(v) for v in values]
+    if not logs:
+        return math.nan, math.nan
+    return math.exp(statistics.fmean(logs)), math.exp(statistics.pstdev(logs))
 
 
-def load(path, col: str = "ms"):
-    """Per (matrix, algo): median of `col` over its rows, GFLOP/s at that time, largest rel_l2.
+# ---- running the driver -----------------------------------------------------------------------
+@dataclass(frozen=True)
+class Job:
+    matrix: str
+    path: Path
+    nnz: str
+    algo: str
+    rep: int
 
-    GFLOP/s for another timing column is recomputed from the row's FLOP count
-    (gflops x ms), which every row of a matrix shares.  Returns (gflops, ms, rel_l2, nnz), each a
-    dict matrix -> algo -> value (nnz: matrix -> int)."""
-    times = collections.defaultdict(lambda: collections.defaultdict(list))
-    errs = collections.defaultdict(lambda: collections.defaultdict(list))
-    mflop, nnz = {}, {}
+
+@dataclass
+class Outcome:
+    job: Job
+    rows: list = field(default_factory=list)
+    problem: str | None = None  # why the job gave no rows
+
+
+class Driver:
+    """Runs one job as a fresh process of the benchmark binary."""
+
+    def __init__(self, binary, extra: Iterable[str] = (), timeout: float = 300):
+        self.binary = str(binary)
+        self.extra = list(extra)
+        self.timeout = timeout
+
+    def __call__(self, job: Job) -> Outcome:
+        argv = [self.binary, "--mtx", str(job.path), "--algo", job.algo, "--csv", *self.extra]
+        try:
+            proc = subprocess.run(argv, capture_output=True, text=True, timeout=self.timeout)
+        except subprocess.TimeoutExpired:
+            return Outcome(job, problem=f"no result within {self.timeout:g} s")
+        if proc.returncode != 0:
+            lines = [l for l in (proc.stderr or "").splitlines() if l.strip()]
+            return Outcome(job, problem=lines[-1].strip() if lines
+                           else f"exit status {proc.returncode}")
+        rows = []
+        for row in csv.DictReader(io.StringIO(proc.stdout)):
+            row.update(nnz=job.nnz, rep=job.rep)
+            rows.append(row)
+        return Outcome(job, rows)
+
+
+def read_corpus(path) -> list[dict]:
     with open(path, newline="") as fh:
-        for r in csv.DictReader(fh):
-            m = matrix_name(r["mtx"])
-            t = float(r[col])
-            times[m][r["algo"]].append(t)
-            errs[m][r["algo"]].append(float(r["rel_l2"]))
-            if float(r["ms"]) > 0:
-                mflop[m] = float(r["gflops"]) * float(r["ms"])
-            nnz[m] = int(r["nnz"]) if r.get("nnz") else 0
-    g, t, e = (collections.defaultdict(dict) for _ in range(3))
-    for m in times:
-        for a, v in times[m].items():
-            t[m][a] = median(v)
-            g[m][a] = mflop.get(m, 0.0) / t[m][a] if t[m][a] > 0 else 0.0
-            e[m][a] = max(errs[m][a])
-    return g, t, e, nnz
+        return list(csv.DictReader(fh))
 
 
-# ---- run (run200.py) ----------------------------------------------------------------------
-def run(binary, corpus, mtxdir, out, algos=None, reps=None, extra=None, timeout=300, log=None):
-    """One process per (matrix, algo, rep); returns the number of rows written."""
-    algos = algos or _env_list("ALGOS", DEFAULT_ALGOS)
-    reps = reps if reps is not None else int(os.environ.get("REPS", "1"))
-    extra = extra if extra is not None else shlex.split(os.environ.get("EXTRA", ""))
-    log = log or sys.stderr
-    rows = 0
-    with open(out, "w", newline="") as fh:
-        w = csv.DictWriter(fh, fieldnames=FIELDS, extrasaction="ignore")
-        w.writeheader()
-        with open(corpus, newline="") as cf:
-            entries = list(csv.DictReader(cf))
-        for m in entries:
-            mtx = Path(mtxdir) / f"{m['name']}.mtx"
-            if not mtx.is_file():
-                print(f"missing {mtx}", file=log)
-                continue
-            for rep in range(reps):
-                for algo in algos:
-                    cmd = [str(binary), "--mtx", str(mtx), "--algo", algo, "--csv"] + list(extra)
-                    try:
-                        r = subprocess.run(cmd, capture_output=True, text=True, timeout=timeout)
-                    except subprocess.TimeoutExpired:
-                        print(f"timeout {m['name']} {algo} rep{rep}", file=log)
-                        continue
-                    if r.returncode != 0:
-                        err = (r.stderr or "").strip().splitlines()
-                        print(f"fail {m['name']} {algo} rep{rep}: {err[-1] if err else r.returncode}",
-                              file=log)
-                        continue
-                    for row in csv.DictReader(io.StringIO(r.stdout)):
-                        row["nnz"] = m.get("nnz", "")
-                        row["rep"] = rep
-                        w.writerow(row)
-                        rows += 1
-                    fh.flush()
-            print(m["name"], file=log, flush=True)
-    return rows
+def plan(entries: Iterable[dict], mtxdir, algos: Iterable[str], reps: int,
+         say: Callable[[str], None]) -> list[Job]:
+    """Jobs for the corpus entries whose file exists: per matrix, every repetition runs every
+    kernel once (so a slow process hits one repetition of all kernels, not one kernel)."""
+    jobs = []
+    for entry in entries:
+        path = Path(mtxdir) / f"{entry['name']}.mtx"
+        if not path.is_file():
+            say(f"{entry['name']}: no Matrix Market file at {path}, skipped")
+            continue
+        jobs += [Job(entry["name"], path, entry.get("nnz", ""), algo, rep)
+                 for rep in range(reps) for algo in algos]
+    return jobs
 
 
-# ---- rerun (rerun_noisy.py) -------------------------------------------------------------
-def noisy_matrices(rows, spread: float = SPREAD):
-    ms = collections.defaultdict(list)
-    for r in rows:
-        ms[(matrix_name(r["mtx"]), r["algo"])].append(float(r["ms"]))
-    return sorted({m for (m, _), v in ms.items() if min(v) > 0 and max(v) / min(v) > spread})
-
-
-def _protocol_extra(extra, O, tileK):
-    """The sweep's extra arguments with --O / --tileK taken from the results file."""
-    rest, toks = [], list(extra)
-    while toks:
-        t = toks.pop(0)
-        if t in ("--O", "--tileK"):
-            if toks:
-                toks.pop(0)
+def execute(jobs: list[Job], driver: Callable[[Job], Outcome], emit: Callable[[list], None],
+            say: Callable[[str], None]) -> int:
+    """Runs the jobs in order, passing each job's rows to `emit`; returns the rows emitted."""
+    count, done = 0, None
+    for job in jobs:
+        if done is not None and job.matrix != done[0]:
+            say(f"{done[0]}: {done[1]} rows")
+            done = None
+        out = driver(job)
+        if out.problem is not None:
+            say(f"{job.matrix} / {job.algo} / repetition {job.rep}: {out.problem}")
         else:
-            rest.append(t)
-    return ["--O", str(O), "--tileK", str(tileK)] + rest
+            emit(out.rows)
+            count += len(out.rows)
+        done = (job.matrix, (done[1] if done else 0) + len(out.rows))
+    if done is not None:
+        say(f"{done[0]}: {done[1]} rows")
+    return count
 
 
-def rerun_noisy(binary, corpus, mtxdir, paths, algos=None, extra=None, reps=RERUN_REPS,
-                spread=SPREAD, log=None):
-    """Reruns the noisy matrices of each results CSV in place; returns {path: [names]}."""
-    log = log or sys.stdout
-    algos = algos or _env_list("ALGOS", ["rocsparse", "vcsr_mc"])
-    extra = extra if extra is not None else shlex.split(
-        os.environ.get("EXTRA", "--repeat 10 --warmup 0 --stat median"))
-    done = {}
+def _logger(stream):
+    def say(text):
+        print(text, file=stream, flush=True)
+    return say
+
+
+def run(binary, corpus, mtxdir, out, algos=None, reps=None, extra=None, timeout=300,
+        log=None) -> int:
+    """Measures every (matrix, repetition, kernel) of the corpus into the CSV `out`; returns the
+    number of rows written.  Unset options come from ALGOS, REPS and EXTRA."""
+    algos = list(algos) if algos else _from_env("ALGOS", ALL_KERNELS)
+    reps = int(os.environ.get("REPS", "1")) if reps is None else reps
+    extra = shlex.split(os.environ.get("EXTRA", "")) if extra is None else list(extra)
+    say = _logger(log or sys.stderr)
+    jobs = plan(read_corpus(corpus), mtxdir, algos, reps, say)
+    with open(out, "w", newline="") as fh:
+        sink = csv.DictWriter(fh, fieldnames=RESULT_COLUMNS, extrasaction="ignore")
+        sink.writeheader()
+
+        def emit(rows):
+            sink.writerows(rows)
+            fh.flush()
+
+        return execute(jobs, Driver(binary, extra, timeout), emit, say)
+
+
+# ---- results ----------------------------------------------------------------------------------
+@dataclass
+class Cell:
+    """One (matrix, kernel) of a results CSV: its repetitions."""
+    times: list = field(default_factory=list)
+    errors: list = field(default_factory=list)
+
+    @property
+    def time(self) -> float:
+        return median(self.times)
+
+    @property
+    def max_error(self) -> float:
+        return max(self.errors)
+
+
+class Results:
+    """A results CSV per (matrix, kernel), timed by one of its timing columns."""
+
+    def __init__(self, rows: Iterable[dict], column: str = "ms"):
+        self.column = column
+        self.cells: dict[tuple[str, str], Cell] = {}
+        self.mflop: dict[str, float] = {}  # FLOP count / 1e6, shared by a matrix's rows
+        self.nnz: dict[str, int] = {}
+        self.width = None
+        for row in rows:
+            m = matrix_of(row["mtx"])
+            cell = self.cells.setdefault((m, row["algo"]), Cell())
+            cell.times.append(float(row[column]))
+            cell.errors.append(float(row["rel_l2"]))
+            if float(row["ms"]) > 0:
+                self.mflop[m] = float(row["gflops"]) * float(row["ms"])
+            self.nnz[m] = int(row["nnz"]) if row.get("nnz") else 0
+            if self.width is None:
+                self.width = int(row["O"])
+
+    @classmethod
+    def read(cls, path, column: str = "ms") -> "Results":
+        with open(path, newline="") as fh:
+            return cls(csv.DictReader(fh), column)
+
+    def time(self, matrix: str, algo: str) -> float:
+        return self.cells[(matrix, algo)].time
+
+    def gflops(self, matrix: str, algo: str) -> float:
+        t = self.time(matrix, algo)
+        return self.mflop.get(matrix, 0.0) / t if t > 0 else 0.0
+
+    def error(self, matrix: str, algo: str) -> float:
+        return self.cells[(matrix, algo)].max_error
+
+    def algos(self) -> set:
+        return {a for _, a in self.cells}
+
+    def speedups(self, kernel: str, base: str = BASELINE) -> dict[str, float]:
+        """t_base / t_kernel for every matrix timed (above zero) for both."""
+        out = {}
+        for (m, a), cell in self.cells.items():
+            if a != kernel or (m, base) not in self.cells:
+                continue
+            tk, tb = cell.time, self.time(m, base)
+            if tk > 0 and tb > 0:
+                out[m] = tb / tk
+        return out
+
+
+# ---- noisy matrices ---------------------------------------------------------------------------
+def noisy_matrices(rows: Iterable[dict], spread: float = NOISE_SPREAD) -> list[str]:
+    """Matrices where some kernel's slowest repetition took more than `spread` x its fastest."""
+    lo: dict = {}
+    hi: dict = {}
+    for row in rows:
+        key, t = (matrix_of(row["mtx"]), row["algo"]), float(row["ms"])
+        lo[key] = min(lo.get(key, t), t)
+        hi[key] = max(hi.get(key, t), t)
+    return sorted({m for (m, a) in lo if lo[(m, a)] > 0 and hi[(m, a)] > spread * lo[(m, a)]})
+
+
+def with_width(extra: Iterable[str], O, tileK) -> list[str]:
+    """`extra` with its --O / --tileK pairs replaced by the given ones."""
+    kept, tokens = [], iter(extra)
+    for tok in tokens:
+        if tok in ("--O", "--tileK"):
+            next(tokens, None)
+        else:
+            kept.append(tok)
+    return ["--O", str(O), "--tileK", str(tileK), *kept]
+
+
+def rerun_noisy(binary, corpus, mtxdir, paths, algos=None, extra=None, reps=NOISY_REPS,
+                spread=NOISE_SPREAD, log=None) -> dict:
+    """Measures each results CSV's noisy matrices again (`reps` fresh repetitions, the CSV's own
+    O and tileK) and replaces their rows in place; the first version of each CSV stays as
+    <name>_raw.csv.  Returns {path: noisy matrices}."""
+    algos = list(algos) if algos else _from_env("ALGOS", RERUN_KERNELS)
+    extra = shlex.split(os.environ.get("EXTRA", RERUN_EXTRA)) if extra is None else list(extra)
+    say = _logger(log or sys.stdout)
+    entries = read_corpus(corpus)
+    found = {}
     for path in map(Path, paths):
-        raw = path.with_name(path.stem + "_raw.csv")
+        raw = path.with_name(f"{path.stem}_raw.csv")
         if not raw.exists():
             shutil.copy(path, raw)
         with raw.open(newline="") as fh:
-            rows = list(csv.DictReader(fh))
-        noisy = noisy_matrices(rows, spread)
-        done[str(path)] = noisy
-        if not rows:
+            first = list(csv.DictReader(fh))
+        noisy = noisy_matrices(first, spread)
+        found[str(path)] = noisy
+        if not first:
             continue
-        O, tk = rows[0]["O"], rows[0]["tileK"]
-        print(f"{path.name}: O={O}, {len(noisy)} noisy: {' '.join(noisy)}", file=log, flush=True)
+        say(f"{path.name} (O = {first[0]['O']}): {len(noisy)} noisy matrices"
+            + (f" -- {', '.join(noisy)}" if noisy else ""))
         if not noisy:
             continue
-        sub = path.with_name(path.stem + "_rerun_corpus.csv")
-        with open(corpus, newline="") as cf, sub.open("w", newline="") as fh:
-            reader = csv.DictReader(cf)
-            w = csv.DictWriter(fh, fieldnames=reader.fieldnames)
-            w.writeheader()
-            w.writerows(m for m in reader if m["name"] in noisy)
-        out = path.with_name(path.stem + "_rerun.csv")
-        run(binary, sub, mtxdir, out, algos=algos, reps=reps, extra=_protocol_extra(extra, O, tk))
-        with out.open(newline="") as fh:
-            new = list(csv.DictReader(fh))
+        driver = Driver(binary, with_width(extra, first[0]["O"], first[0]["tileK"]))
+        fresh: list = []
+        jobs = plan([e for e in entries if e["name"] in noisy], mtxdir, algos, reps, say)
+        execute(jobs, driver, fresh.extend, lambda _text: None)
         with path.open("w", newline="") as fh:
-            w = csv.DictWriter(fh, fieldnames=list(rows[0].keys()), extrasaction="ignore")
+            w = csv.DictWriter(fh, fieldnames=list(first[0]), extrasaction="ignore")
             w.writeheader()
-            w.writerows(r for r in rows if matrix_name(r["mtx"]) not in noisy)
-            w.writerows(new)
-        sub.unlink()
-        print(f"  replaced with {len(new)} rows from {reps} reps -> {path.name}", file=log,
-              flush=True)
-    return done
+            w.writerows(r for r in first if matrix_of(r["mtx"]) not in noisy)
+            w.writerows(fresh)
+        say(f"  {len(fresh)} rows from {reps} new repetitions now stand for them in {path.name}")
+    return found
 
 
-# ---- table (orig_table.py) ----------------------------------------------------------------
-def speedups(path, col, kernel, base=BASE):
-    _, t, e, _ = load(path, col)
-    sp = [t[m][base] / t[m][kernel] for m in t
-          if t[m].get(base, 0) > 0 and t[m].get(kernel, 0) > 0]
-    err = max((e[m][kernel] for m in e if kernel in e[m]), default=float("nan"))
-    return sp, err
+# ---- report -----------------------------------------------------------------------------------
+@dataclass
+class Summary:
+    n: int
+    geomean: float
+    gstd: float
+    median: float
+    min: float
+    max: float
+    wins: int
+    max_rel_l2: float = math.nan
 
 
-def summary(sp):
-    gm, gs = geo_gstd(sp)
-    return dict(n=len(sp), geomean=gm, gstd=gs, median=median(sp), min=min(sp), max=max(sp),
-                wins=sum(s > 1 for s in sp))
+def summarize(speedups: list[float], max_rel_l2: float = math.nan) -> Summary:
+    gm, gs = geo_gstd(speedups)
+    return Summary(len(speedups), gm, gs, median(speedups), min(speedups), max(speedups),
+                   sum(1 for s in speedups if s > 1.0), max_rel_l2)
 
 
-def table(paths, kernels=KERNELS, base=BASE, out=None) -> dict:
-    """Prints the speedup table; returns {(col, O or 'all', kernel): summary}."""
+def _line(width, kernel: str, s: Summary) -> str:
+    err = "" if math.isnan(s.max_rel_l2) else f"{s.max_rel_l2:.1e}"
+    return (f"| {width} | {kernel} | {s.n} | {s.geomean:.2f}x | {s.gstd:.2f} | {s.median:.2f}x "
+            f"| {s.min:.2f}x | {s.max:.1f}x | {s.wins}/{s.n} | {err} |")
+
+
+def report(paths, kernels=REPORTED, base=BASELINE, out=None) -> dict:
+    """Prints the speedup tables (Markdown) and returns {(column, O or 'all', kernel): Summary}."""
     out = out or sys.stdout
-    res = {}
-    for col, what in (("ms_mean", "MEAN of the timed launches"),
-                      ("ms_median", "MEDIAN of the timed launches")):
-        print(f"\n=== Speedup over rocSPARSE default -- {what} ===", file=out)
-        print(f"{'O':>5}  {'kernel':<22}{'n':>4}{'geomean':>9}{'gstd':>7}{'median':>8}{'min':>7}"
-              f"{'max':>8}{'wins':>9}{'max rel_l2':>12}", file=out)
-        pooled = {}
+    found = {}
+    for column, what in (("ms_mean", "mean"), ("ms_median", "median")):
+        print(f"\n### Speedup over {base} (its default algorithm), by the {what} of each "
+              f"process's timed launches\n", file=out)
+        print("| O | kernel | matrices | geomean | gstd | median | min | max | wins | "
+              "max rel_l2 |", file=out)
+        print("|---|---|---|---|---|---|---|---|---|---|", file=out)
+        pooled: dict[str, list] = {}
         for path in paths:
-            with open(path, newline="") as fh:
-                first = next(csv.DictReader(fh), None)
-            if first is None:
+            res = Results.read(path, column)
+            if res.width is None:
                 continue
-            O = int(first["O"])
-            _, t, _, _ = load(path, col)
-            present = {a for m in t for a in t[m]}
-            for k in [k for k in kernels if k in present]:
-                sp, err = speedups(path, col, k, base)
+            for k in (k for k in kernels if k in res.algos()):
+                sp = res.speedups(k, base)
                 if not sp:
                     continue
-                pooled.setdefault(k, []).extend(sp)
-                s = summary(sp)
-                res[(col, O, k)] = dict(s, max_rel_l2=err)
-                print(f"{O:>5}  {k:<22}{s['n']:>4}{s['geomean']:>8.2f}x{s['gstd']:>7.2f}"
-                      f"{s['median']:>7.2f}x{s['min']:>6.2f}x{s['max']:>7.1f}x"
-                      f"{s['wins']:>5}/{s['n']:<3}{err:>12.1e}", file=out)
-            print(file=out)
+                err = max(res.error(m, a) for (m, a) in res.cells if a == k)
+                s = summarize(list(sp.values()), err)
+                found[(column, res.width, k)] = s
+                pooled.setdefault(k, []).extend(sp.values())
+                print(_line(res.width, k, s), file=out)
         if len(paths) > 1:
             for k, sp in pooled.items():
-                s = summary(sp)
-                res[(col, "all", k)] = s
-                print(f"{'all':>5}  {k:<22}{s['n']:>4}{s['geomean']:>8.2f}x{s['gstd']:>7.2f}"
-                      f"{s['median']:>7.2f}x{s['min']:>6.2f}x{s['max']:>7.1f}x"
-                      f"{s['wins']:>5}/{s['n']:<3}", file=out)
-    print("\nPer matrix: median over repetitions (fresh processes). "
-          "gstd = exp(sigma of log speedup).", file=out)
-    return res
+                s = summarize(sp)
+                found[(column, "all", k)] = s
+                print(_line("all", k, s), file=out)
+    print("\nEach matrix counts once per width: the median of its repetitions, each a fresh "
+          "process. gstd = exp(standard deviation of ln speedup).", file=out)
+    return found
 
 
-# ---- the whole sweep (run.sh) -------------------------------------------------------------
+# ---- the whole sweep --------------------------------------------------------------------------
 def sweep(corpus, mtxdir, tag="MI355X_S32T128", widths=(128,), tileK=128, segw=32, warmup=3,
           reps=3, algos=None, binary=DRIVER, logdir="logs", outdir="."):
-    algos = algos or _env_list("ALGOS", DEFAULT_ALGOS)
+    """Every width O: measure the corpus into results200_<tag>_O<O>.csv; then re-measure noisy
+    matrices and report.  Returns (CSV paths, report summaries)."""
+    algos = list(algos) if algos else _from_env("ALGOS", ALL_KERNELS)
     Path(logdir).mkdir(parents=True, exist_ok=True)
-    log_path = Path(logdir) / f"run_{tag}.log"
-    with open(log_path, "w") as log:
-        def say(*a):
-            print(*a, file=log, flush=True)
-            print(*a, flush=True)
-        with open(corpus, newline="") as cf:
-            count = sum(1 for _ in csv.DictReader(cf))
-        say(f"### host: {socket.gethostname()}   {time.strftime('%Y-%m-%dT%H:%M:%SZ', time.gmtime())}")
-        say(f"### corpus: {corpus} ({count} matrices)")
-        say(f"### protocol: repeat=10 warmup={warmup}, mean and median recorded; O in "
-            f"{{{' '.join(map(str, widths))}}}; tileK=min(O,{tileK}) segw={segw}")
-        say(f"### kernels (one process each): {' '.join(algos)}")
-        say(f"### repetitions: {reps} per (matrix, kernel); per-matrix median reported")
-        csvs = []
+    with open(Path(logdir) / f"run_{tag}.log", "w") as logf:
+        def say(text):
+            print(text, file=logf, flush=True)
+            print(text, flush=True)
+
+        entries = read_corpus(corpus)
+        say(f"sweep {tag} on {platform.node()} at "
+            f"{time.strftime('%Y-%m-%d %H:%M:%S UTC', time.gmtime())}")
+        say(f"  corpus {corpus}: {len(entries)} matrices; kernels {', '.join(algos)}, "
+            f"each in its own process, {reps} repetitions (median kept)")
+        say(f"  widths O = {', '.join(map(str, widths))}; tileK = min(O, {tileK}); segw {segw}; "
+            f"10 timed launches after {warmup} warm-ups, mean and median")
+        paths = []
         for O in widths:
             tk = min(O, tileK)
-            extra = ["--O", str(O), "--tileK", str(tk), "--segw", str(segw), "--repeat", "10",
-                     "--warmup", str(warmup), "--stat", "median"]
+            common = ["--segw", str(segw), "--repeat", "10", "--warmup", str(warmup), "--stat",
+                      "median"]
             path = Path(outdir) / f"results200_{tag}_O{O}.csv"
-            say(f"\n### O={O} tileK={tk} -> {path}")
-            n = run(binary, corpus, mtxdir, path, algos=algos, reps=reps, extra=extra, log=log)
-            say(f"### rows: {n}")
-            csvs.append(str(path))
-        say("\n### rerunning noisy matrices")
-        extra = ["--segw", str(segw), "--repeat", "10", "--warmup", str(warmup), "--stat", "median"]
-        rerun_noisy(binary, corpus, mtxdir, csvs, algos=algos, extra=extra, log=log)
-        buf = io.StringIO()
-        res = table(csvs, out=buf)
-        say(buf.getvalue())
-    return csvs, res
+            n = run(binary, corpus, mtxdir, path, algos=algos, reps=reps,
+                    extra=with_width(common, O, tk), log=logf)
+            say(f"  O = {O}: {n} rows in {path}")
+            paths.append(str(path))
+        rerun_noisy(binary, corpus, mtxdir, paths, algos=algos,
+                    extra=["--segw", str(segw), "--repeat", "10", "--warmup", str(warmup),
+                           "--stat", "median"], log=logf)
+        text = io.StringIO()
+        found = report(paths, out=text)
+        say(text.getvalue())
+    return paths, found
 
 
-def main(argv=None):
+def main(argv=None) -> int:
     p = argparse.ArgumentParser(prog="python -m vcsr_mc_amd.sweep")
     sub = p.add_subparsers(dest="cmd", required=True)
-    r = sub.add_parser("run")
-    r.add_argument("binary"), r.add_argument("corpus"), r.add_argument("mtxdir")
-    r.add_argument("out")
-    q = sub.add_parser("rerun")
-    q.add_argument("binary"), q.add_argument("corpus"), q.add_argument("mtxdir")
+    r = sub.add_parser("run", help="measure a corpus into one results CSV")
+    for name in ("binary", "corpus", "mtxdir", "out"):
+        r.add_argument(name)
+    q = sub.add_parser("rerun", help="re-measure the noisy matrices of results CSVs")
+    for name in ("binary", "corpus", "mtxdir"):
+        q.add_argument(name)
     q.add_argument("results", nargs="+")
-    t = sub.add_parser("table")
+    t = sub.add_parser("report", help="speedup tables of results CSVs")
     t.add_argument("results", nargs="+")
-    a = sub.add_parser("all")
+    a = sub.add_parser("all", help="measure every width, re-measure noisy matrices, report")
     a.add_argument("--corpus", required=True)
     a.add_argument("--mtx-dir", required=True)
     a.add_argument("--tag", default="MI355X_S32T128")
@@ -333,8 +443,8 @@ def main(argv=None):
         run(args.binary, args.corpus, args.mtxdir, args.out)
     elif args.cmd == "rerun":
         rerun_noisy(args.binary, args.corpus, args.mtxdir, args.results)
-    elif args.cmd == "table":
-        table(args.results)
+    elif args.cmd == "report":
+        report(args.results)
     else:
         sweep(args.corpus, args.mtx_dir, args.tag, tuple(args.O), args.tileK, args.segw,
               args.warmup, args.reps, binary=args.binary)
