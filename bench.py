@@ -14,7 +14,12 @@ C = A.B that never reads C), with its HBM roofline, matrix-core fraction, hipSPA
 the same GPU in the same run, the row-sample parity check, and the reference's CPU SpMM
 (main.cpp:202-207, restated in the oracle) timed on this host on a bounded sample.
 
-Prints one JSON line.
+Every timed region (K launches after W warm-ups) is preceded by about 30 ms of untimed
+launches, so that it measures the GPU's steady state rather than the power transient that
+follows an idle period; the launch count is `settle_launches`.  The reference protocol's single
+launches (median of 10 after 3 warm-ups) are taken as the reference takes them.
+
+Prints one JSON line; its last keys, and the last lines of stderr, summarise every workload.
 """
 from __future__ import annotations
 
@@ -41,6 +46,7 @@ HEADLINE = 2
 TRAFFIC_SOURCES = ("vcsr_mc_amd/csrc/spmm_kernels.hip", "vcsr_mc_amd/csrc/format_build.hip",
                    "vcsr_mc_amd/csrc/row_groups.hip", "vcsr_mc_amd/csrc/internal.hpp")
 PARITY_ROWS = 2000
+SETTLE_MS = 30.0  # untimed GPU time before the warm-up launches of every timed region
 
 
 def log(*a):
@@ -99,10 +105,33 @@ def measured_traffic(key: str):
     return int(e["bytes"]), d["sources_sha256_16"]
 
 
-def timed_steps(run, steps, warmup, stream):
-    """W untimed launches, then K launches bracketed by a synchronisation on both sides; the
-    K launches are also bracketed by two HIP events on the launch stream."""
+def settle(run, stream, ms=SETTLE_MS):
+    """Untimed launches for about `ms` of GPU time.  After the GPU has idled (workload
+    generation, CPU baseline), a heavy kernel's first few launches run fast, the next few tens
+    slower (block FP32, 262,144^2 at O = 256, measured launch by launch after 3 s idle: ~270 us,
+    then ~320 us at launches 10-19 and ~288 us at 20-49, then 265 us from launch 50 on); the
+    timed region measures the steady state.  Returns the number of launches."""
     import torch
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    n, spent = 0, 0.0
+    while spent < ms:
+        batch = 1 if n == 0 else max(1, min(4096, n))
+        e0.record(stream)
+        for _ in range(batch):
+            run()
+        e1.record(stream)
+        e1.synchronize()
+        spent += e0.elapsed_time(e1)
+        n += batch
+    return n
+
+
+def timed_steps(run, steps, warmup, stream):
+    """A settling phase (see settle), W untimed launches, then K launches bracketed by a
+    synchronisation on both sides; the K launches are also bracketed by two HIP events on the
+    launch stream.  Returns (wall ms per step, event ms per step, settling launches)."""
+    import torch
+    settled = settle(run, stream)
     for _ in range(warmup):
         run()
     torch.cuda.synchronize()
@@ -114,7 +143,7 @@ def timed_steps(run, steps, warmup, stream):
     e1.record(stream)
     torch.cuda.synchronize()
     t1 = time.perf_counter()
-    return (t1 - t0) * 1e3 / steps, e0.elapsed_time(e1) / steps
+    return (t1 - t0) * 1e3 / steps, e0.elapsed_time(e1) / steps, settled
 
 
 def sub_csr(rp, col, val, rows, np):
@@ -268,7 +297,7 @@ def run_config(cfg, args, stream, want_cpu, cpu_seconds, prec_override=None):
             stream.wait_stream(cap)
             run = graph.replay
         C.zero_()
-        ms_per_step, kernel_ms = timed_steps(run, args.steps, args.warmup, stream)
+        ms_per_step, kernel_ms, settled = timed_steps(run, args.steps, args.warmup, stream)
         achieved = bytes_alg / (kernel_ms * 1e-3) / 1e9
         traffic, stamp = measured_traffic(f"config{cfg}-{prec}-{mode}") if full else \
             (None, "measured at the full workload only")
@@ -281,6 +310,7 @@ def run_config(cfg, args, stream, want_cpu, cpu_seconds, prec_override=None):
         ref_tf = f_pad / (kernel_ms * 1e-3) / 1e12
         out[mode] = {
             "ms_per_step": round(ms_per_step, 6),
+            "settle_launches": settled,
             "gflops": round(flops / (ms_per_step * 1e-3) / 1e9, 2),
             "kernel_ms": round(kernel_ms, 6),
             "kernel_gflops": round(flops / (kernel_ms * 1e-3) / 1e9, 2),
@@ -393,6 +423,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "settle_ms_before_warmup": SETTLE_MS,
         "ms_per_step": h["ms_per_step"],
         "higher_is_better": True,
         "scaling": "weak",

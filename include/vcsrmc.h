@@ -136,10 +136,12 @@ int vcsrmc_spmm(vcsrmc_t h, const void *dB, int b_dtype, int O, int tileK, float
 
 /* vcsrmc_spmm with flags; flags = 0 is vcsrmc_spmm (C += A.B).  VCSRMC_SPMM_OVERWRITE writes
  * C = A.B on every row that holds a nonzero of A and leaves the other rows as they are, so it
- * never reads C: it equals zeroing C and calling vcsrmc_spmm, bit for bit (the reference's
- * measured protocol, src/main.cpp:242-245), and saves the read of C.  Where a 16-row panel of A
- * is split across work-groups (panels of very many 32-column tiles), its rows are first set to
- * zero by a small kernel on `stream`.  No counterpart in the reference, whose kernels always
+ * never reads C: it equals zeroing C and calling vcsrmc_spmm (the reference's measured protocol,
+ * src/main.cpp:242-245), and saves the read of C.  Equal bit for bit on every row outside split
+ * panels; where a 16-row panel of A is split across work-groups (panels of very many 32-column
+ * tiles), its rows are first set to zero by a small kernel on `stream` and its work-groups add
+ * into them with float atomics in no fixed order, so those rows agree within rounding (as two
+ * runs of either call may).  No counterpart in the reference, whose kernels always
  * accumulate into C with atomicAdd (src/vcsr_mc.cu:228-234). */
 int vcsrmc_spmm_ex(vcsrmc_t h, const void *dB, int b_dtype, int O, int tileK, float *dC,
                    int flags, void *stream, float *ms);
@@ -156,8 +158,9 @@ int vcsrmc_spmm_ex(vcsrmc_t h, const void *dB, int b_dtype, int O, int tileK, fl
  * need more returns VCSRMC_ERR_SCRATCH before launching anything.  Every call on one GPU shares
  * that GPU's scratch, so calls that overlap on one GPU (several streams or threads) race; the
  * scratch keeps the last call's contents, and nothing in it needs to start at zero.  No timing
- * events: the launch is asynchronous on `stream`.  Same results as vcsrmc_spmm_ex, bit for
- * bit, under the same arguments. */
+ * events: the launch is asynchronous on `stream`.  Same results as vcsrmc_spmm_ex under the
+ * same arguments: bit for bit outside split panels, within rounding on their rows (float
+ * atomics in no fixed order, see vcsrmc_spmm_ex). */
 int vcsrmc_spmm_noalloc(vcsrmc_t h, const void *dB, int b_dtype, int O, int tileK, float *dC,
                         int flags, void *stream);
 

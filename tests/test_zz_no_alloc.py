@@ -1,7 +1,8 @@
 """vcsrmc_spmm_noalloc (the entry point that allocates nothing) against vcsrmc_spmm_ex, through
 the C ABI: bit for bit on two calls in a row, the second with a smaller input, for the launch
 that converts an FP32 B into the static scratch (FP16 format) and for launches that need no
-scratch; an input whose conversion exceeds the scratch is refused before anything runs."""
+scratch; an input whose conversion exceeds the scratch is refused before anything runs; and the
+call leaves the device's free memory unchanged where vcsrmc_spmm_ex allocates."""
 import ctypes as C
 
 import numpy as np
@@ -93,3 +94,34 @@ def test_noalloc_refuses_oversized_conversion():
         assert b"static scratch" in vm.lib().vcsrmc_last_error()
         torch.cuda.synchronize()
         assert bool(torch.all(Cout == 2.0))
+
+
+def test_noalloc_allocates_nothing():
+    """On a fresh FP16-format handle given an FP32 B that the launch converts, the first
+    vcsrmc_spmm_noalloc call leaves the device's free memory where it was; the first
+    vcsrmc_spmm_ex call on the same handle then allocates the N x O binary16 copy, which the
+    same measurement sees.  (A first call on another handle loads the kernels beforehand, so
+    code loading does not count.)"""
+    import torch
+    M, O = 30000, 128
+    rng = np.random.default_rng(43)
+    rp, c, v = random_csr(rng, M, M, nnz_per_row=16)
+    B = rng.uniform(-1, 1, (M, O)).astype(np.float32)
+    dB = dev(B)
+    C0 = torch.zeros((M, O), dtype=torch.float32, device="cuda")
+    say("noalloc allocates nothing", M, O)
+    with vm.DeviceFormat.from_device_csr(dev(rp), dev(c), dev(v), M, M, False, 32) as warm:
+        assert _converts(len(c), M, O, warm.info()["num_chunks"])
+        assert _noalloc(warm, dB, C0, O) == vm.OK, vm.lib().vcsrmc_last_error()
+        torch.cuda.synchronize()
+    with vm.DeviceFormat.from_device_csr(dev(rp), dev(c), dev(v), M, M, False, 32) as f:
+        torch.cuda.synchronize()
+        free0 = torch.cuda.mem_get_info()[0]
+        assert _noalloc(f, dB, C0, O) == vm.OK, vm.lib().vcsrmc_last_error()
+        torch.cuda.synchronize()
+        free1 = torch.cuda.mem_get_info()[0]
+        f.spmm(dB, C0, tileK=128)
+        torch.cuda.synchronize()
+        free2 = torch.cuda.mem_get_info()[0]
+    assert free0 - free1 < M * O * 2, (free0, free1)
+    assert free1 - free2 >= M * O * 2, (free1, free2)

@@ -20,6 +20,7 @@ from __future__ import annotations
 
 import ctypes as C
 import os
+import weakref
 from dataclasses import dataclass, field
 
 import numpy as np
@@ -558,9 +559,28 @@ def dense(n_rows: int, n_cols: int, seed: int, dist: int = 0, fp16_exact: bool =
     return out
 
 
+# The A operand of the hipSPARSE plans the bench library keeps: weak references to the tensors
+# and their version counters.  The library keys plans by device address, so a new matrix at a
+# reused address would find another matrix's analysis; the session is released first whenever
+# A is not the same live tensors, unmodified.
+_rs_matrix = None
+
+
+def _rs_same_matrix(tensors) -> bool:
+    global _rs_matrix
+    now = [(weakref.ref(t), t._version) for t in tensors]
+    same = _rs_matrix is not None and all(r() is t and v == t._version
+                                          for (r, v), t in zip(_rs_matrix, tensors))
+    _rs_matrix = now
+    return same
+
+
 def rocsparse_spmm(M, N, row_ptr, col, val, B, C_out, alpha=1.0, alg=0, stream=None):
-    """hipSPARSE SpMM C = alpha A.B (beta 0) on device tensors; returns (ms, setup_ms)."""
+    """hipSPARSE SpMM C = alpha A.B (beta 0) on device tensors; returns (ms, setup_ms).  Plans
+    (descriptors, buffer, preprocess analysis) are kept while A is the same tensors."""
     import torch
+    if not _rs_same_matrix((row_ptr, col, val)):
+        bench_lib().vcsrmc_rocsparse_release()
     ms, setup = C.c_float(0.0), C.c_float(0.0)
     rc = bench_lib().vcsrmc_rocsparse_spmm(
         int(M), int(N), int(col.numel()), _ptr(row_ptr), _ptr(col), _ptr(val),

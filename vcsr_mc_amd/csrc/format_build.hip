@@ -486,7 +486,7 @@ __global__ void k_row_step_fill(const int* __restrict__ cbase, const int* __rest
         const int t = s & 7;
         // FP32 tiles keep their columns in K-step order: column k at slot (k & 3) * 8 + k / 4
         rs_cols[32 * b + 8 * g + t] = chunk_cols[c * kChunkCols + (k & 3) * 8 + (k >> 2)];
-        rs_vals[256 * b + 64 * g + 8 * x + t] = __uint_as_float(entries[2 * (long long)e + 1]);
+        rs_vals[128 * b + 32 * g + 8 * x + t] = __uint_as_float(entries[2 * (long long)e + 1]);
     }
 }
 
@@ -738,9 +738,9 @@ static void build_exec_layout_k(DeviceFormat& F, const int* trow, const int* tco
         NB = read_scalar(rbase.p + NP, st);
         if (NB > 0) {
             F.rs_cols.alloc((size_t)NB * kChunkCols);
-            F.rs_vals.alloc((size_t)NB * 256);
+            F.rs_vals.alloc((size_t)NB * 128);
             fill<int>(F.rs_cols.p, (long long)NB * kChunkCols, -1, st);
-            fill<float>(F.rs_vals.p, (long long)NB * 256, 0.0f, st);
+            fill<float>(F.rs_vals.p, (long long)NB * 128, 0.0f, st);
             LAUNCH(k_row_step_fill, NC, cbase.p, rbase.p, nbat.p, rsmask.p, rspre.p,
                    F.chunk_eptr.p, F.entries.p, F.chunk_cols.p, NP, NC, F.rs_cols.p, F.rs_vals.p);
             // a panel's work items: its batches where it takes row steps, else its tiles

@@ -71,7 +71,7 @@ struct XcdSplit {
 //                   -1 after the last; a panel has as many steps as its busiest row group has
 //                   columns, rounded up to 8.  rs_cols[32b + 8g + t] = the column of step t of
 //                   batch b for row group g (the slots the tile path's lane group g reads), and
-//                   rs_vals[256b + 64g + 8x + t] = the value of row 4g + x at that column (0 if
+//                   rs_vals[128b + 32g + 8x + t] = the value of row 4g + x at that column (0 if
 //                   the row does not hold it), so a lane reads its eight A values with two
 //                   128-bit loads.  A panel takes row steps when its batches are at most
 //                   kRowStepRatioNum / kRowStepRatioDen times its tiles: each step costs a

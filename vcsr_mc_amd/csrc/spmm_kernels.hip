@@ -701,7 +701,7 @@ __device__ __forceinline__ void a_operand_f32(const TileMeta& m, const AState32&
 //   4. load X (c + 2W), A state; multiply steps 4-7 of d (Y); load columns of c + 3W
 //
 // RS: the unit's work items are row-step batches instead (column slots in chunk_cols = rs_cols,
-// A values in dense_a = rs_vals, 256 per batch, this lane's eight at 64 g + 8 (lane & 3)), with
+// A values in dense_a = rs_vals, 128 per batch, this lane's eight at 32 g + 8 (lane & 3)), with
 // the same loads of columns and B rows and mfma_half_rs as the product.
 template <int TK, bool ALIGNED, bool RS, typename Pre>
 __device__ __forceinline__ void tiles_f32(int first, int end, int W, int lane, int n, int g,
@@ -715,7 +715,7 @@ __device__ __forceinline__ void tiles_f32(int first, int end, int W, int lane, i
     constexpr int VEC = TK / 16;
     if (first >= end) return;
     const int a_off = g * 128 + n * 8;  // in a dense copy
-    const int rs_off = g * 64 + (lane & 3) * 8;  // in a row-step batch
+    const int rs_off = g * 32 + (lane & 3) * 8;  // in a row-step batch
     float* my_a = &Aw[g * kAgroup32 + n * kApitch32];
     auto meta = [&](int c) {
         if constexpr (RS) return TileMeta{c, 0, 0};
@@ -723,7 +723,7 @@ __device__ __forceinline__ void tiles_f32(int first, int end, int W, int lane, i
     };
     auto load_a = [&](const TileMeta& m) {
         if constexpr (RS) {
-            const float* p = dense_a + (long long)m.d * 256 + rs_off;
+            const float* p = dense_a + (long long)m.d * 128 + rs_off;
             return AState32{*reinterpret_cast<const uint4*>(p),
                             *reinterpret_cast<const uint4*>(p + 4)};
         } else {
