@@ -15,8 +15,9 @@ extern "C" {
  *   1 uniform   n x n, n = size (4096); nnz per row ~ Poisson(16) clipped to [0, n], distinct
  *               uniform columns (Floyd); values U[-1,1] FP32
  *   2 powerlaw  n x n, n = size (36692); symmetric pattern from a configuration model with
- *               degrees Zipf(2.1) on [1, 1383] scaled to 368000 * n / 36692 stubs; self loops
- *               and duplicates dropped; values U[-1,1] rounded to FP16
+ *               degrees Zipf(2.1) on [1, 1383], scaled so that about 368000 * n / 36692
+ *               nonzeros remain after self loops and duplicates are dropped (367,570 at the
+ *               full size); values U[-1,1] rounded to FP16
  *   3 stencil   27-point stencil on a g^3 grid, g = size (100), natural order; diagonal 26,
  *               off-diagonals -1
  *   4 block     nb block rows of height 32, nb = size (8192), each with 4 distinct uniform
