@@ -104,6 +104,37 @@ def test_fp16_b_matches_fp32_b(orc, M, N, kw):
     check(orc, rp, c, v, M, N, B, False, b16=True)
 
 
+@pytest.mark.parametrize("O,tileK", [(128, 128), (256, 128), (192, 64), (128, 32), (160, 128)])
+def test_converted_b_o_tile_major(orc, O, tileK):
+    """An FP16 format given FP32 B above the conversion threshold rounds B to binary16 in one
+    pass per call, laid out O-tile-major where the launch has several O tiles, all full (O tiles
+    of 64 here for 128, 256 and 192 columns, of 32 at tileK 32) and row-major otherwise (160
+    columns, O tiles of 64): the result equals the launch on the same B rounded by the caller,
+    bit for bit, in both launch modes, and meets the parity norm."""
+    import torch
+    rng = np.random.default_rng(O + tileK)
+    M = 30000
+    rp, c, v = random_csr(rng, M, M, nnz_per_row=16)
+    B = rng.uniform(-2, 2, (M, O)).astype(np.float32)
+    say("converted B, O-tile-major", O, tileK, len(c))
+    with vm.DeviceFormat.from_device_csr(dev(rp), dev(c), dev(v), M, M, False, 32) as f:
+        info = f.info()
+        assert info["num_units"] == info["num_panels"]  # no split panel: no atomics
+        assert len(c) >= 12 * M and len(c) < 48 * info["num_chunks"] and M * O * 4 > 12 << 20
+        tile = f.traffic_floor(O, tileK=tileK, b_f16=False)["o_tile_width"]
+        assert (O % tile == 0 and O > tile) == (O != 160)
+        dB = dev(B)
+        for overwrite in (False, True):
+            C1 = torch.full((M, O), 0.25, dtype=torch.float32, device="cuda")
+            C2 = C1.clone()
+            f.spmm(dB, C1, tileK=tileK, overwrite=overwrite)
+            f.spmm(dB.half(), C2, tileK=tileK, overwrite=overwrite)
+            torch.cuda.synchronize()
+            assert torch.equal(C1, C2), overwrite
+        assert np.array_equal(dB.cpu().numpy(), B)
+    check(orc, rp, c, v, M, M, B, False, tileK=tileK)
+
+
 def test_scaled_values(orc):
     """|A| > 60000: A is divided by the range scale before FP16 and C multiplied back."""
     rng = np.random.default_rng(13)

@@ -202,6 +202,7 @@ struct SpmmPlan {
     bool b_f16 = false, accumulate = true, zero_split = false, launch = false;
     _Float16* convert_to = nullptr;  // FP32 B converted into this binary16 buffer first
     long long convert_n = 0;
+    bool b_tiled = false;  // ... and laid out O-tile-major ([O tile][N][tk]; every O tile full)
 };
 SpmmPlan plan_spmm(const DeviceFormat& F, const void* dB, bool b_f16, int O, int tileK, float* dC,
                    bool accumulate, HalfScratch ext = HalfScratch());
