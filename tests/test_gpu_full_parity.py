@@ -2,7 +2,8 @@
 
 For each workload (uniform 4096^2, power-law 36,692^2, 27-point stencil 100^3, 32 x 32 blocks
 262,144^2 at O = 256, R-MAT scale 22), in the precision it is configured for and in the other
-one (the reference's driver runs both kernels on every matrix, src/main.cpp:345), in both launch
+one (the reference's driver runs both kernels on every matrix, src/main.cpp:345), and for the
+FP16 workloads also their own kernel fed FP32 B (the reference's interface), in both launch
 modes (C += A.B from C = 0, and C = A.B over a C holding 9.0), every row of C is checked with the
 parity norm, per row r:
     ||C[r,:] - C_ref[r,:]||_1 <= tau * sum_k sum_p |a_rp b_{c_p,k}|,
@@ -40,26 +41,33 @@ def split_rows(f):
     return np.unique(np.concatenate(rows)) if rows else np.zeros(0, np.int64)
 
 
-@pytest.mark.parametrize("config", [1, 2, 3, 4, 5])
-@pytest.mark.parametrize("second", [False, True])
-def test_every_row_full_size(orc, config, second):
+# (config, variant): "configured" -- the workload's precision, FP16 formats fed FP16 B;
+# "second" -- the other kernel of the reference's driver (src/main.cpp:345), fed FP32 B as
+# run_vcsr_mc_spmm_gpu is; "fp32_b" -- an FP16 workload's own kernel fed FP32 B through that
+# same reference interface (R-MAT and the blocks convert B once per call, O-tile-major;
+# power-law reads FP32 rows directly).
+CASES = [(c, v) for v in ("configured", "second") for c in (1, 2, 3, 4, 5)] + \
+        [(c, "fp32_b") for c in (2, 4, 5)]
+
+
+@pytest.mark.parametrize("config,variant", CASES)
+def test_every_row_full_size(orc, config, variant):
     import torch
     w = vm.WORKLOADS[config]
     configured_fp32 = w["precision"] == "fp32"
+    second = variant == "second"
     fp32 = configured_fp32 != second
     A = workload(config)
     O = w["O"]
-    if second:
-        # the other kernel of the reference's driver, fed FP32 B as run_vcsr_mc_spmm_gpu is
-        B = vm.dense(A.N, O, seed=vm.SEED_BASE + 200 + config)
-        b16 = False
-    else:
+    if variant == "configured":
         B = vm.dense(A.N, O, seed=vm.SEED_BASE + 100 + config, fp16_exact=not fp32)
         b16 = not fp32
+    else:
+        B = vm.dense(A.N, O, seed=vm.SEED_BASE + 200 + config)
+        b16 = False
     deg = np.diff(A.row_ptr)
     nonempty = deg > 0
-    say("full-C parity", config, "fp32" if fp32 else "fp16", "second" if second else "configured",
-        A.M, A.nnz, O)
+    say("full-C parity", config, "fp32" if fp32 else "fp16", variant, A.M, A.nnz, O)
     mode = 0 if fp32 else 1
     with vm.DeviceFormat.from_device_csr(dev(A.row_ptr), dev(A.col), dev(A.val), A.M, A.N,
                                          fp32, 32) as f:
