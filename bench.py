@@ -251,7 +251,7 @@ def run_config(cfg, args, stream, want_cpu, cpu_seconds, prec_override=None):
     # algorithmic bytes: A values and columns, row pointers, each distinct B row once (in the
     # type B is held in), each non-empty C row written once
     bytes_alg = A.nnz * (s_a + 4) + (A.M + 1) * 4 + U * O * s_b + M_ne * O * 4
-    # Matrix-core work: the 16 x 32 tiles this build multiplies (each against O columns of B),
+    # Matrix-core work: the 16 x 32 tiles of the execution layout (each against O columns of B),
     # and, for comparison, the reference's padded 16 x segw groups.
     f_exec = info["num_chunks"] * 2.0 * 16 * 32 * O
     f_pad = info["num_groups"] * 2.0 * 16 * SEGW * O
@@ -451,7 +451,7 @@ def main():
                                 if l.startswith("model name")][0]
         except Exception:
             out["cpu_model"] = "unknown"
-    # the BASELINE target: geomean over workloads 1-4 of rocSPARSE FP32 time / ours, each at its
+    # the target: geomean over workloads 1-4 of rocSPARSE FP32 time / ours, each at its
     # configured precision, reference protocol (median single launch)
     if not args.no_rocsparse:
         for mode in modes:

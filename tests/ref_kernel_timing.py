@@ -1,5 +1,5 @@
 """Times the reference's own VCSR-MC kernels against this library's, with the reference's driver
-and protocol on both sides (run on the GPU box; not a pytest module).
+and protocol on both sides (run on a machine with an MI355X; not a pytest module).
 
 * oracle/_ref/spmm_vcsr_ref:    the reference's src/main.cpp, src/kernels.cu and src/vcsr_mc.cu,
                                 built as-is for gfx950 (`make -C oracle ref`);
