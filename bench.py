@@ -16,7 +16,10 @@ the same GPU in the same run, the row-sample parity check, and the reference's C
 
 Every timed region (K launches after W warm-ups) is preceded by about 30 ms of untimed
 launches, so that it measures the GPU's steady state rather than the power transient that
-follows an idle period; the launch count is `settle_launches`.  The reference protocol's single
+follows an idle period; the launch count is `settle_launches`.  The K timed launches are
+captured into one HIP graph after the warm-ups and replayed once between the synchronisations
+(`--eager` enqueues them one by one instead): the smallest workload's kernel is shorter than the
+host's enqueue of a launch.  The reference protocol's single
 launches (median of 10 after 3 warm-ups) are taken as the reference takes them.
 
 Prints one JSON line; its last keys, and the last lines of stderr, summarise every workload.
@@ -74,8 +77,9 @@ def parse():
                    help="CPU-baseline time budget, shared by the workloads")
     p.add_argument("--b-fp32", action="store_true",
                    help="FP16 formats read B in FP32 (the reference's run_vcsr_mc_spmm_gpu path)")
-    p.add_argument("--graph", action="store_true",
-                   help="replay the timed steps from a captured HIP graph")
+    p.add_argument("--eager", action="store_true",
+                   help="enqueue the timed launches one by one instead of replaying them from "
+                        "one captured HIP graph")
     p.add_argument("--copy-probe-mib", type=int, default=0,
                    help="also run a plain device copy of this size (PMC traffic calibration)")
     return p.parse_args()
@@ -126,20 +130,30 @@ def settle(run, stream, ms=SETTLE_MS):
     return n
 
 
-def timed_steps(run, steps, warmup, stream):
+def timed_steps(run, steps, warmup, stream, capture=None):
     """A settling phase (see settle), W untimed launches, then K launches bracketed by a
     synchronisation on both sides; the K launches are also bracketed by two HIP events on the
-    launch stream.  Returns (wall ms per step, event ms per step, settling launches)."""
+    launch stream.  With `capture` (a function of K returning a callable), the K launches are
+    captured into one HIP graph after the warm-ups and the timed region replays it once: the
+    same K launches, without the host enqueueing each (the smallest workload's 5 us kernel is
+    shorter than one enqueue: 4-6 us per launch through the API, ~14 us in a cold loop's first
+    iterations; a graph of 20 launches runs them at 5.5 us each).  Returns (wall ms per step,
+    event ms per step, settling launches)."""
     import torch
     settled = settle(run, stream)
     for _ in range(warmup):
         run()
     torch.cuda.synchronize()
+    timed = capture(steps) if capture is not None else None
+    torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     e0.record(stream)
-    for _ in range(steps):
-        run()
+    if timed is not None:
+        timed()
+    else:
+        for _ in range(steps):
+            run()
     e1.record(stream)
     torch.cuda.synchronize()
     t1 = time.perf_counter()
@@ -217,6 +231,7 @@ def run_config(cfg, args, stream, want_cpu, cpu_seconds, prec_override=None):
     O = args.O or w["O"]
     dev = torch.device("cuda:0")
     modes = [m for m in args.modes.split(",") if m]
+    graphs = []
 
     t = time.time()
     A = vm.generate(cfg, args.size)
@@ -272,8 +287,9 @@ def run_config(cfg, args, stream, want_cpu, cpu_seconds, prec_override=None):
     for mode in modes:
         ow = mode == "overwrite"
 
-        def step(ow=ow):
-            fmt.spmm(dB, C, tileK=args.tileK, O=O, stream=stream, overwrite=ow)
+        # the timed launches go through a pre-bound launcher: the checks of fmt.spmm take
+        # longer than the smallest workload's kernel, and the loop must keep the GPU fed
+        step = fmt.launcher(dB, C, tileK=args.tileK, O=O, stream=stream, overwrite=ow)
 
         # reference protocol: median of 10 event-timed single launches after 3 warm-ups, C
         # zeroed outside the timing (main.cpp:239-298)
@@ -287,17 +303,22 @@ def run_config(cfg, args, stream, want_cpu, cpu_seconds, prec_override=None):
         parity = (row_sample_parity(A, Bh, C, fp32, info["scale"], oracle, np, torch)
                   if oracle is not None else None)
 
-        run = step
-        if args.graph:
+        def capture(k, ow=ow):
+            """The k timed launches as one HIP graph, replayed on the launch stream (the
+            launch enqueues kernels only: no allocation, no memset)."""
             graph = torch.cuda.CUDAGraph()
             cap = torch.cuda.Stream()
             cap.wait_stream(stream)
             with torch.cuda.graph(graph, stream=cap):
-                fmt.spmm(dB, C, tileK=args.tileK, O=O, stream=cap, overwrite=ow)
+                for _ in range(k):
+                    fmt.spmm(dB, C, tileK=args.tileK, O=O, stream=cap, overwrite=ow)
             stream.wait_stream(cap)
-            run = graph.replay
+            graphs.append(graph)  # kept until the workload's buffers are freed
+            return graph.replay
+
         C.zero_()
-        ms_per_step, kernel_ms, settled = timed_steps(run, args.steps, args.warmup, stream)
+        ms_per_step, kernel_ms, settled = timed_steps(step, args.steps, args.warmup, stream,
+                                                      None if args.eager else capture)
         achieved = bytes_alg / (kernel_ms * 1e-3) / 1e9
         traffic, stamp = measured_traffic(f"config{cfg}-{prec}-{mode}") if full else \
             (None, "measured at the full workload only")
@@ -311,6 +332,7 @@ def run_config(cfg, args, stream, want_cpu, cpu_seconds, prec_override=None):
         out[mode] = {
             "ms_per_step": round(ms_per_step, 6),
             "settle_launches": settled,
+            "timed_launches": "enqueued one by one" if args.eager else "one HIP graph of K",
             "gflops": round(flops / (ms_per_step * 1e-3) / 1e9, 2),
             "kernel_ms": round(kernel_ms, 6),
             "kernel_gflops": round(flops / (kernel_ms * 1e-3) / 1e9, 2),
@@ -365,6 +387,7 @@ def run_config(cfg, args, stream, want_cpu, cpu_seconds, prec_override=None):
             A, Bh, O, cpu_seconds, oracle, np)
         log(f"[config {cfg}] CPU baseline {out['cpu_baseline']['value']} GFLOP/s (1 core)")
 
+    del graphs[:]
     fmt.close()
     del C, dB, dB32, d_rp, d_col, d_val
     torch.cuda.empty_cache()
@@ -424,6 +447,7 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "settle_ms_before_warmup": SETTLE_MS,
+        "timed_launches": "enqueued one by one" if args.eager else "one HIP graph of K launches",
         "ms_per_step": h["ms_per_step"],
         "higher_is_better": True,
         "scaling": "weak",

@@ -135,6 +135,29 @@ def test_converted_b_o_tile_major(orc, O, tileK):
     check(orc, rp, c, v, M, M, B, False, tileK=tileK)
 
 
+@pytest.mark.parametrize("overwrite", [False, True])
+def test_launcher_equals_spmm(overwrite):
+    """The pre-bound launcher (checks and argument conversion once) enqueues the same launch as
+    spmm: the same C bit for bit over repeated calls, and a bad tileK is reported when called."""
+    import torch
+    rng = np.random.default_rng(21)
+    rp, c, v = random_csr(rng, 3000, 2500, density=0.01)
+    B = dev(rng.uniform(-1, 1, (2500, 96)).astype(np.float32)).half()
+    say("launcher", overwrite)
+    with vm.DeviceFormat.from_device_csr(dev(rp), dev(c), dev(v), 3000, 2500, False, 32) as f:
+        C1 = torch.full((3000, 96), 0.5, dtype=torch.float32, device="cuda")
+        C2 = C1.clone()
+        go = f.launcher(B, C2, tileK=64, overwrite=overwrite)
+        for _ in range(3):
+            f.spmm(B, C1, tileK=64, overwrite=overwrite)
+            go()
+        torch.cuda.synchronize()
+        assert torch.equal(C1, C2)
+        bad = f.launcher(B, C2, tileK=48)
+        with pytest.raises(vm.VCSRMCError):
+            bad()
+
+
 def test_scaled_values(orc):
     """|A| > 60000: A is divided by the range scale before FP16 and C multiplied back."""
     rng = np.random.default_rng(13)

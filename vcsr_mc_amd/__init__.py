@@ -362,10 +362,8 @@ class DeviceFormat:
                       num_segments=i["num_segments"], scale=float(np.float32(i["scale"])),
                       fp32=bool(i["fp32"]), **out)
 
-    def spmm(self, B, C_out, tileK=128, O=None, stream=None, timed=False, overwrite=False):
-        """C_out += A . B on the GPU (overwrite: C_out = A . B on the rows A touches, C_out
-        not read).  B: (N, O) float32 or float16 device tensor; C_out: (M, O) float32.
-        Returns the event-timed kernel time in ms when timed, else None."""
+    def _operands(self, B, C_out, O):
+        """Checks B and C_out for a multiply of width O (None: B's); returns (B dtype code, O)."""
         import torch
         b_dtype = B_F16 if B.dtype == torch.float16 else B_F32
         if B.dtype not in (torch.float16, torch.float32) or C_out.dtype != torch.float32:
@@ -382,6 +380,33 @@ class DeviceFormat:
         if O < 0 or B.numel() < N * O or C_out.numel() < M * O:
             raise VCSRMCError(ERR_ARG, f"B needs N x O = {N} x {O} and C M x O = {M} x {O} "
                                        f"elements; got {B.numel()} and {C_out.numel()}")
+        return b_dtype, O
+
+    def launcher(self, B, C_out, tileK=128, O=None, stream=None, overwrite=False):
+        """A callable with no arguments that enqueues spmm(B, C_out, ...) asynchronously, with
+        the checks and the ctypes conversions done once here: for loops of launches whose
+        kernels are shorter than the checks (a 6 us multiply).  It holds B and C_out."""
+        b_dtype, O = self._operands(B, C_out, O)
+        fn = lib().vcsrmc_spmm_ex
+        args = (self.handle, C.c_void_p(_ptr(B)), C.c_int(b_dtype), C.c_int(O),
+                C.c_int(int(tileK)), C.c_void_p(_ptr(C_out)),
+                C.c_int(SPMM_OVERWRITE if overwrite else 0), C.c_void_p(_stream_ptr(stream)),
+                None)
+        keep = (B, C_out)
+
+        def launch():
+            rc = fn(*args)
+            if rc != 0:
+                _check(rc, "vcsrmc_spmm")
+            return keep is not None
+
+        return launch
+
+    def spmm(self, B, C_out, tileK=128, O=None, stream=None, timed=False, overwrite=False):
+        """C_out += A . B on the GPU (overwrite: C_out = A . B on the rows A touches, C_out
+        not read).  B: (N, O) float32 or float16 device tensor; C_out: (M, O) float32.
+        Returns the event-timed kernel time in ms when timed, else None."""
+        b_dtype, O = self._operands(B, C_out, O)
         ms = C.c_float(0.0)
         _check(lib().vcsrmc_spmm_ex(self.handle, _ptr(B), b_dtype, O, int(tileK), _ptr(C_out),
                                     SPMM_OVERWRITE if overwrite else 0, _stream_ptr(stream),
