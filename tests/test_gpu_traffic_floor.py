@@ -85,3 +85,33 @@ def test_floor_counts_split_panels_and_row_steps(orc):
             assert t["a_bytes"] >= (16 * info["num_units"] + 640 * batches) * t["o_tiles"]
     finally:
         vm.set_fp32_row_steps(1)
+
+
+def test_floor_and_units_edge_cases():
+    """An empty matrix has no units and a zero floor; a bad tileK and FP16 B for an FP32 format
+    are refused with the launch's own errors; units of a 3-row matrix cover its rows."""
+    import torch
+    rp = np.zeros(6, np.int32)
+    say("traffic floor: edge cases")
+    with vm.DeviceFormat.from_device_csr(dev(rp), dev(np.zeros(0, np.int32)),
+                                         dev(np.zeros(0, np.float32)), 5, 7, False, 32) as f:
+        units, xs = f.units()
+        assert units.shape == (0, 4) and xs.tolist() == [0] * 9
+        t = f.traffic_floor(128)
+        assert t["total"] == 0 and t["b_bytes"] == 0 and t["c_bytes"] == 0
+    rp = np.array([0, 2, 2, 5], np.int32)
+    c = np.array([0, 9, 1, 2, 9], np.int32)
+    v = np.ones(5, np.float32)
+    with vm.DeviceFormat.from_device_csr(dev(rp), dev(c), dev(v), 3, 10, True, 32) as f:
+        units, _ = f.units()
+        rows = np.unique(np.concatenate(f.rows_of_units(units)))
+        assert rows.tolist() == [0, 2]  # row 1 holds no nonzero
+        with pytest.raises(vm.VCSRMCError) as e:
+            f.traffic_floor(64, tileK=48)
+        assert e.value.status == vm.ERR_TILEK
+        with pytest.raises(vm.VCSRMCError) as e:
+            f.traffic_floor(64, b_f16=True)
+        assert e.value.status == vm.ERR_ARG
+        t = f.traffic_floor(64)
+        # four distinct columns, FP32 B, one row part holding them all, two rows of C
+        assert t["b_once_bytes"] == 4 * 64 * 4 and t["c_bytes"] == 2 * 64 * 4 * 2
