@@ -203,6 +203,7 @@ struct SpmmPlan {
     _Float16* convert_to = nullptr;  // FP32 B converted into this binary16 buffer first
     long long convert_n = 0;
     bool b_tiled = false;  // ... and laid out O-tile-major ([O tile][N][tk]; every O tile full)
+    bool nt_c = false;     // C += A.B reads C non-temporally (C and B beyond the last-level cache)
 };
 SpmmPlan plan_spmm(const DeviceFormat& F, const void* dB, bool b_f16, int O, int tileK, float* dC,
                    bool accumulate, HalfScratch ext = HalfScratch());

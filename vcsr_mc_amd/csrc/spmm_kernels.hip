@@ -154,7 +154,21 @@ struct CAhead {
     floatx4 v[N > 0 ? N : 1];
 };
 
-template <int TK, int W, typename PR>
+// Sixteen bytes of C read ahead: an ordinary load, or (NT) a non-temporal one, which neither L2
+// nor the last-level cache keeps.  Where C is larger than that cache can hold with B, ordinary
+// reads of C only evict the B rows and layout that later units reuse; where it fits (power-law
+// 36,692^2 at O = 128: 19 MB), back-to-back launches find C there.  Measured on gfx950, C += A.B
+// back to back, ordinary -> non-temporal: 32 x 32 blocks, 262,144^2 at O = 256, FP16 180 ->
+// 163 us, FP32 269 -> 254 us; 27-point stencil 100^3 FP32 426 -> 410 us; R-MAT scale 22 2.48
+// -> 2.42 ms; power-law 15.9 -> 17.4 us.  (NT is a template parameter: the compiler merges a
+// load whose kind a run-time flag selects into one ordinary load.)
+template <bool NT>
+__device__ __forceinline__ floatx4 load_c4(const float* p) {
+    if constexpr (NT) return __builtin_nontemporal_load(reinterpret_cast<const floatx4*>(p));
+    else return *reinterpret_cast<const floatx4*>(p);
+}
+
+template <int TK, int W, bool NT = false, typename PR>
 __device__ __forceinline__ void read_c_ahead(CAhead<TK, W>& ca, const int4& U,
                                              const PR& pr, int k0, int O, bool c4,
                                              bool accumulate, const float* __restrict__ C) {
@@ -174,7 +188,7 @@ __device__ __forceinline__ void read_c_ahead(CAhead<TK, W>& ca, const int4& U,
                 const long long cr = pr.row(row);
                 const bool in = accumulate && ((U.w >> row) & 1);
                 const float* src = in ? C + cr * OL + k0 + col : kZeroRow;
-                ca.v[j] = *reinterpret_cast<const floatx4*>(src);
+                ca.v[j] = load_c4<NT>(src);
             }
         } else if constexpr (VEC >= 4) {
             const int c0 = k0 + VEC * n;
@@ -187,7 +201,7 @@ __device__ __forceinline__ void read_c_ahead(CAhead<TK, W>& ca, const int4& U,
                 const float* src = in ? C + cr * OL + c0 : kZeroRow;
 #pragma unroll
                 for (int h = 0; h < VEC / 4; ++h)
-                    ca.v[i * (VEC / 4) + h] = *reinterpret_cast<const floatx4*>(src + 4 * h);
+                    ca.v[i * (VEC / 4) + h] = load_c4<NT>(src + 4 * h);
             }
         }
     } else {
@@ -198,7 +212,7 @@ __device__ __forceinline__ void read_c_ahead(CAhead<TK, W>& ca, const int4& U,
             const long long cr = pr.row(row);
             const bool in = ok && e < 16 * TK && ((U.w >> row) & 1) && cc + 4 <= O;
             const float* src = in ? C + cr * OL + cc : kZeroRow;
-            ca.v[j] = *reinterpret_cast<const floatx4*>(src);
+            ca.v[j] = load_c4<NT>(src);
         }
     }
 }
@@ -507,7 +521,7 @@ __device__ __forceinline__ void tiles_f16(int first, int end, int W, int lane, i
 template <typename TB, bool ALIGNED>
 constexpr int f16_min_waves() { return (sizeof(TB) == 2 && ALIGNED) ? 3 : 2; }
 
-template <int TK, typename TB, bool ALIGNED, bool ACC, bool MAPPED>
+template <int TK, typename TB, bool ALIGNED, bool ACC, bool MAPPED, bool NTC>
 __global__ __launch_bounds__(64 * kWaves, (f16_min_waves<TB, ALIGNED>())) void k_spmm_f16(
     const int4* __restrict__ units, const int* __restrict__ rmap, int num_heavy, XcdSplit xs,
     const int* __restrict__ chunk_eptr, const int* __restrict__ chunk_cols,
@@ -542,7 +556,7 @@ __global__ __launch_bounds__(64 * kWaves, (f16_min_waves<TB, ALIGNED>())) void k
     // counting sees one fixed sequence of loads on each.
     if (heavy) {
         CAhead<TK, kWaves> ca;
-        read_c_ahead<TK, kWaves>(ca, U, pr, k0, O, c4, ACC, C);
+        read_c_ahead<TK, kWaves, NTC>(ca, U, pr, k0, O, c4, ACC, C);
         tiles_f16<TK, TB, ALIGNED>(U.y + wave, U.z, kWaves, lane, n, g, cb, ldb,
                                    chunk_eptr, chunk_cols, chunk_dense, entries, dense_a, Bt,
                                    As[wave], acc, [] {});
@@ -551,7 +565,7 @@ __global__ __launch_bounds__(64 * kWaves, (f16_min_waves<TB, ALIGNED>())) void k
         CAhead<TK, 1> ca;
         tiles_f16<TK, TB, ALIGNED>(U.y, U.z, 1, lane, n, g, cb, ldb, chunk_eptr,
                                    chunk_cols, chunk_dense, entries, dense_a, Bt, As[wave], acc,
-                                   [&] { read_c_ahead<TK, 1>(ca, U, pr, k0, O, c4, ACC, C); });
+                                   [&] { read_c_ahead<TK, 1, NTC>(ca, U, pr, k0, O, c4, ACC, C); });
         merge_into_c<TK, 1, ACC>(acc, scale, U, pr, k0, O, c4, C, P, ca);
     }
 }
@@ -808,7 +822,7 @@ __device__ __forceinline__ void tiles_f32(int first, int end, int W, int lane, i
     }
 }
 
-template <int TK, bool ALIGNED, bool ACC, bool MAPPED>
+template <int TK, bool ALIGNED, bool ACC, bool MAPPED, bool NTC>
 __global__ __launch_bounds__(64 * kWaves, 3) void k_spmm_f32(
     const int4* __restrict__ units, const int* __restrict__ rmap, int num_heavy, XcdSplit xs,
     const int* __restrict__ chunk_eptr, const int* __restrict__ chunk_cols,
@@ -851,17 +865,19 @@ __global__ __launch_bounds__(64 * kWaves, 3) void k_spmm_f32(
     };
     if (heavy) {
         CAhead<TK, kWaves> ca;
-        read_c_ahead<TK, kWaves>(ca, U, pr, k0, O, c4, ACC, C);
+        read_c_ahead<TK, kWaves, NTC>(ca, U, pr, k0, O, c4, ACC, C);
         run(U.y + wave, kWaves, [] {});
         merge_into_c<TK, kWaves, ACC>(acc, 1.0f, U, pr, k0, O, c4, C, P, ca);
     } else {
         CAhead<TK, 1> ca;
-        run(U.y, 1, [&] { read_c_ahead<TK, 1>(ca, U, pr, k0, O, c4, ACC, C); });
+        run(U.y, 1, [&] { read_c_ahead<TK, 1, NTC>(ca, U, pr, k0, O, c4, ACC, C); });
         merge_into_c<TK, 1, ACC>(acc, 1.0f, U, pr, k0, O, c4, C, P, ca);
     }
 }
 
-template <int TK, bool ACC, bool MAPPED>
+// NTC: C read ahead with non-temporal loads (accumulating launches whose C and B exceed the
+// last-level cache, see load_c4); only the aligned variants take it.
+template <int TK, bool ACC, bool MAPPED, bool NTC>
 static void launch_tk_mode(const DeviceFormat& F, const void* dB, bool b_f16, bool b_tiled, int O,
                            float* dC, hipStream_t st) {
     constexpr int VEC = TK / 16;
@@ -897,11 +913,11 @@ static void launch_tk_mode(const DeviceFormat& F, const void* dB, bool b_f16, bo
         const int* rsc = F.rs_cols.p;
         const float* rsv = F.rs_vals.p;
         if (aligned)
-            hipLaunchKernelGGL((k_spmm_f32<TK, true, ACC, MAPPED>), grid, block, 0, st, U, rmap,
+            hipLaunchKernelGGL((k_spmm_f32<TK, true, ACC, MAPPED, NTC>), grid, block, 0, st, U, rmap,
                                NH, xs, eptr, cols, dense, ent, F.dense_a32.p, rsc, rsv, B, O, c4,
                                dC);
         else
-            hipLaunchKernelGGL((k_spmm_f32<TK, false, ACC, MAPPED>), grid, block, 0, st, U, rmap,
+            hipLaunchKernelGGL((k_spmm_f32<TK, false, ACC, MAPPED, false>), grid, block, 0, st, U, rmap,
                                NH, xs, eptr, cols, dense, ent, F.dense_a32.p, rsc, rsv, B, O, c4,
                                dC);
     } else if (b_f16) {
@@ -911,21 +927,21 @@ static void launch_tk_mode(const DeviceFormat& F, const void* dB, bool b_f16, bo
             throw Error(VCSRMC_ERR_STATE, "O-tile-major B needs full, aligned O tiles");
         const int tiled_n = b_tiled ? F.N : 0;
         if (aligned)
-            hipLaunchKernelGGL((k_spmm_f16<TK, _Float16, true, ACC, MAPPED>), grid, block, 0, st,
+            hipLaunchKernelGGL((k_spmm_f16<TK, _Float16, true, ACC, MAPPED, NTC>), grid, block, 0, st,
                                U, rmap, NH, xs, eptr, cols, dense, ent, F.dense_a16.p, B, O,
                                tiled_n, F.scale, c4, dC);
         else
-            hipLaunchKernelGGL((k_spmm_f16<TK, _Float16, false, ACC, MAPPED>), grid, block, 0, st,
+            hipLaunchKernelGGL((k_spmm_f16<TK, _Float16, false, ACC, MAPPED, false>), grid, block, 0, st,
                                U, rmap, NH, xs, eptr, cols, dense, ent, F.dense_a16.p, B, O, 0,
                                F.scale, c4, dC);
     } else if constexpr (TK <= 64) {
         const float* B = static_cast<const float*>(dB);
         if (aligned)
-            hipLaunchKernelGGL((k_spmm_f16<TK, float, true, ACC, MAPPED>), grid, block, 0, st, U,
+            hipLaunchKernelGGL((k_spmm_f16<TK, float, true, ACC, MAPPED, NTC>), grid, block, 0, st, U,
                                rmap, NH, xs, eptr, cols, dense, ent, F.dense_a16.p, B, O, 0,
                                F.scale, c4, dC);
         else
-            hipLaunchKernelGGL((k_spmm_f16<TK, float, false, ACC, MAPPED>), grid, block, 0, st, U,
+            hipLaunchKernelGGL((k_spmm_f16<TK, float, false, ACC, MAPPED, false>), grid, block, 0, st, U,
                                rmap, NH, xs, eptr, cols, dense, ent, F.dense_a16.p, B, O, 0,
                                F.scale, c4, dC);
     } else {
@@ -937,14 +953,17 @@ static void launch_tk_mode(const DeviceFormat& F, const void* dB, bool b_f16, bo
 
 template <int TK>
 static void launch_tk(const DeviceFormat& F, const void* dB, bool b_f16, bool b_tiled, int O,
-                      float* dC, bool accumulate, hipStream_t st) {
+                      float* dC, bool accumulate, bool nt_c, hipStream_t st) {
     const bool mapped = F.row_map.n > 0;
-    if (accumulate) {
-        if (mapped) launch_tk_mode<TK, true, true>(F, dB, b_f16, b_tiled, O, dC, st);
-        else launch_tk_mode<TK, true, false>(F, dB, b_f16, b_tiled, O, dC, st);
+    if (accumulate && nt_c) {
+        if (mapped) launch_tk_mode<TK, true, true, true>(F, dB, b_f16, b_tiled, O, dC, st);
+        else launch_tk_mode<TK, true, false, true>(F, dB, b_f16, b_tiled, O, dC, st);
+    } else if (accumulate) {
+        if (mapped) launch_tk_mode<TK, true, true, false>(F, dB, b_f16, b_tiled, O, dC, st);
+        else launch_tk_mode<TK, true, false, false>(F, dB, b_f16, b_tiled, O, dC, st);
     } else {
-        if (mapped) launch_tk_mode<TK, false, true>(F, dB, b_f16, b_tiled, O, dC, st);
-        else launch_tk_mode<TK, false, false>(F, dB, b_f16, b_tiled, O, dC, st);
+        if (mapped) launch_tk_mode<TK, false, true, false>(F, dB, b_f16, b_tiled, O, dC, st);
+        else launch_tk_mode<TK, false, false, false>(F, dB, b_f16, b_tiled, O, dC, st);
     }
 }
 
@@ -1101,6 +1120,10 @@ SpmmPlan plan_spmm(const DeviceFormat& F, const void* dB, bool b_f16, int O, int
     // half of 256-byte rows, which reach only half of an L2's sets (R-MAT scale 22, O tiles of
     // 64: 2.44 -> 2.29 ms; O tiles of 32: 4.78 -> 3.96 ms).  Same values either way.
     p.b_tiled = p.convert_to != nullptr && O > p.tk && O % p.tk == 0;
+    // C read non-temporally where C and B together exceed the 256 MB last-level cache (load_c4)
+    const long long c_bytes = (long long)F.M * O * 4;
+    const long long b_bytes = (long long)F.N * O * (p.b_f16 ? 2 : 4);
+    p.nt_c = accumulate && c_bytes + b_bytes > (256LL << 20);
     p.launch = true;
     return p;
 }
@@ -1122,10 +1145,10 @@ void run_spmm(const SpmmPlan& p, hipStream_t st) {
         VCSRMC_HIP(hipGetLastError());
     }
     switch (p.tk) {
-        case 16: launch_tk<16>(F, dB, p.b_f16, p.b_tiled, p.O, p.dC, p.accumulate, st); break;
-        case 32: launch_tk<32>(F, dB, p.b_f16, p.b_tiled, p.O, p.dC, p.accumulate, st); break;
-        case 64: launch_tk<64>(F, dB, p.b_f16, p.b_tiled, p.O, p.dC, p.accumulate, st); break;
-        default: launch_tk<128>(F, dB, p.b_f16, p.b_tiled, p.O, p.dC, p.accumulate, st); break;
+        case 16: launch_tk<16>(F, dB, p.b_f16, p.b_tiled, p.O, p.dC, p.accumulate, p.nt_c, st); break;
+        case 32: launch_tk<32>(F, dB, p.b_f16, p.b_tiled, p.O, p.dC, p.accumulate, p.nt_c, st); break;
+        case 64: launch_tk<64>(F, dB, p.b_f16, p.b_tiled, p.O, p.dC, p.accumulate, p.nt_c, st); break;
+        default: launch_tk<128>(F, dB, p.b_f16, p.b_tiled, p.O, p.dC, p.accumulate, p.nt_c, st); break;
     }
 }
 
