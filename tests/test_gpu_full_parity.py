@@ -109,3 +109,42 @@ def test_every_row_full_size(orc, config, variant):
                 r = err[rows] / (TAU[fp32] * bound[rows] + 1e-30)
                 print(f"  overwrite={overwrite} {name} rows: {rows.size}, worst error / bound "
                       f"{r.max():.3g}", flush=True)
+
+
+@pytest.mark.parametrize("fp32", [True, False])
+def test_nontemporal_c_reads_with_initial_c(orc, fp32):
+    """An accumulating launch whose C and B exceed 256 MB reads C with non-temporal loads:
+    uniform 240,000^2 (8 per row) at O = 200 (C 192 MB, B 192 / 96 MB), C starting from random
+    values, the last O tile partial (72 of 128 columns: the read path of unstaged tiles).  Every
+    row against the oracle with the norm that counts the initial C; rows without nonzeros keep
+    their values bit for bit."""
+    import torch
+    M = N = 240000
+    O = 200
+    rng = np.random.default_rng(44 + fp32)
+    k = rng.poisson(8, M)
+    k[rng.random(M) < 0.05] = 0
+    rp = np.zeros(M + 1, np.int32)
+    rp[1:] = np.cumsum(k)
+    col = np.concatenate([np.sort(rng.choice(N, size=int(x), replace=False)) for x in k
+                          if x]).astype(np.int32)
+    val = rng.uniform(-1, 1, col.size).astype(np.float32)
+    B = rng.uniform(-1, 1, (N, O)).astype(np.float32)
+    if not fp32:
+        B = B.astype(np.float16).astype(np.float32)
+    C0 = rng.uniform(-1, 1, (M, O)).astype(np.float32)
+    b_bytes = N * O * (4 if fp32 else 2)
+    assert M * O * 4 + b_bytes > 256 << 20
+    say("non-temporal C reads", fp32, M, col.size, O)
+    with vm.DeviceFormat.from_device_csr(dev(rp), dev(col), dev(val), M, N, fp32, 32) as f:
+        scale = f.info()["scale"]
+        dB = dev(B) if fp32 else dev(B).half()
+        C = dev(C0)
+        f.spmm(dB, C, tileK=128)
+        torch.cuda.synchronize()
+        Ch = C.cpu().numpy()
+    empty = k == 0
+    assert Ch[empty].tobytes() == C0[empty].tobytes()
+    err, bound = orc.spmm_check(rp, col, val, M, B, Ch, mode=0 if fp32 else 1, scale=scale, C0=C0)
+    ratio = err[~empty] / (TAU[fp32] * bound[~empty] + 1e-30)
+    assert np.all(ratio <= 1.0), f"worst {ratio.max():.3g}"
