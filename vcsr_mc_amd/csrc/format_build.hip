@@ -607,11 +607,12 @@ static void check_err(const int* d_err, hipStream_t st) {
 // Panels of at most this many tiles are light units (one wave each, four per work-group);
 // larger panels become heavy units that the four waves of a work-group share and merge in LDS.
 // With fewer than 2048 panels one wave per panel leaves most of the 1024 SIMDs idle, so every
-// multi-tile panel is shared by a work-group; otherwise panels of up to 6 tiles stay on one
-// wave (measured on gfx950: 6 to 12 tiles are equally good for stencil and R-MAT matrices, 6 is
-// 2% faster than 7 or 8 on the power-law matrix; 4 starves the stencil of waves and slows the
-// power-law one by 6%, 16 leaves R-MAT with long single-wave units).
-static int light_tile_limit(int num_panels) { return num_panels >= kFewPanels ? 6 : 1; }
+// multi-tile panel is shared by a work-group; otherwise panels of up to 5 tiles stay on one
+// wave (measured on gfx950: 5 to 12 tiles are equally good for the uniform, stencil, 32 x 32
+// block and R-MAT matrices, within 0.5%; on the 36,692-row power-law matrix 5 is 2% faster
+// than 6, 7 or 8 accumulating and 4% faster overwriting, and 4 is 7% slower accumulating; 16
+// leaves R-MAT with long single-wave units).
+static int light_tile_limit(int num_panels) { return num_panels >= kFewPanels ? 5 : 1; }
 
 // Largest heavy unit.  Heavy units run first, larger first, each on the four waves of one
 // work-group, while the GPU holds about 3072 waves (1024 SIMDs, three waves each); a unit of
