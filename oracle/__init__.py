@@ -74,7 +74,8 @@ def lib():
         L.orc_spmm_format.argtypes = [C.POINTER(OrcFormat), f32p, C.c_int, f64p]
         L.orc_spmm_check.restype = C.c_int
         L.orc_spmm_check.argtypes = [i32p, i32p, f32p, C.c_int, f32p, C.c_longlong, C.c_int,
-                                     C.c_int, C.c_float, f32p, f32p, C.c_int, f64p, f64p]
+                                     C.c_int, C.c_float, f32p, f32p, C.c_int, f64p, f64p, f64p, f64p,
+                                     f64p]
         L.orc_cpu_spmm_f64.argtypes = [i32p, i32p, f32p, C.c_int, f32p, C.c_int, f64p]
         L.orc_cpu_spmm_f64_rows.argtypes = [i32p, i32p, f32p, C.c_int, C.c_int, f32p, C.c_int, f64p]
         L.orc_cpu_spmm_f64_omp.argtypes = [i32p, i32p, f32p, C.c_int, C.c_int, f32p, C.c_int, f64p,
@@ -231,11 +232,15 @@ def spmm_csr(row_ptr, col, val, M, B, mode=0, scale=1.0):
     return R, L1
 
 
-def spmm_check(row_ptr, col, val, M, B, prod, mode=0, scale=1.0, C0=None, threads=None):
+def spmm_check(row_ptr, col, val, M, B, prod, mode=0, scale=1.0, C0=None, threads=None,
+               norms=False):
     """The parity norm's terms for every row of a product `prod` (C, M x O float32): returns (err,
     bound) with err[r] = ||C[r] - (R[r] + C0[r])||_1 and bound[r] = rowL1[r] + ||C0[r]||_1,
     R and rowL1 those of spmm_csr (same arithmetic), computed row by row on `threads` threads
-    (default: up to 16) without holding R."""
+    (default: up to 16) without holding R.  norms=True returns (err, bound, ref_l1, sq_err,
+    sq_ref) with, per row and C_ref = R + C0, ref_l1 = ||C_ref[r]||_1 (the stricter norm),
+    sq_err = ||C[r] - C_ref[r]||_2^2 and sq_ref = ||C_ref[r]||_2^2: sqrt(sum sq_err) /
+    sqrt(sum sq_ref) is the reference driver's relative L2 error (main.cpp:262-275)."""
     rp, ci, vv, Bf = _i32(row_ptr), _i32(col), _f32(val), _f32(B)
     if ci.size == 0:
         ci = np.zeros(1, np.int32); vv = np.zeros(1, np.float32)
@@ -250,14 +255,16 @@ def spmm_check(row_ptr, col, val, M, B, prod, mode=0, scale=1.0, C0=None, thread
         threads = max(1, min(16, os.cpu_count() or 1))
     err = np.empty(M, np.float64)
     bound = np.empty(M, np.float64)
+    extra = [np.empty(M, np.float64) for _ in range(3)] if norms else []
     rc = lib().orc_spmm_check(_p(rp, C.c_int), _p(ci, C.c_int), _p(vv, C.c_float), M,
                               _p(Bf, C.c_float), Bf.size, O, mode, float(scale),
                               _p(Cf, C.c_float),
                               None if C0f is None else _p(C0f, C.c_float), threads,
-                              _p(err, C.c_double), _p(bound, C.c_double))
+                              _p(err, C.c_double), _p(bound, C.c_double),
+                              *([_p(x, C.c_double) for x in extra] if norms else [None] * 3))
     if rc != 0:
         raise OracleError(f"orc_spmm_check failed with status {rc}")
-    return err, bound
+    return (err, bound, *extra) if norms else (err, bound)
 
 
 def spmm_format(fm: Format, B) -> np.ndarray:

@@ -430,7 +430,8 @@ void orc_spmm_csr(const int *row_ptr, const int *col, const float *val, int M, c
 
 int orc_spmm_check(const int *row_ptr, const int *col, const float *val, int M, const float *B,
                    long long nb, int O, int mode, float scale, const float *C, const float *C0,
-                   int threads, double *err, double *bound) {
+                   int threads, double *err, double *bound, double *ref_l1, double *sq_err,
+                   double *sq_ref) {
     const float inv = 1.0f / scale;
     float *Bq = NULL;
     if (mode != 0) {
@@ -454,17 +455,24 @@ int orc_spmm_check(const int *row_ptr, const int *col, const float *val, int M, 
             spmm_row(row_ptr, col, val, r, B, Bq, O, mode, inv, scale, out, &l1);
             const float *c = C + (size_t)r * O;
             const float *c0 = C0 ? C0 + (size_t)r * O : NULL;
-            double e = 0.0, n0 = 0.0;
+            double e = 0.0, n0 = 0.0, rl1 = 0.0, se = 0.0, sr = 0.0;
             for (int k = 0; k < O; ++k) {
                 double want = out[k];
                 if (c0) {
                     want += (double)c0[k];
                     n0 += fabs((double)c0[k]);
                 }
-                e += fabs((double)c[k] - want);
+                const double d = (double)c[k] - want;
+                e += fabs(d);
+                rl1 += fabs(want);
+                se += d * d;
+                sr += want * want;
             }
             err[r] = e;
             bound[r] = l1 + n0;
+            if (ref_l1) ref_l1[r] = rl1;
+            if (sq_err) sq_err[r] = se;
+            if (sq_ref) sq_ref[r] = sr;
         }
         free(out);
     }

@@ -35,9 +35,10 @@
  *     seg_base + lcol = col, depth = max count, items partition the groups).
  *   - orc_spmm_csr: a dense numpy matmul in float64 of the same quantised inputs.
  *   - orc_spmm_format: equals orc_spmm_csr on the same matrix.
- *   - orc_spmm_check: its err and bound equal |C - R| and rowL1 of orc_spmm_csr, bit for bit,
- *     in both modes, with and without C0, at 1 and several threads; a planted error in one
- *     element of C shows up in that row only.
+ *   - orc_spmm_check: its err, bound, ref_l1, sq_err and sq_ref equal |C - R|, rowL1, |R|,
+ *     (C - R)^2 and R^2 summed in index order from orc_spmm_csr's R, bit for bit, in both modes,
+ *     with and without C0, at 1 and several threads; a planted error in one element of C shows
+ *     up in that row only.
  */
 #ifndef VCSRMC_ORACLE_H
 #define VCSRMC_ORACLE_H
@@ -84,12 +85,15 @@ void orc_spmm_format(const orc_format *f, const float *B, int O, double *R);
 /* The parity check of a whole product, rows split over `threads` OpenMP threads, without an
  * M x O result buffer: for every row r, the row of orc_spmm_csr (same arithmetic, so the same
  * doubles), then err[r] = sum_k |C[r,k] - (R[r,k] + C0[r,k])| and bound[r] = rowL1[r] +
- * sum_k |C0[r,k]| (C0 = C's values before a C += A.B launch; NULL = zero).  nb = the number of
- * B elements (mode 1 rounds B to binary16 once, in a buffer of that size).  Returns ORC_OK or
- * ORC_NOMEM. */
+ * sum_k |C0[r,k]| (C0 = C's values before a C += A.B launch; NULL = zero).  Optional (NULL = not
+ * wanted), with want = R + C0: ref_l1[r] = sum_k |want[r,k]| (the stricter norm ||C_ref[r,:]||_1),
+ * sq_err[r] = sum_k (C[r,k] - want[r,k])^2 and sq_ref[r] = sum_k want[r,k]^2, whose totals give
+ * the reference driver's relative L2 error (src/main.cpp:262-275).  nb = the number of B elements
+ * (mode 1 rounds B to binary16 once, in a buffer of that size).  Returns ORC_OK or ORC_NOMEM. */
 int orc_spmm_check(const int *row_ptr, const int *col, const float *val, int M, const float *B,
                    long long nb, int O, int mode, float scale, const float *C, const float *C0,
-                   int threads, double *err, double *bound);
+                   int threads, double *err, double *bound, double *ref_l1, double *sq_err,
+                   double *sq_ref);
 
 /* The reference's CPU SpMM exactly as the driver runs it (main.cpp:202-207): plain FP32
  * inputs, double accumulation, r -> p -> k.  R must be zeroed by the caller (+=). */

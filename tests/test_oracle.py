@@ -261,8 +261,9 @@ def test_cpu_baseline_loop_matches_dense(orc, rng):
 @pytest.mark.parametrize("with_c0", [False, True])
 def test_spmm_check_equals_spmm_csr(orc, rng, mode, with_c0):
     """The whole-matrix check gives, per row, exactly |C - (R + C0)|_1 and rowL1 + |C0|_1 of
-    spmm_csr (the same arithmetic, row by row), at one and at several threads; a planted error
-    in one element of C moves that row's error and no other."""
+    spmm_csr (the same arithmetic, row by row), and with norms=True |R + C0|_1, |C - (R + C0)|_2^2
+    and |R + C0|_2^2, at one and at several threads; a planted error in one element of C moves
+    that row's error and no other."""
     rp, c, v = random_csr(rng, 300, 200, density=0.05, empty_frac=0.2, mag=1e5 if mode else 1)
     B = rng.uniform(-2, 2, (200, 19)).astype(np.float32)  # not binary16-exact: mode 1 rounds it
     s = float(orc.half_scale(v)) if mode else 1.0
@@ -274,11 +275,18 @@ def test_spmm_check_equals_spmm_csr(orc, rng, mode, with_c0):
     err_want = np.cumsum(np.abs(C.astype(np.float64) - want), axis=1)[:, -1]
     bound_want = L1 + (np.cumsum(np.abs(C0.astype(np.float64)), axis=1)[:, -1] if with_c0
                        else 0.0)
+    d = C.astype(np.float64) - want
+    norms_want = [np.cumsum(x, axis=1)[:, -1] for x in (np.abs(want), d * d, want * want)]
     for threads in (1, 5):
         err, bound = orc.spmm_check(rp, c, v, 300, B, C, mode=mode, scale=s, C0=C0,
                                     threads=threads)
         assert err.tobytes() == err_want.tobytes()
         assert bound.tobytes() == bound_want.tobytes()
+        out = orc.spmm_check(rp, c, v, 300, B, C, mode=mode, scale=s, C0=C0, threads=threads,
+                             norms=True)
+        assert len(out) == 5
+        for got, ref in zip(out, [err_want, bound_want] + norms_want):
+            assert got.tobytes() == ref.tobytes()
     C2 = C.copy()
     C2[17, 3] += 0.5
     err2, _ = orc.spmm_check(rp, c, v, 300, B, C2, mode=mode, scale=s, C0=C0, threads=3)
