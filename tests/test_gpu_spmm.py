@@ -138,7 +138,8 @@ def test_converted_b_o_tile_major(orc, O, tileK):
 @pytest.mark.parametrize("overwrite", [False, True])
 def test_launcher_equals_spmm(overwrite):
     """The pre-bound launcher (checks and argument conversion once) enqueues the same launch as
-    spmm: the same C bit for bit over repeated calls, and a bad tileK is reported when called."""
+    spmm: the same C bit for bit over repeated calls; a bad tileK is reported when called, and a
+    call after the format is closed raises instead of passing the freed handle on."""
     import torch
     rng = np.random.default_rng(21)
     rp, c, v = random_csr(rng, 3000, 2500, density=0.01)
@@ -156,6 +157,8 @@ def test_launcher_equals_spmm(overwrite):
         bad = f.launcher(B, C2, tileK=48)
         with pytest.raises(vm.VCSRMCError):
             bad()
+    with pytest.raises(vm.VCSRMCError, match="closed"):
+        go()
 
 
 def test_scaled_values(orc):

@@ -385,20 +385,23 @@ class DeviceFormat:
     def launcher(self, B, C_out, tileK=128, O=None, stream=None, overwrite=False):
         """A callable with no arguments that enqueues spmm(B, C_out, ...) asynchronously, with
         the checks and the ctypes conversions done once here: for loops of launches whose
-        kernels are shorter than the checks (a 6 us multiply).  It holds B and C_out."""
+        kernels are shorter than the checks (a 6 us multiply).  It holds this format, B and
+        C_out; once the format is closed, calling it raises ERR_STATE."""
         b_dtype, O = self._operands(B, C_out, O)
         fn = lib().vcsrmc_spmm_ex
-        args = (self.handle, C.c_void_p(_ptr(B)), C.c_int(b_dtype), C.c_int(O),
+        h = self.handle
+        args = (h, C.c_void_p(_ptr(B)), C.c_int(b_dtype), C.c_int(O),
                 C.c_int(int(tileK)), C.c_void_p(_ptr(C_out)),
                 C.c_int(SPMM_OVERWRITE if overwrite else 0), C.c_void_p(_stream_ptr(stream)),
                 None)
-        keep = (B, C_out)
+        keep = (self, B, C_out)
 
         def launch():
+            if keep[0]._h is not h:
+                raise VCSRMCError(ERR_STATE, "format closed")
             rc = fn(*args)
             if rc != 0:
                 _check(rc, "vcsrmc_spmm")
-            return keep is not None
 
         return launch
 
