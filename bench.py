@@ -17,9 +17,10 @@ the same GPU in the same run, the row-sample parity check, and the reference's C
 Every timed region (K launches after W warm-ups) is preceded by about 30 ms of untimed
 launches, so that it measures the GPU's steady state rather than the power transient that
 follows an idle period; the launch count is `settle_launches`.  The K timed launches are
-captured into one HIP graph after the warm-ups and replayed once between the synchronisations
-(`--eager` enqueues them one by one instead): the smallest workload's kernel is shorter than the
-host's enqueue of a launch.  The reference protocol's single
+captured into one HIP graph after the warm-ups, replayed once untimed (a new graph's first
+replay is slower per kernel), then once between the synchronisations (`--eager` enqueues them
+one by one instead): the smallest workload's kernel is shorter than the host's enqueue of a
+launch.  The reference protocol's single
 launches (median of 10 after 3 warm-ups) are taken as the reference takes them.
 
 Prints one JSON line; its last keys, and the last lines of stderr, summarise every workload.
@@ -137,14 +138,19 @@ def timed_steps(run, steps, warmup, stream, capture=None):
     captured into one HIP graph after the warm-ups and the timed region replays it once: the
     same K launches, without the host enqueueing each (the smallest workload's 5 us kernel is
     shorter than one enqueue: 4-6 us per launch through the API, ~14 us in a cold loop's first
-    iterations; a graph of 20 launches runs them at 5.5 us each).  Returns (wall ms per step,
-    event ms per step, settling launches)."""
+    iterations; a graph of 20 launches runs them at 5.5 us each).  The graph is replayed once
+    untimed before that: a freshly captured graph's first replay runs each of its kernels
+    ~0.75 us slower (uniform 4096^2: 6.1 against 5.35 us per launch, 20 launches), a one-time
+    cost of the graph, not of the launches.  Returns (wall ms per step, event ms per step,
+    settling launches)."""
     import torch
     settled = settle(run, stream)
     for _ in range(warmup):
         run()
     torch.cuda.synchronize()
     timed = capture(steps) if capture is not None else None
+    if timed is not None:
+        timed()  # the graph's first replay, untimed
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
@@ -447,7 +453,8 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "settle_ms_before_warmup": SETTLE_MS,
-        "timed_launches": "enqueued one by one" if args.eager else "one HIP graph of K launches",
+        "timed_launches": ("enqueued one by one" if args.eager else
+                           "one HIP graph of K launches, its first replay untimed"),
         "ms_per_step": h["ms_per_step"],
         "higher_is_better": True,
         "scaling": "weak",
