@@ -184,3 +184,39 @@ def test_nontemporal_c_reads_with_initial_c(orc, fp32):
     err, bound = orc.spmm_check(rp, col, val, M, B, Ch, mode=0 if fp32 else 1, scale=scale, C0=C0)
     ratio = err[~empty] / (TAU[fp32] * bound[~empty] + 1e-30)
     assert np.all(ratio <= 1.0), f"worst {ratio.max():.3g}"
+
+
+# (workload, O, kernel precision, B dtype): widths whose B and C rows are not 16-byte aligned
+# (except 72 FP16: 144-byte rows, a partial O tile), so the kernels take their element-wise
+# load paths, at the workloads' full sizes.
+ODD_WIDTHS = [(2, 100, "fp16", "fp16"), (2, 100, "fp32", "fp32"), (3, 36, "fp32", "fp32"),
+              (4, 68, "fp16", "fp16"), (4, 72, "fp16", "fp16"), (5, 33, "fp16", "fp32")]
+
+
+@pytest.mark.parametrize("config,O,prec,b_dtype", ODD_WIDTHS)
+def test_odd_widths_full_size(orc, config, O, prec, b_dtype):
+    """A full-size workload at a width whose rows are not 16-byte aligned, C += A.B onto a
+    random initial C: every row against the oracle with the norm that counts the initial C,
+    rows without nonzeros keeping C bit for bit."""
+    import torch
+    fp32 = prec == "fp32"
+    A = workload(config)
+    B = vm.dense(A.N, O, seed=vm.SEED_BASE + 300 + config, fp16_exact=b_dtype == "fp16")
+    C0 = np.random.default_rng(1000 * config + O).uniform(-1, 1, (A.M, O)).astype(np.float32)
+    nonempty = np.diff(A.row_ptr) > 0
+    say("odd width", config, O, prec, b_dtype, A.M, A.nnz)
+    with vm.DeviceFormat.from_device_csr(dev(A.row_ptr), dev(A.col), dev(A.val), A.M, A.N,
+                                         fp32, 32) as f:
+        scale = f.info()["scale"]
+        dB = dev(B).half() if b_dtype == "fp16" else dev(B)
+        C = dev(C0)
+        f.spmm(dB, C, tileK=128)
+        torch.cuda.synchronize()
+        Ch = C.cpu().numpy()
+        del C, dB
+    assert Ch[~nonempty].tobytes() == C0[~nonempty].tobytes()
+    err, bound = orc.spmm_check(A.row_ptr, A.col, A.val, A.M, B, Ch, mode=0 if fp32 else 1,
+                                scale=scale, C0=C0)
+    ratio = err[nonempty] / (TAU[fp32] * bound[nonempty] + 1e-30)
+    print(f"  worst error / bound {ratio.max():.3g}", flush=True)
+    assert np.all(ratio <= 1.0), f"{int(np.count_nonzero(ratio > 1))} rows over, worst {ratio.max():.3g}"
