@@ -53,10 +53,13 @@ def test_random_bit_exact(orc, seed):
 
 @pytest.mark.parametrize("config,size,segw", [(1, 0, 32), (2, 0, 32), (3, 0, 32), (4, 0, 32),
                                               (5, 0, 32), (3, 20, 32), (4, 64, 32), (5, 12, 32),
-                                              (5, 16, 16)])
+                                              (5, 16, 16), (1, 0, 48), (2, 0, 16), (2, 0, 64),
+                                              (3, 0, 16), (4, 0, 16), (4, 0, 64), (5, 0, 48)])
 def test_workloads_bit_exact(orc, config, size, segw):
-    """Every workload at its full benchmark size (and reduced sizes, one at segw 16): the
-    format arrays of the GPU pipeline equal the oracle's (src/vcsr_mc.cu:25-123) bit for bit."""
+    """Every workload at its full benchmark size (and reduced sizes), at segw 32 and at the
+    other segment widths the reference takes (16, 48, 64; 48 does not divide N, so the last
+    segment is partial): the format arrays of the GPU pipeline equal the oracle's
+    (src/vcsr_mc.cu:25-123) bit for bit."""
     A = vm.generate(config, size)
     fp32 = vm.WORKLOADS[config]["precision"] == "fp32"
     say("workload", config, size, A.M, A.nnz)
