@@ -71,8 +71,11 @@ def test_rcm_random_gpu(orc):
         assert np.array_equal(pos, orc.rcm_order(rp, col, M, N)), t
 
 
-@pytest.mark.parametrize("config,size", [(1, 2048), (2, 0), (3, 40), (4, 512), (5, 14)])
+@pytest.mark.parametrize("config,size", [(1, 2048), (2, 0), (3, 40), (4, 512), (5, 14),
+                                         (1, 0), (3, 0), (4, 0), (5, 0)])
 def test_rcm_workloads_gpu(orc, config, size):
+    """Column positions and the permuted CSR and B equal the oracle's element for element, on
+    reduced workloads and on all five at their full benchmark sizes."""
     A = vm.generate(config, size)
     say("rcm workload", config, size, A.M, A.N, A.nnz)
     pos = gpu_rcm(A.row_ptr, A.col, A.M, A.N)
