@@ -68,3 +68,27 @@ def test_reference_driver_other_shapes(mtx, segw, tileK, O):
                 "--check", "cpu", "--csv"])
     for name in ("vcsr_mc", "vcsr_mc_fp32"):
         assert rows[name][11] == "pass", rows[name]
+
+
+DRIVER = os.path.join(ROOT, "vcsr_mc_amd", "spmm_vcsr")
+
+
+@pytest.mark.parametrize("config,O,check", [(1, 128, "cpu"), (2, 128, "cpu"),
+                                            (3, 128, "rocsparse"), (4, 256, "rocsparse")])
+def test_reference_driver_full_workloads(tmp_path, config, O, check):
+    """The reference's driver validates both of this library's kernels on full benchmark
+    workloads: the Matrix Market file spmm_vcsr --gen K --write-mtx writes, read by the
+    reference's own reader, checked against its CPU loop or hipSPARSE."""
+    if not os.path.exists(DROPIN):
+        pytest.skip("oracle/_ref/spmm_vcsr_dropin not built (needs the reference sources)")
+    path = str(tmp_path / f"workload{config}.mtx")
+    say("write workload", config)
+    subprocess.run([DRIVER, "--gen", str(config), "--write-mtx", path], check=True, timeout=600,
+                   capture_output=True)
+    rows = run(["--mtx", path, "--O", str(O), "--segw", "32", "--tileK", "128", "--repeat", "2",
+                "--warmup", "1", "--algo", "vcsr_mc,vcsr_mc_fp32", "--check", check,
+                "--bdist", "uniform", "--csv"])
+    os.remove(path)
+    for name in ("vcsr_mc", "vcsr_mc_fp32"):
+        assert rows[name][11] == "pass", rows[name]
+        print(f"  {name}: rel_l2 {rows[name][12]}", flush=True)
